@@ -1,0 +1,289 @@
+"""Benchmark of the HiF8 fake-quant linear path on one MI355X.
+
+Workload (Wan-14B 720P): one HIF8Linear forward of the FFN-up
+projection, x [75600, 5120] bf16 (N(0,1), 16 outlier channels x20) against
+W [13824, 5120] held as packed 8-bit HiF8 codes (N(0,0.02), prepacked once,
+outside the timed region).  A step = amax+scale of x, fake-quant of x, fused
+dequant-GEMM + bias -> y [75600, 13824] bf16: the reference's
+_HIF8LinearFunction.forward (ospnext/modules/hif8_linear.py:68-86).
+
+value = 2*M*N*K / step time (TFLOP/s).  The per-kernel times come from HIP
+events on the stream the kernels run on (torch's current stream).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--a-format bf16|codes]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+METRIC = "HiF8 linear TFLOP/s + encode GB/s (14B 720P shapes), 1 GPU, % of roofline"
+PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
+PEAK_HBM_GBPS = 8000.0      # MI355X HBM3E
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def make_inputs(torch, M, K, N, seed=0, dev="cuda:0"):
+    g = torch.Generator(device=dev).manual_seed(seed)
+    x = torch.randn(M, K, generator=g, device=dev, dtype=torch.float32)
+    ch = torch.randperm(K, generator=g, device=dev)[:16]
+    x[:, ch] *= 20
+    x = x.to(torch.bfloat16)
+    w = (torch.randn(N, K, generator=g, device=dev, dtype=torch.float32) * 0.02).to(torch.bfloat16)
+    b = torch.zeros(N, dtype=torch.bfloat16, device=dev)
+    return x, w, b
+
+
+def time_linear(pkg, torch, x, packed, b, steps, warmup, a_format):
+    """Times steps of [amax+scale, quantise, fused GEMM]; returns per-phase ms lists."""
+    st = pkg.QuantState(x.device)
+    L = pkg._lib.load()
+    stream = pkg._lib.stream_ptr(x.device)
+    M, K = x.shape
+    N = packed.shape[0]
+    y = torch.empty(M, N, dtype=torch.bfloat16, device=x.device)
+    use_codes = a_format == "codes"
+    a = torch.empty((M, K), dtype=torch.uint8 if use_codes else torch.bfloat16, device=x.device)
+    fmt = pkg._lib.A_CODES if use_codes else pkg._lib.A_BF16
+
+    def step():
+        pkg._lib.check(L.hif8_absmax_scale(x.data_ptr(), 0, x.numel(), 15.0, st.ptr, stream), "amax")
+        if use_codes:
+            pkg._lib.check(L.hif8_encode(x.data_ptr(), 0, x.numel(), st.ptr, a.data_ptr(), stream), "encode")
+        else:
+            pkg._lib.check(L.hif8_fake_quant(x.data_ptr(), 0, x.numel(), st.ptr, a.data_ptr(), 0, stream), "qdq")
+        pkg._lib.check(L.hif8_linear_fwd(a.data_ptr(), fmt, st.ptr, packed.codes.data_ptr(), packed.state.ptr,
+                                         b.data_ptr(), y.data_ptr(), M, N, K, stream), "linear")
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        e = ev[i]
+        e[0].record()
+        pkg._lib.check(L.hif8_absmax_scale(x.data_ptr(), 0, x.numel(), 15.0, st.ptr, stream), "amax")
+        e[1].record()
+        if use_codes:
+            pkg._lib.check(L.hif8_encode(x.data_ptr(), 0, x.numel(), st.ptr, a.data_ptr(), stream), "encode")
+        else:
+            pkg._lib.check(L.hif8_fake_quant(x.data_ptr(), 0, x.numel(), st.ptr, a.data_ptr(), 0, stream), "qdq")
+        e[2].record()
+        pkg._lib.check(L.hif8_linear_fwd(a.data_ptr(), fmt, st.ptr, packed.codes.data_ptr(), packed.state.ptr,
+                                         b.data_ptr(), y.data_ptr(), M, N, K, stream), "linear")
+        e[3].record()
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) * 1e3
+    amax = [e[0].elapsed_time(e[1]) for e in ev]
+    quant = [e[1].elapsed_time(e[2]) for e in ev]
+    gemm = [e[2].elapsed_time(e[3]) for e in ev]
+    return {"wall_ms": wall, "amax": amax, "quant": quant, "gemm": gemm, "y": y}
+
+
+def median(v):
+    s = sorted(v)
+    return s[len(s) // 2]
+
+
+def cpu_baseline(torch, M, K, N, sample_rows=1024):
+    """The reference CPU path (torch ops: _quant + quant_hif8 + F.linear in bf16) on a
+    row slice; the per-call weight quantisation is timed once and the activation
+    part scaled linearly in M."""
+    sys.path.insert(0, ROOT)
+    from oracle import hif8_ref as R
+
+    threads = min(os.cpu_count() or 1, 16)
+    torch.set_num_threads(threads)
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(sample_rows, K, generator=g)
+    x[:, torch.randperm(K, generator=g)[:16]] *= 20
+    x = x.to(torch.bfloat16)
+    w = (torch.randn(N, K, generator=g) * 0.02).to(torch.bfloat16)
+    import torch.nn.functional as F
+    R.quant_torch_cpu(x[:64], 15.0)  # warm
+    t0 = time.perf_counter()
+    wq, _ = R.quant_torch_cpu(w, 15.0)
+    t_w = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    xq, _ = R.quant_torch_cpu(x, 15.0)
+    t_x = time.perf_counter() - t0
+    F.linear(xq[:64], wq)  # warm
+    t0 = time.perf_counter()
+    F.linear(xq, wq)
+    t_g = time.perf_counter() - t0
+    t_full = t_w + (M / sample_rows) * (t_x + t_g)
+    value = 2.0 * M * N * K / t_full / 1e12
+    return {
+        "value": round(value, 4), "unit": "TFLOP/s", "cores": threads, "kind": "port",
+        "sample": (f"reference CPU path (torch ops, bf16 F.linear) on x[{sample_rows},{K}] x W[{N},{K}]: "
+                   f"W qdq {t_w:.2f}s, x qdq {t_x:.3f}s, GEMM {t_g:.3f}s; full-M time extrapolated "
+                   f"linearly to M={M}: {t_full:.1f}s"),
+        "cpu_model": platform.processor() or platform.machine(),
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--a-format", default="bf16", choices=["bf16", "codes"])
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--shapes", default="up", help="comma list of up,down,qkvo to time in addition")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py: this build targets one GPU (no collectives); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    sys.path.insert(0, ROOT)
+    from __graft_entry__ import load_package
+    pkg = load_package()
+    pkg._lib.load()
+    dev = torch.device("cuda:0")
+    M, K, N = 75600, 5120, 13824
+
+    log(f"[bench] inputs M={M} K={K} N={N}")
+    x, w, b = make_inputs(torch, M, K, N)
+    packed = pkg.PackedWeight(w, 15.0)
+    torch.cuda.synchronize()
+    log("[bench] timing FFN-up step")
+    r = time_linear(pkg, torch, x, packed, b, args.steps, args.warmup, args.a_format)
+    step_ms = [a + q + g for a, q, g in zip(r["amax"], r["quant"], r["gemm"])]
+    ms_step = r["wall_ms"] / args.steps
+    flops = 2.0 * M * N * K
+    value = flops / (ms_step * 1e-3) / 1e12
+    gemm_ms = sum(r["gemm"]) / len(r["gemm"])
+    amax_ms = sum(r["amax"]) / len(r["amax"])
+    quant_ms = sum(r["quant"]) / len(r["quant"])
+    gemm_tflops = flops / (gemm_ms * 1e-3) / 1e12
+    n = M * K
+    enc_bytes = 5 * n if args.a_format == "codes" else 6 * n   # amax read + quantise read/write
+    enc_gbps = enc_bytes / ((amax_ms + quant_ms) * 1e-3) / 1e9
+
+    # encode (codes) throughput, the bandwidth headline: amax + encode of x
+    st = pkg.QuantState(dev)
+    codes = torch.empty((M, K), dtype=torch.uint8, device=dev)
+    L = pkg._lib.load()
+    stream = pkg._lib.stream_ptr(dev)
+    for _ in range(2):
+        L.hif8_absmax_scale(x.data_ptr(), 0, n, 15.0, st.ptr, stream)
+        L.hif8_encode(x.data_ptr(), 0, n, st.ptr, codes.data_ptr(), stream)
+    torch.cuda.synchronize()
+    e0, e1, e2 = (torch.cuda.Event(enable_timing=True) for _ in range(3))
+    ta, te = [], []
+    for _ in range(args.steps):
+        e0.record()
+        pkg._lib.check(L.hif8_absmax_scale(x.data_ptr(), 0, n, 15.0, st.ptr, stream), "amax")
+        e1.record()
+        pkg._lib.check(L.hif8_encode(x.data_ptr(), 0, n, st.ptr, codes.data_ptr(), stream), "encode")
+        e2.record()
+        torch.cuda.synchronize()
+        ta.append(e0.elapsed_time(e1))
+        te.append(e1.elapsed_time(e2))
+    enc_ms = sum(ta) / len(ta) + sum(te) / len(te)
+    encode = {
+        "workload": f"amax+scale+encode of x[{M},{K}] bf16 -> uint8 codes",
+        "bytes_algorithmic": 5 * n, "ms": round(enc_ms, 4),
+        "achieved_GBps": round(5 * n / (enc_ms * 1e-3) / 1e9, 1),
+        "amax_ms": round(sum(ta) / len(ta), 4), "encode_ms": round(sum(te) / len(te), 4),
+        "amax_GBps": round(2 * n / (sum(ta) / len(ta) * 1e-3) / 1e9, 1),
+        "encode_kernel_GBps": round(3 * n / (sum(te) / len(te) * 1e-3) / 1e9, 1),
+        "peak_GBps": PEAK_HBM_GBPS,
+    }
+    encode["frac"] = round(encode["achieved_GBps"] / PEAK_HBM_GBPS, 4)
+    del codes
+
+    extra_shapes = {}
+    for name in [s for s in args.shapes.split(",") if s and s != "up"]:
+        n_, k_ = {"down": (5120, 13824), "qkvo": (5120, 5120)}[name]
+        xs, ws, bs = make_inputs(torch, M, k_, n_, seed=1)
+        ps = pkg.PackedWeight(ws, 15.0)
+        rr = time_linear(pkg, torch, xs, ps, bs, max(3, args.steps // 2), 2, args.a_format)
+        gm = sum(rr["gemm"]) / len(rr["gemm"])
+        extra_shapes[name] = {"M": M, "N": n_, "K": k_, "gemm_ms": round(gm, 4),
+                              "gemm_TFLOPs": round(2.0 * M * n_ * k_ / (gm * 1e-3) / 1e12, 1),
+                              "step_ms": round(rr["wall_ms"] / max(3, args.steps // 2), 4)}
+        del xs, ws, bs, ps, rr
+
+    # the vendor bf16 GEMM on the same shape, for context (not part of the product)
+    vendor = None
+    try:
+        xq = pkg.fake_quant(x, pkg.absmax_scale(x, 15.0, pkg.QuantState(dev)))
+        wq = packed.dequantize()
+        for _ in range(2):
+            torch.nn.functional.linear(xq, wq, b)
+        torch.cuda.synchronize()
+        ea, eb = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        ea.record()
+        for _ in range(5):
+            torch.nn.functional.linear(xq, wq, b)
+        eb.record()
+        torch.cuda.synchronize()
+        vms = ea.elapsed_time(eb) / 5
+        vendor = {"what": "torch F.linear (hipBLASLt) bf16 on the dequantised operands", "ms": round(vms, 4),
+                  "TFLOPs": round(flops / (vms * 1e-3) / 1e12, 1)}
+        del xq, wq
+    except Exception as ex:  # informative only
+        vendor = {"error": str(ex)}
+
+    cpu = None
+    if not args.no_cpu:
+        log("[bench] CPU baseline")
+        try:
+            cpu = cpu_baseline(torch, M, K, N)
+        except Exception as ex:
+            cpu = {"error": str(ex)}
+
+    out = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": ("Wan-14B 720P FFN-up HIF8Linear forward: x[75600,5120] bf16 -> amax+scale -> "
+                         f"{'encode' if args.a_format == 'codes' else 'fake-quant'} -> fused HiF8 dequant-GEMM "
+                         "(W[13824,5120] packed 8-bit HiF8, bias) -> y bf16"),
+            "M": M, "K": K, "N": N, "a_format": args.a_format, "scale_max": 15.0,
+        },
+        "roofline": {
+            "kernel": "k_linear (fused HiF8 dequant-GEMM)",
+            "bound": "mfma",
+            "achieved": round(gemm_tflops, 2),
+            "peak": PEAK_BF16_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(gemm_tflops / PEAK_BF16_TFLOPS, 4),
+            "traffic": None,
+            "gemm_ms": round(gemm_ms, 4),
+        },
+        "phases_ms": {"amax": round(amax_ms, 4), "quant": round(quant_ms, 4), "gemm": round(gemm_ms, 4),
+                      "events_sum": round(median(step_ms), 4)},
+        "act_quant_GBps": round(enc_gbps, 1),
+        "encode": encode,
+        "shapes": extra_shapes,
+        "vendor_bf16_gemm": vendor,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

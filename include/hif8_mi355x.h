@@ -1,0 +1,130 @@
+/*
+ * hif8_mi355x.h -- C ABI of the MI355X (gfx950) HiF8 fake-quant linear library.
+ *
+ * Drop-in boundary for OSP-Next's per-tensor HiF8 quantized linear path.  Every
+ * entry point names the reference interface it replaces (paths relative to the
+ * OSP-Next tree).
+ *
+ * Conventions
+ *   - Every function returns an int status: HIF8_OK (0) or a negative HIF8_ERR_*.
+ *     hif8_strerror() turns it into text; a HIP launch failure is HIF8_ERR_HIP.
+ *   - All pointers are device pointers the caller owns (no allocation inside any
+ *     entry point), already offset to the first element.  Element counts are
+ *     int64_t.  bf16 tensors are passed as uint16_t bit patterns.
+ *   - Work is enqueued on the given HIP stream (NULL = legacy default stream) and
+ *     is stream-ordered; no entry point synchronises the host.
+ *   - Per-tensor quantisation state (amax, scale, decode tables) lives in a
+ *     caller-allocated device buffer of hif8_state_size() bytes ("state").  A
+ *     state must be initialised once with hif8_state_init() and must not be used
+ *     by two streams at the same time.
+ *
+ * Semantics of the two HiF8 qdq flavours the reference has:
+ *   HIF8_SEM_NPU   -- ospnext/quant_cy_npu/base/cusrc/hif8_quant_op.h:88-151, the
+ *                     path taken when quant_dequant_float is called without
+ *                     force_py (QTensor.py:115-117): a true 8-bit format (flush
+ *                     below 2^-23, 2^-22 for [2^-23,2^-22), +-Inf from |x|>=40960).
+ *   HIF8_SEM_TORCH -- ospnext/quant_cy_npu/base/QFuncs/hif8.py:6-23, the
+ *                     force_py=True path (no flush, no saturation).
+ *   They agree exactly on {0} U [2^-22, 40960).  Codes always follow HIF8_SEM_NPU.
+ */
+#ifndef HIF8_MI355X_H
+#define HIF8_MI355X_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t *hif8_stream_t; /* == hipStream_t */
+
+enum {
+    HIF8_OK = 0,
+    HIF8_ERR_ARG = -1,       /* null pointer, negative or empty size, bad enum */
+    HIF8_ERR_SHAPE = -2,     /* shape the kernel does not support (see each call) */
+    HIF8_ERR_ALIGN = -3,     /* pointer alignment the kernel needs is not met */
+    HIF8_ERR_HIP = -4,       /* a HIP runtime call or kernel launch failed */
+};
+
+enum { HIF8_DTYPE_BF16 = 0, HIF8_DTYPE_F32 = 1 };
+enum { HIF8_SEM_NPU = 0, HIF8_SEM_TORCH = 1 };
+enum { HIF8_A_BF16 = 0, HIF8_A_CODES = 1 };
+
+/* Text for a status code (static storage). */
+const char *hif8_strerror(int status);
+
+/* ---------------------------------------------------------------------------
+ * Per-tensor state.  Holds the reduction counter, amax, scale and the two
+ * 256-entry decode tables x_q(code) of one quantised tensor.
+ * Replaces the scalar tensors x_max / scale of _quant
+ * (ospnext/modules/hif8_linear.py:45-46), which the reference keeps on device.
+ */
+size_t hif8_state_size(void);
+/* Clear the counters of a fresh state (a fill kernel, no hipMemset). */
+int hif8_state_init(void *state, hif8_stream_t stream);
+/* Host-readable copy of a state's scalars: amax bits, scale (fp32 value). */
+int hif8_state_read(const void *state, uint32_t *amax_bits, float *scale, hif8_stream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * amax + scale: hif8_linear.py:45-46
+ *   x_max = x.abs().amax().clamp(min=1e-8);  scale = scale_max / x_max
+ * with torch's rounding: scale = rnd(rnd(1/x_max) * scale_max), rnd = the input
+ * dtype.  One pass over x; the last workgroup also fills the decode tables.
+ * dtype: HIF8_DTYPE_BF16 or HIF8_DTYPE_F32.  n >= 1.
+ */
+int hif8_absmax_scale(const void *x, int dtype, int64_t n, float scale_max, void *state,
+                      hif8_stream_t stream);
+
+/* Set a state's scale directly (no amax): used for the unscaled qdq drop-ins and
+ * for callers that carry their own scale. */
+int hif8_set_scale(void *state, int dtype, float scale, hif8_stream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * Encode: HiF8 codes of qdq(x * scale), NPU semantics (hif8_linear.py:47-48 with
+ * QTensor.py:94-128 -> hif8_quant_op.h:88-151).  codes: n bytes.
+ */
+int hif8_encode(const void *x, int dtype, int64_t n, const void *state, uint8_t *codes,
+                hif8_stream_t stream);
+
+/* Fake quant: y = quant_dequant_float(x * scale, QType('hif8'), force_fp32=True) / scale
+ * (hif8_linear.py:47-48).  y has the dtype of x.  semantics: HIF8_SEM_*. */
+int hif8_fake_quant(const void *x, int dtype, int64_t n, const void *state, void *y,
+                    int semantics, hif8_stream_t stream);
+
+/* Decode codes to x_q = decode(code) / scale in out_dtype (bf16 x_q of a bf16
+ * tensor, or fp32 x_q of an fp32 tensor). */
+int hif8_decode(const uint8_t *codes, int64_t n, const void *state, int out_dtype, void *y,
+                hif8_stream_t stream);
+
+/* Unscaled qdq drop-ins for the reference's pybind entry points
+ * npu_quant.hif8_quant(x, y) and npu_quant.hif8_quant_bf16(x, y)
+ * (ospnext/quant_cy_npu/base/cusrc/npu_quant.cpp:19-33 -> run_hif8_kernel[_bf16],
+ * hif8_quant_op.h:208-214).  Unlike the reference, n is 64-bit, every length is
+ * handled (no 512-element batches past the end) and semantics is selectable
+ * (HIF8_SEM_TORCH gives QFuncs/hif8.py:6-23). */
+int hif8_quant_f32(const float *x, float *y, int64_t n, int semantics, hif8_stream_t stream);
+int hif8_quant_bf16(const uint16_t *x, uint16_t *y, int64_t n, int semantics,
+                    hif8_stream_t stream);
+
+/* ---------------------------------------------------------------------------
+ * Fused HiF8 linear forward: hif8_linear.py:68-86
+ *   y[M,N] = F.linear(x_q, w_q, bias) = x_q @ w_q^T + bias
+ * with w_q = decode(w_codes)/scale_w taken from w_state's table, and x_q either
+ * bf16 values (a_fmt = HIF8_A_BF16, e.g. from hif8_fake_quant) or HiF8 codes
+ * decoded through a_state's table (a_fmt = HIF8_A_CODES; a_state ignored for
+ * bf16).  bf16 MFMA, fp32 accumulation, bias added in fp32, bf16 output (RNE).
+ *   a: [M,K] row-major; w_codes: [N,K] row-major bytes; bias: [N] bf16 or NULL;
+ *   y: [M,N] row-major bf16.
+ * Shapes: K % 64 == 0, N % 8 == 0; M, N, K >= 1 and < 2^31.  16-byte aligned
+ * a, w_codes and y.
+ */
+int hif8_linear_fwd(const void *a, int a_fmt, const void *a_state, const uint8_t *w_codes,
+                    const void *w_state, const uint16_t *bias, uint16_t *y, int64_t M,
+                    int64_t N, int64_t K, hif8_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* HIF8_MI355X_H */

@@ -1,0 +1,581 @@
+// HiF8 per-tensor quantisation kernels for MI355X (gfx950): amax + scale,
+// encode to 8-bit codes, fake-quant (qdq) and decode.  C ABI at the bottom;
+// declarations and reference citations in include/hif8_mi355x.h.
+//
+// Data layout: a quantised tensor is its original buffer plus a State (device
+// memory, caller-owned) holding amax, scale and two 256-entry decode tables
+// x_q(code).  Codes are one byte per element in the input's element order.
+//
+// Bandwidth design: each thread moves 16 elements per step with 128-bit loads
+// and stores (bf16: 2 x 16 B in, 16 B of codes out); the code of an element is
+// an LDS table lookup indexed by the bf16 magnitude bits of x*scale, so the
+// per-element ALU work is a multiply, a packed bf16 convert, a clamp and one
+// ds_read_u8.  amax is one read pass with packed u16 max and one atomic per
+// workgroup; the last workgroup computes the scale and the decode tables.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "hif8_common.h"
+#include "hif8_internal.h"
+
+namespace hif8 {
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+__constant__ EncTable kEncTable = make_enc_table();
+
+// ---------------------------------------------------------------- helpers
+
+__device__ __forceinline__ uint32_t f2u(float f) { return __builtin_bit_cast(uint32_t, f); }
+__device__ __forceinline__ float u2f(uint32_t u) { return __builtin_bit_cast(float, u); }
+__device__ __forceinline__ float bf2f(uint32_t b) { return u2f(b << 16); }
+
+// float -> bf16 bits, round-to-nearest-even, NaN -> 0x7FC0 (c10::BFloat16).
+__device__ __forceinline__ uint32_t f2bf(float f)
+{
+    uint32_t u = f2u(f);
+    if ((u & 0x7FFFFFFFu) > 0x7F800000u) return 0x7FC0u;
+    return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
+}
+
+// Packed RNE convert of two finite floats (v_cvt_pk_bf16_f32).
+__device__ __forceinline__ uint32_t f2bf_pk(float lo, float hi)
+{
+    typedef float f32x2 __attribute__((ext_vector_type(2)));
+    typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+    f32x2 v = {lo, hi};
+    bf16x2 r = __builtin_convertvector(v, bf16x2);
+    return __builtin_bit_cast(uint32_t, r);
+}
+
+// QFuncs/hif8.py:6-23 on one fp32 value, with the same fp32 operations.
+// floor(log2(v)) of the normal value v = |x| + 2^-45 is taken from its exponent
+// field; torch's log2 agrees with it wherever the result can differ.
+__device__ float qdq_torch(float x)
+{
+    float xu = fabsf(x);
+    float sign = float(x > 0.0f) - float(x < 0.0f);
+    if (!(xu <= 3.402823466e38f)) return __builtin_nanf("");   // NaN, Inf -> NaN
+    float v = xu + 0x1p-45f;
+    int e = int((f2u(v) >> 23) & 0xFF) - 127;
+    int ae = e < 0 ? -e : e;
+    int mb = ae <= 3 ? 3 : ae <= 7 ? 2 : ae <= 15 ? 1 : 0;
+    float t = xu * __builtin_ldexpf(1.0f, mb - e);
+    float r = __builtin_floorf(t + 0.5f);
+    return r * __builtin_ldexpf(1.0f, e - mb) * sign;
+}
+
+__device__ __forceinline__ float qdq_npu(float x) { return u2f(decode_bits(encode_npu_bits(f2u(x)))); }
+
+// Scalar reference route for one element: returns the qdq output in the
+// tensor's dtype (bf16 bits in the low half, or fp32 bits) and the code.
+template <int DT>
+__device__ __forceinline__ void slow_elem(uint32_t xbits, float s, int sem, uint32_t &ybits, uint32_t &code)
+{
+    if (DT == kBF16) {
+        uint32_t xs = f2bf(bf2f(xbits) * s);                  // x * scale   (bf16)
+        code = encode_npu_bits(xs << 16);
+        float q = sem == kSemTorch ? qdq_torch(bf2f(xs)) : qdq_npu(bf2f(xs));
+        uint32_t qb = f2bf(q);                                // out.to(bf16)
+        ybits = f2bf(bf2f(qb) / s);                           // / scale     (bf16)
+    } else {
+        float xs = u2f(xbits) * s;
+        code = encode_npu_bits(f2u(xs));
+        float q = sem == kSemTorch ? qdq_torch(xs) : qdq_npu(xs);
+        ybits = f2u(q / s);
+    }
+}
+
+// Scale rule of hif8_linear.py:45-46 for the dtype; returns scale as fp32.
+__device__ float scale_from_amax(uint32_t amax_bits, int dtype, float smax, bool &fast)
+{
+    float a, s;
+    if (dtype == kBF16) {
+        uint32_t ab = amax_bits & 0x7FFFu;
+        if (ab <= 0x7F80u) ab = ab > 0x322Cu ? ab : 0x322Cu;   // clamp(min=bf16(1e-8))
+        a = bf2f(ab);
+        float r = bf2f(f2bf(1.0f / a));                      // reciprocal()   (bf16)
+        s = bf2f(f2bf(r * smax));                            // * scale_max    (bf16)
+    } else {
+        a = u2f(amax_bits & 0x7FFFFFFFu);
+        if (!__builtin_isnan(a)) a = a > 1e-8f ? a : 1e-8f;
+        float r = 1.0f / a;
+        s = r * smax;
+    }
+    fast = __builtin_isfinite(a) && __builtin_isfinite(s) && s > 0.0f;
+    return s;
+}
+
+// Fill the decode tables of st for scale s (one entry per thread, 256 threads).
+// bf16 tensors: x_q = rnd_bf16(q / s) with q exact in bf16 (QTensor.py:126-127
+// then the bf16 division of hif8_linear.py:48).  fp32 tensors: x_q = q / s in
+// fp32, and the bf16 GEMM operand is its autocast rounding.
+__device__ void fill_luts(State *st, float s, uint32_t c)
+{
+    float y = u2f(decode_bits(c)) / s;
+    st->lut_f32[c] = y;
+    st->lut_bf16[c] = uint16_t(f2bf(y));
+}
+
+// ---------------------------------------------------------------- kernels
+
+__global__ void k_state_init(State *st)
+{
+    if (threadIdx.x == 0) {
+        st->counter = 0;
+        st->amax_acc = 0;
+        st->amax_bits = 0;
+        st->scale = 0.0f;
+        st->fast = 0;
+        st->dtype = 0;
+        st->finite = 0;
+    }
+}
+
+__global__ __launch_bounds__(256) void k_set_scale(State *st, int dtype, float s)
+{
+    uint32_t c = threadIdx.x;
+    if (c == 0) {
+        st->scale = s;
+        st->dtype = uint32_t(dtype);
+        st->fast = (__builtin_isfinite(s) && s > 0.0f) ? 1u : 0u;
+        st->finite = 0;   // no amax pass: inputs may hold NaN
+        st->amax_bits = 0;
+    }
+    fill_luts(st, s, c);
+}
+
+constexpr int kTPB = 256;
+
+// One pass of |x| max.  Magnitude bit patterns order like the values and put
+// NaN above Inf, so an unsigned max propagates NaN as torch's amax does.
+template <int DT>
+__global__ __launch_bounds__(kTPB) void k_absmax(const void *__restrict__ xv, int64_t n,
+                                                  State *__restrict__ st, float smax)
+{
+    typedef uint16_t u16x2 __attribute__((ext_vector_type(2)));
+    const int tid = threadIdx.x;
+    uint32_t m = 0;
+    const int64_t stride = int64_t(gridDim.x) * kTPB;
+    if (DT == kBF16) {
+        const uint16_t *x = (const uint16_t *)xv;
+        const int64_t nvec = n >> 3;                       // uint4 = 8 bf16
+        const u32x4 *xq = (const u32x4 *)x;
+        u16x2 acc = {0, 0};
+        int64_t i = int64_t(blockIdx.x) * kTPB + tid;
+        for (; i + 3 * stride < nvec; i += 4 * stride) {
+            u32x4 v0 = xq[i];
+            u32x4 v1 = xq[i + stride];
+            u32x4 v2 = xq[i + 2 * stride];
+            u32x4 v3 = xq[i + 3 * stride];
+#define HIF8_ACC(v)                                                                          \
+    acc = __builtin_elementwise_max(acc, __builtin_bit_cast(u16x2, (v).x & 0x7FFF7FFFu));   \
+    acc = __builtin_elementwise_max(acc, __builtin_bit_cast(u16x2, (v).y & 0x7FFF7FFFu));   \
+    acc = __builtin_elementwise_max(acc, __builtin_bit_cast(u16x2, (v).z & 0x7FFF7FFFu));   \
+    acc = __builtin_elementwise_max(acc, __builtin_bit_cast(u16x2, (v).w & 0x7FFF7FFFu));
+            HIF8_ACC(v0) HIF8_ACC(v1) HIF8_ACC(v2) HIF8_ACC(v3)
+        }
+        for (; i < nvec; i += stride) {
+            u32x4 v0 = xq[i];
+            HIF8_ACC(v0)
+        }
+#undef HIF8_ACC
+        m = acc.x > acc.y ? acc.x : acc.y;
+        for (int64_t j = (nvec << 3) + int64_t(blockIdx.x) * kTPB + tid; j < n; j += stride) {
+            uint32_t b = x[j] & 0x7FFFu;
+            m = b > m ? b : m;
+        }
+    } else {
+        const uint32_t *x = (const uint32_t *)xv;
+        const int64_t nvec = n >> 2;
+        const u32x4 *xq = (const u32x4 *)x;
+        int64_t i = int64_t(blockIdx.x) * kTPB + tid;
+        uint32_t m0 = 0, m1 = 0;
+        for (; i + stride < nvec; i += 2 * stride) {
+            u32x4 v0 = xq[i];
+            u32x4 v1 = xq[i + stride];
+            m0 = max(m0, max(max(v0.x & 0x7FFFFFFFu, v0.y & 0x7FFFFFFFu), max(v0.z & 0x7FFFFFFFu, v0.w & 0x7FFFFFFFu)));
+            m1 = max(m1, max(max(v1.x & 0x7FFFFFFFu, v1.y & 0x7FFFFFFFu), max(v1.z & 0x7FFFFFFFu, v1.w & 0x7FFFFFFFu)));
+        }
+        for (; i < nvec; i += stride) {
+            u32x4 v0 = xq[i];
+            m0 = max(m0, max(max(v0.x & 0x7FFFFFFFu, v0.y & 0x7FFFFFFFu), max(v0.z & 0x7FFFFFFFu, v0.w & 0x7FFFFFFFu)));
+        }
+        m = max(m0, m1);
+        for (int64_t j = (nvec << 2) + int64_t(blockIdx.x) * kTPB + tid; j < n; j += stride)
+            m = max(m, x[j] & 0x7FFFFFFFu);
+    }
+    // wavefront reduction, then across the 4 waves through LDS
+    for (int o = 32; o > 0; o >>= 1) m = max(m, (uint32_t)__shfl_xor((int)m, o, 64));
+    __shared__ uint32_t red[kTPB / 64];
+    __shared__ uint32_t last;
+    if ((tid & 63) == 0) red[tid >> 6] = m;
+    __syncthreads();
+    if (tid == 0) {
+        m = max(max(red[0], red[1]), max(red[2], red[3]));
+        __hip_atomic_fetch_max(&st->amax_acc, m, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        uint32_t prev = __hip_atomic_fetch_add(&st->counter, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+        last = (prev == gridDim.x - 1) ? 1u : 0u;
+    }
+    __syncthreads();
+    if (!last) return;
+    // last workgroup: read and reset the accumulators, compute scale and tables
+    __shared__ float s_sh;
+    if (tid == 0) {
+        uint32_t a = __hip_atomic_exchange(&st->amax_acc, 0u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(&st->counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        bool fast;
+        float s = scale_from_amax(a, DT, smax, fast);
+        st->amax_bits = a;
+        st->scale = s;
+        st->fast = fast ? 1u : 0u;
+        st->finite = fast ? 1u : 0u;   // amax finite => every element finite
+        st->dtype = uint32_t(DT);
+        s_sh = s;
+    }
+    __syncthreads();
+    fill_luts(st, s_sh, uint32_t(tid));
+}
+
+// LDS map of the quantise kernels: [0,512) bf16 decode table, [1024,2048) fp32
+// decode table, [kTabLo, kTabHi] the encode table (so the clamped magnitude
+// bits are the LDS address).
+constexpr uint32_t kLdsLutBf16 = 0;
+constexpr uint32_t kLdsLutF32 = 1024;
+constexpr uint32_t kLdsBytes = (kTabLo + sizeof(EncTable) + 15) & ~15u;
+static_assert(kLdsLutF32 + 1024 <= kTabLo, "LDS map overlap");
+
+__device__ __forceinline__ uint32_t clampu(uint32_t u)
+{
+    return u < kTabLo ? kTabLo : (u > kTabHi ? kTabHi : u);
+}
+
+// Sign fix-up for 4 magnitude codes: a code of magnitude 0 stays 0x00 (0x80 is NaN).
+__device__ __forceinline__ uint32_t apply_signs(uint32_t mags, uint32_t signs80)
+{
+    return mags | ((mags + 0x7F7F7F7Fu) & signs80);
+}
+
+// MODE 0: codes, MODE 1: qdq in the input dtype, MODE 2: decode codes -> x_q.
+template <int DT, int MODE>
+__global__ __launch_bounds__(kTPB) void k_quant(const void *__restrict__ xv, int64_t n,
+                                                 const State *__restrict__ st, void *__restrict__ outv,
+                                                 int sem, int use_state)
+{
+    __shared__ __attribute__((aligned(16))) uint8_t lds[kLdsBytes];
+    const int tid = threadIdx.x;
+    float s = use_state ? st->scale : 1.0f;
+    bool fast = use_state ? (st->fast != 0) : true;
+    // NaN inputs map to the Inf entry of the table; unless an amax pass proved
+    // the tensor finite, each 16-element group is checked and patched.
+    const bool nan_guard = use_state ? (st->finite == 0) : true;
+    // decode tables for this scale
+    {
+        uint32_t c = uint32_t(tid);
+        float y;
+        if (use_state) y = st->lut_f32[c];
+        else y = u2f(decode_bits(c));
+        ((float *)(lds + kLdsLutF32))[c] = y;
+        ((uint16_t *)(lds + kLdsLutBf16))[c] = use_state ? st->lut_bf16[c] : uint16_t(f2bf(y));
+    }
+    if (MODE != 2) {
+        const uint4 *src = (const uint4 *)&kEncTable;
+        uint4 *dst = (uint4 *)(lds + kTabLo);
+        for (uint32_t i = tid; i < sizeof(EncTable) / 16; i += kTPB) dst[i] = src[i];
+    }
+    __syncthreads();
+    const uint16_t *lut16 = (const uint16_t *)(lds + kLdsLutBf16);
+    const float *lut32 = (const float *)(lds + kLdsLutF32);
+
+    const int64_t ngrp = n >> 4;  // 16 elements per step
+    const int64_t stride = int64_t(gridDim.x) * kTPB;
+    int64_t g = int64_t(blockIdx.x) * kTPB + tid;
+
+    if (MODE == 2) {
+        // decode: 16 codes -> 16 outputs
+        const uint4 *cq = (const uint4 *)xv;
+        for (; g < ngrp; g += stride) {
+            uint4 c = cq[g];
+            uint32_t cw[4] = {c.x, c.y, c.z, c.w};
+            if (DT == kBF16) {
+                uint32_t o[8];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    uint32_t d = cw[j];
+                    o[2 * j] = uint32_t(lut16[d & 0xFF]) | (uint32_t(lut16[(d >> 8) & 0xFF]) << 16);
+                    o[2 * j + 1] = uint32_t(lut16[(d >> 16) & 0xFF]) | (uint32_t(lut16[d >> 24]) << 16);
+                }
+                uint4 *out = (uint4 *)outv;
+                out[2 * g] = make_uint4(o[0], o[1], o[2], o[3]);
+                out[2 * g + 1] = make_uint4(o[4], o[5], o[6], o[7]);
+            } else {
+                uint4 *out = (uint4 *)outv;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    uint32_t d = cw[j];
+                    out[4 * g + j] = make_uint4(f2u(lut32[d & 0xFF]), f2u(lut32[(d >> 8) & 0xFF]),
+                                                f2u(lut32[(d >> 16) & 0xFF]), f2u(lut32[d >> 24]));
+                }
+            }
+        }
+        for (int64_t j = (ngrp << 4) + int64_t(blockIdx.x) * kTPB + tid; j < n; j += stride) {
+            uint32_t c = ((const uint8_t *)xv)[j];
+            if (DT == kBF16) ((uint16_t *)outv)[j] = lut16[c];
+            else ((float *)outv)[j] = lut32[c];
+        }
+        return;
+    }
+
+    if (fast) {
+        for (; g < ngrp; g += stride) {
+            uint32_t codes[4];
+            uint32_t wide[16];   // per element: magnitude bits of xs, and the full bits for fp32
+            uint32_t xs_full[16];
+            if (DT == kBF16) {
+                const u32x4 *xq = (const u32x4 *)xv;
+                u32x4 a = xq[2 * g];
+                u32x4 b = xq[2 * g + 1];
+                uint32_t p[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    uint32_t p0 = p[2 * j], p1 = p[2 * j + 1];
+                    uint32_t q01 = f2bf_pk(u2f(p0 << 16) * s, u2f(p0 & 0xFFFF0000u) * s);
+                    uint32_t q23 = f2bf_pk(u2f(p1 << 16) * s, u2f(p1 & 0xFFFF0000u) * s);
+                    uint32_t u0 = q01 & 0x7FFFu, u1 = (q01 >> 16) & 0x7FFFu;
+                    uint32_t u2 = q23 & 0x7FFFu, u3 = (q23 >> 16) & 0x7FFFu;
+                    wide[4 * j] = u0; wide[4 * j + 1] = u1; wide[4 * j + 2] = u2; wide[4 * j + 3] = u3;
+                    xs_full[4 * j] = q01 & 0xFFFFu; xs_full[4 * j + 1] = q01 >> 16;
+                    xs_full[4 * j + 2] = q23 & 0xFFFFu; xs_full[4 * j + 3] = q23 >> 16;
+                    uint32_t mags = uint32_t(lds[clampu(u0)]) | (uint32_t(lds[clampu(u1)]) << 8) |
+                                    (uint32_t(lds[clampu(u2)]) << 16) | (uint32_t(lds[clampu(u3)]) << 24);
+                    uint32_t signs = __builtin_amdgcn_perm(p1, p0, 0x07050301u) & 0x80808080u;
+                    codes[j] = apply_signs(mags, signs);
+                }
+            } else {
+                const u32x4 *xq = (const u32x4 *)xv;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    u32x4 a = xq[4 * g + j];
+                    uint32_t v[4] = {a.x, a.y, a.z, a.w};
+                    uint32_t mags = 0;
+#pragma unroll
+                    for (int t = 0; t < 4; ++t) {
+                        uint32_t xs = f2u(u2f(v[t]) * s);
+                        xs_full[4 * j + t] = xs;
+                        uint32_t u = (xs >> 16) & 0x7FFFu;
+                        wide[4 * j + t] = u;
+                        mags |= uint32_t(lds[clampu(u)]) << (8 * t);
+                    }
+                    uint32_t signs = __builtin_amdgcn_perm(v[3], v[2], 0x07030C0Cu) & 0x80800000u;
+                    signs |= (__builtin_amdgcn_perm(v[1], v[0], 0x0C0C0703u) & 0x00008080u);
+                    codes[j] = apply_signs(mags, signs);
+                }
+            }
+            if (nan_guard) {
+                uint32_t mx = 0;
+#pragma unroll
+                for (int t = 0; t < 16; ++t) mx = wide[t] > mx ? wide[t] : mx;
+                if (mx > 0x7F80u) {
+#pragma unroll
+                    for (int t = 0; t < 16; ++t)
+                        if (wide[t] > 0x7F80u) codes[t >> 2] = (codes[t >> 2] & ~(0xFFu << (8 * (t & 3)))) | (0x80u << (8 * (t & 3)));
+                }
+            }
+            if (MODE == 0) {
+                ((uint4 *)outv)[g] = make_uint4(codes[0], codes[1], codes[2], codes[3]);
+                continue;
+            }
+            // qdq output through the decode table
+            uint32_t y[16];
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                uint32_t d = codes[j];
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    uint32_t c = (d >> (8 * t)) & 0xFF;
+                    y[4 * j + t] = DT == kBF16 ? uint32_t(lut16[c]) : f2u(lut32[c]);
+                }
+            }
+            if (sem == kSemTorch) {
+                // the torch route differs only below 2^-22 (non-zero) and from 40960 up
+#pragma unroll
+                for (int t = 0; t < 16; ++t) {
+                    uint32_t u = wide[t];
+                    uint32_t full = DT == kBF16 ? (xs_full[t] & 0x7FFFu) : (xs_full[t] & 0x7FFFFFFFu);
+                    if ((full != 0u && u < 0x3480u) || u >= 0x4720u) {
+                        float xs = DT == kBF16 ? bf2f(xs_full[t]) : u2f(xs_full[t]);
+                        float q = qdq_torch(xs);
+                        if (DT == kBF16) y[t] = f2bf(bf2f(f2bf(q)) / s);
+                        else y[t] = f2u(q / s);
+                    }
+                }
+            }
+            if (DT == kBF16) {
+                uint4 *out = (uint4 *)outv;
+                out[2 * g] = make_uint4(y[0] | (y[1] << 16), y[2] | (y[3] << 16), y[4] | (y[5] << 16), y[6] | (y[7] << 16));
+                out[2 * g + 1] = make_uint4(y[8] | (y[9] << 16), y[10] | (y[11] << 16), y[12] | (y[13] << 16), y[14] | (y[15] << 16));
+            } else {
+                uint4 *out = (uint4 *)outv;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) out[4 * g + j] = make_uint4(y[4 * j], y[4 * j + 1], y[4 * j + 2], y[4 * j + 3]);
+            }
+        }
+    } else {
+        // degenerate scale (amax Inf/NaN, scale 0/Inf/NaN): element-wise reference route
+        for (int64_t j = g; j < (ngrp << 4); j += stride) {
+            uint32_t xb = DT == kBF16 ? ((const uint16_t *)xv)[j] : ((const uint32_t *)xv)[j];
+            uint32_t yb, code;
+            slow_elem<DT>(xb, s, sem, yb, code);
+            if (MODE == 0) ((uint8_t *)outv)[j] = uint8_t(code);
+            else if (DT == kBF16) ((uint16_t *)outv)[j] = uint16_t(yb);
+            else ((uint32_t *)outv)[j] = yb;
+        }
+    }
+    // tail (n % 16) through the scalar route
+    for (int64_t j = (ngrp << 4) + int64_t(blockIdx.x) * kTPB + tid; j < n; j += stride) {
+        uint32_t xb = DT == kBF16 ? ((const uint16_t *)xv)[j] : ((const uint32_t *)xv)[j];
+        uint32_t yb, code;
+        slow_elem<DT>(xb, s, sem, yb, code);
+        if (MODE == 0) ((uint8_t *)outv)[j] = uint8_t(code);
+        else if (DT == kBF16) ((uint16_t *)outv)[j] = uint16_t(yb);
+        else ((uint32_t *)outv)[j] = yb;
+    }
+}
+
+// ---------------------------------------------------------------- launch
+
+static int grid_for(int64_t units, int max_blocks)
+{
+    int64_t b = (units + kTPB - 1) / kTPB;
+    if (b < 1) b = 1;
+    return int(b < max_blocks ? b : max_blocks);
+}
+
+static int cu_count()
+{
+    static int cus[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (cus[dev] == 0) {
+        int c = 0;
+        if (hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || c <= 0) c = 256;
+        cus[dev] = c;
+    }
+    return cus[dev];
+}
+
+static inline bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+static int last_launch() { return hipGetLastError() == hipSuccess ? HIF8_OK : HIF8_ERR_HIP; }
+
+}  // namespace hif8
+
+using namespace hif8;
+
+extern "C" {
+
+const char *hif8_strerror(int status)
+{
+    switch (status) {
+    case HIF8_OK: return "ok";
+    case HIF8_ERR_ARG: return "invalid argument (null pointer, empty or negative size, or bad enum)";
+    case HIF8_ERR_SHAPE: return "unsupported shape";
+    case HIF8_ERR_ALIGN: return "pointer not 16-byte aligned";
+    case HIF8_ERR_HIP: return "HIP launch or runtime failure";
+    default: return "unknown hif8 status";
+    }
+}
+
+size_t hif8_state_size(void) { return sizeof(State); }
+
+int hif8_state_init(void *state, hif8_stream_t stream)
+{
+    if (!state) return HIF8_ERR_ARG;
+    hipLaunchKernelGGL(k_state_init, dim3(1), dim3(64), 0, (hipStream_t)stream, (State *)state);
+    return last_launch();
+}
+
+int hif8_state_read(const void *state, uint32_t *amax_bits, float *scale, hif8_stream_t stream)
+{
+    if (!state) return HIF8_ERR_ARG;
+    State h;
+    if (hipMemcpyAsync(&h, state, 32, hipMemcpyDeviceToHost, (hipStream_t)stream) != hipSuccess) return HIF8_ERR_HIP;
+    if (hipStreamSynchronize((hipStream_t)stream) != hipSuccess) return HIF8_ERR_HIP;
+    if (amax_bits) *amax_bits = h.amax_bits;
+    if (scale) *scale = h.scale;
+    return HIF8_OK;
+}
+
+int hif8_absmax_scale(const void *x, int dtype, int64_t n, float scale_max, void *state,
+                      hif8_stream_t stream)
+{
+    if (!x || !state || n <= 0 || (dtype != HIF8_DTYPE_BF16 && dtype != HIF8_DTYPE_F32)) return HIF8_ERR_ARG;
+    if (!aligned16(x)) return HIF8_ERR_ALIGN;
+    const int per_thread_vec = dtype == HIF8_DTYPE_BF16 ? 8 : 4;
+    int grid = grid_for((n + per_thread_vec * 4 - 1) / (per_thread_vec * 4), cu_count() * 8);
+    if (dtype == HIF8_DTYPE_BF16)
+        hipLaunchKernelGGL(k_absmax<kBF16>, dim3(grid), dim3(kTPB), 0, (hipStream_t)stream, x, n, (State *)state, scale_max);
+    else
+        hipLaunchKernelGGL(k_absmax<kF32>, dim3(grid), dim3(kTPB), 0, (hipStream_t)stream, x, n, (State *)state, scale_max);
+    return last_launch();
+}
+
+int hif8_set_scale(void *state, int dtype, float scale, hif8_stream_t stream)
+{
+    if (!state || (dtype != HIF8_DTYPE_BF16 && dtype != HIF8_DTYPE_F32)) return HIF8_ERR_ARG;
+    hipLaunchKernelGGL(k_set_scale, dim3(1), dim3(256), 0, (hipStream_t)stream, (State *)state, dtype, scale);
+    return last_launch();
+}
+
+static int launch_quant(const void *x, int dtype, int64_t n, const void *state, void *out, int mode,
+                        int sem, int use_state, hif8_stream_t stream)
+{
+    if (!x || !out || n <= 0 || (use_state && !state)) return HIF8_ERR_ARG;
+    if (dtype != HIF8_DTYPE_BF16 && dtype != HIF8_DTYPE_F32) return HIF8_ERR_ARG;
+    if (sem != HIF8_SEM_NPU && sem != HIF8_SEM_TORCH) return HIF8_ERR_ARG;
+    if (!aligned16(x) || !aligned16(out)) return HIF8_ERR_ALIGN;
+    int grid = grid_for((n + 15) / 16, cu_count() * 8);
+    hipStream_t s = (hipStream_t)stream;
+    const State *st = (const State *)state;
+#define HIF8_LAUNCH(DT, MODE) \
+    hipLaunchKernelGGL((k_quant<DT, MODE>), dim3(grid), dim3(kTPB), 0, s, x, n, st, out, sem, use_state)
+    if (dtype == HIF8_DTYPE_BF16) {
+        if (mode == 0) HIF8_LAUNCH(kBF16, 0);
+        else if (mode == 1) HIF8_LAUNCH(kBF16, 1);
+        else HIF8_LAUNCH(kBF16, 2);
+    } else {
+        if (mode == 0) HIF8_LAUNCH(kF32, 0);
+        else if (mode == 1) HIF8_LAUNCH(kF32, 1);
+        else HIF8_LAUNCH(kF32, 2);
+    }
+#undef HIF8_LAUNCH
+    return last_launch();
+}
+
+int hif8_encode(const void *x, int dtype, int64_t n, const void *state, uint8_t *codes, hif8_stream_t stream)
+{
+    return launch_quant(x, dtype, n, state, codes, 0, HIF8_SEM_NPU, 1, stream);
+}
+
+int hif8_fake_quant(const void *x, int dtype, int64_t n, const void *state, void *y, int semantics,
+                    hif8_stream_t stream)
+{
+    return launch_quant(x, dtype, n, state, y, 1, semantics, 1, stream);
+}
+
+int hif8_decode(const uint8_t *codes, int64_t n, const void *state, int out_dtype, void *y, hif8_stream_t stream)
+{
+    return launch_quant(codes, out_dtype, n, state, y, 2, HIF8_SEM_NPU, 1, stream);
+}
+
+int hif8_quant_f32(const float *x, float *y, int64_t n, int semantics, hif8_stream_t stream)
+{
+    return launch_quant(x, HIF8_DTYPE_F32, n, nullptr, y, 1, semantics, 0, stream);
+}
+
+int hif8_quant_bf16(const uint16_t *x, uint16_t *y, int64_t n, int semantics, hif8_stream_t stream)
+{
+    return launch_quant(x, HIF8_DTYPE_BF16, n, nullptr, y, 1, semantics, 0, stream);
+}
+
+}  // extern "C"

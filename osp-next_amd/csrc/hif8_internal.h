@@ -1,0 +1,31 @@
+// Internal declarations shared by the codec and GEMM translation units.
+#pragma once
+
+#include <stdint.h>
+
+#include "../../include/hif8_mi355x.h"
+
+namespace hif8 {
+
+constexpr int kBF16 = HIF8_DTYPE_BF16;
+constexpr int kF32 = HIF8_DTYPE_F32;
+constexpr int kSemNpu = HIF8_SEM_NPU;
+constexpr int kSemTorch = HIF8_SEM_TORCH;
+
+// Per-tensor quantisation state (device memory, hif8_state_size() bytes).
+struct alignas(256) State {
+    uint32_t counter;      // workgroups finished in the running amax pass (reset by the last)
+    uint32_t amax_acc;     // running max of magnitude bits (reset by the last workgroup)
+    uint32_t amax_bits;    // amax of the last pass: bf16 or fp32 magnitude bits
+    float scale;           // scale in the tensor dtype's rounding, held as fp32
+    uint32_t fast;         // 1 when amax and scale are finite and scale > 0
+    uint32_t dtype;        // HIF8_DTYPE_* the tables were built for
+    uint32_t finite;       // 1 when an amax pass proved every input element finite
+    uint32_t pad;
+    uint16_t lut_bf16[256];  // bf16 bits of x_q(code) = rnd(decode(code) / scale)
+    float lut_f32[256];      // fp32 decode(code) / scale
+};
+
+static_assert(sizeof(State) % 256 == 0, "state size");
+
+}  // namespace hif8

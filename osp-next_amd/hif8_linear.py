@@ -1,0 +1,276 @@
+"""HiF8 fake-quant linear layer, mirroring ``ospnext/modules/hif8_linear.py``.
+
+Forward (hif8_linear.py:68-86)::
+
+    x_q = qdq(x * s_x) / s_x,  s_x = scale_max_forward / max|x|
+    w_q = qdq(W * s_w) / s_w,  s_w = scale_max_forward / max|W|
+    y   = x_q @ w_q.T + bias
+
+Here ``x_q`` comes from one amax pass and one quantise pass (HIP kernels), ``W``
+is held as packed 8-bit HiF8 codes plus a per-tensor state, and the product is
+the fused dequant-GEMM ``hif8_linear_fwd``.  The dequantised operands are
+bit-identical to the reference's; only the fp32 accumulation order differs.
+
+Backward (hif8_linear.py:88-111) quantises the incoming gradient with
+``scale_max_backward`` through the same HIP kernels and forms the products
+with torch matmuls on the decoded operands.
+"""
+from __future__ import annotations
+
+from typing import Optional, Tuple
+
+import torch
+import torch.nn as nn
+from torch import Tensor
+
+from . import _lib
+
+
+# --------------------------------------------------------------------- state
+
+
+class QuantState:
+    """Device-side per-tensor quantisation state (amax, scale, decode tables)."""
+
+    def __init__(self, device: torch.device):
+        self.device = torch.device(device)
+        self.buf = _lib.new_state(self.device)
+
+    @property
+    def ptr(self) -> int:
+        return self.buf.data_ptr()
+
+    def scale(self) -> Tensor:
+        """The scale as a 0-dim fp32 device tensor (a copy; no host sync)."""
+        return self.buf[12:16].view(torch.float32).reshape(()).clone()
+
+    def read(self) -> Tuple[int, float]:
+        """(amax bits, scale) on the host (synchronises the stream)."""
+        import ctypes
+        a = ctypes.c_uint32()
+        s = ctypes.c_float()
+        _lib.check(_lib.load().hif8_state_read(self.ptr, ctypes.byref(a), ctypes.byref(s),
+                                               _lib.stream_ptr(self.device)), "hif8_state_read")
+        return int(a.value), float(s.value)
+
+    def lut_bf16(self) -> Tensor:
+        """The 256-entry bf16 decode table x_q(code) (a device view)."""
+        return self.buf[32:544].view(torch.bfloat16)
+
+
+def _aligned(t: Tensor) -> Tensor:
+    """The kernels use 128-bit accesses: realign offset views with one copy."""
+    return t if t.data_ptr() % 16 == 0 else t.clone()
+
+
+def absmax_scale(x: Tensor, scale_max: float, state: QuantState) -> QuantState:
+    """hif8_linear.py:45-46 into ``state`` (amax, scale and decode tables)."""
+    _lib.require_gpu_tensor(x, "x")
+    x = _aligned(x)
+    if x.numel() == 0:
+        raise ValueError("amax of an empty tensor")
+    _lib.check(_lib.load().hif8_absmax_scale(x.data_ptr(), _lib.dtype_code(x.dtype), x.numel(),
+                                             float(scale_max), state.ptr, _lib.stream_ptr(x.device)),
+               "hif8_absmax_scale")
+    return state
+
+
+def encode(x: Tensor, state: QuantState) -> Tensor:
+    """HiF8 codes of qdq(x * scale) (NPU semantics), one byte per element."""
+    _lib.require_gpu_tensor(x, "x")
+    x = _aligned(x)
+    codes = torch.empty(x.shape, dtype=torch.uint8, device=x.device)
+    if x.numel():
+        _lib.check(_lib.load().hif8_encode(x.data_ptr(), _lib.dtype_code(x.dtype), x.numel(), state.ptr,
+                                           codes.data_ptr(), _lib.stream_ptr(x.device)), "hif8_encode")
+    return codes
+
+
+def fake_quant(x: Tensor, state: QuantState, semantics: int = _lib.SEM_NPU) -> Tensor:
+    """qdq(x * scale) / scale in x's dtype (hif8_linear.py:47-48)."""
+    _lib.require_gpu_tensor(x, "x")
+    x = _aligned(x)
+    y = torch.empty_like(x)
+    if x.numel():
+        _lib.check(_lib.load().hif8_fake_quant(x.data_ptr(), _lib.dtype_code(x.dtype), x.numel(), state.ptr,
+                                               y.data_ptr(), semantics, _lib.stream_ptr(x.device)),
+                   "hif8_fake_quant")
+    return y
+
+
+def decode(codes: Tensor, state: QuantState, dtype: torch.dtype = torch.bfloat16) -> Tensor:
+    """x_q = decode(code) / scale in ``dtype``."""
+    _lib.require_gpu_tensor(codes, "codes")
+    codes = _aligned(codes)
+    y = torch.empty(codes.shape, dtype=dtype, device=codes.device)
+    if codes.numel():
+        _lib.check(_lib.load().hif8_decode(codes.data_ptr(), codes.numel(), state.ptr, _lib.dtype_code(dtype),
+                                           y.data_ptr(), _lib.stream_ptr(codes.device)), "hif8_decode")
+    return y
+
+
+def _quant(x: Tensor, scale_max: float, semantics: int = _lib.SEM_NPU) -> Tuple[Tensor, Tensor]:
+    """hif8_linear.py:42-50: returns ``(x_q, scale)``, scale a 0-dim tensor of x's dtype."""
+    xc = x.contiguous()
+    st = absmax_scale(xc, scale_max, QuantState(xc.device))
+    xq = fake_quant(xc, st, semantics)
+    return xq.view(x.shape), st.scale().to(x.dtype)
+
+
+# ------------------------------------------------------------ packed weight
+
+
+class PackedWeight:
+    """8-bit HiF8 weight storage: codes [N, K] (uint8) + the weight's state.
+
+    Halves the bytes of a bf16 weight; ``dequantize()`` gives the reference's
+    ``w_q`` exactly.
+    """
+
+    def __init__(self, weight: Tensor, scale_max: float):
+        w = weight.detach().contiguous()
+        self.shape = tuple(w.shape)
+        self.src_dtype = w.dtype
+        self.state = absmax_scale(w, scale_max, QuantState(w.device))
+        self.codes = encode(w, self.state)
+        self.scale_max = float(scale_max)
+        self.key = (w.data_ptr(), weight._version, w.device)
+
+    def dequantize(self, dtype: Optional[torch.dtype] = None) -> Tensor:
+        return decode(self.codes, self.state, dtype or self.src_dtype)
+
+
+def linear_fwd(a: Tensor, a_fmt: int, a_state: Optional[QuantState], w: PackedWeight,
+               bias: Optional[Tensor]) -> Tensor:
+    """hif8_linear_fwd: y[M,N] = x_q[M,K] @ w_q[N,K]^T + bias, bf16 out."""
+    M, K = a.shape
+    N = w.shape[0]
+    if w.shape[1] != K:
+        raise ValueError(f"in_features mismatch: x has {K}, weight has {w.shape[1]}")
+    y = torch.empty((M, N), dtype=torch.bfloat16, device=a.device)
+    b_ptr = 0
+    if bias is not None:
+        bias = bias.detach().to(torch.bfloat16).contiguous()
+        b_ptr = bias.data_ptr()
+    _lib.check(_lib.load().hif8_linear_fwd(a.data_ptr(), a_fmt, a_state.ptr if a_state is not None else None,
+                                           w.codes.data_ptr(), w.state.ptr, b_ptr or None, y.data_ptr(),
+                                           M, N, K, _lib.stream_ptr(a.device)), "hif8_linear_fwd")
+    return y
+
+
+def quantize_activation(x2: Tensor, scale_max: float, a_format: str):
+    """Quantise a [M,K] activation for the fused GEMM: returns (a, a_fmt, state)."""
+    st = absmax_scale(x2, scale_max, QuantState(x2.device))
+    if a_format == "codes" or x2.dtype != torch.bfloat16:
+        return encode(x2, st), _lib.A_CODES, st
+    return fake_quant(x2, st), _lib.A_BF16, st
+
+
+# --------------------------------------------------------------- autograd
+
+
+class _HIF8LinearFunction(torch.autograd.Function):
+    """hif8_linear.py:56-111 with the fused HIP forward."""
+
+    @staticmethod
+    def forward(ctx, x, weight, bias, scale_max_forward: float, scale_max_backward: float,
+                packed: Optional[PackedWeight] = None, a_format: str = "bf16"):
+        if x.dtype not in (torch.bfloat16, torch.float32):
+            raise TypeError(f"HIF8Linear takes bfloat16 or float32 input, got {x.dtype}")
+        K = x.shape[-1]
+        x2 = x.reshape(-1, K).contiguous()
+        if packed is None:
+            packed = PackedWeight(weight, scale_max_forward)
+        a, a_fmt, a_st = quantize_activation(x2, scale_max_forward, a_format)
+        y = linear_fwd(a, a_fmt, a_st, packed, bias)
+        if any(ctx.needs_input_grad[:3]):
+            ctx.a, ctx.a_fmt, ctx.a_st, ctx.packed = a, a_fmt, a_st, packed
+            ctx.x_dtype, ctx.w_dtype = x.dtype, weight.dtype
+            ctx.x_shape = x.shape
+            ctx.has_bias = bias is not None
+            ctx.b_dtype = bias.dtype if bias is not None else None
+            ctx.smb = float(scale_max_backward)
+        return y.view(*x.shape[:-1], y.shape[-1])
+
+    @staticmethod
+    def backward(ctx, grad_output):
+        # x_q and w_q as the reference saves them (hif8_linear.py:78-82)
+        if ctx.a_fmt == _lib.A_CODES:
+            x_q = decode(ctx.a, ctx.a_st, torch.bfloat16 if ctx.x_dtype == torch.bfloat16 else torch.float32)
+        else:
+            x_q = ctx.a
+        w_q = ctx.packed.dequantize(ctx.w_dtype)
+        grad_q, _ = _quant(grad_output.contiguous(), ctx.smb)            # :93
+        g_2d = grad_q.reshape(-1, grad_q.shape[-1])
+        ct = torch.promote_types(g_2d.dtype, w_q.dtype)
+        grad_input = (g_2d.to(ct) @ w_q.to(ct).contiguous()).to(ctx.x_dtype).view(ctx.x_shape)  # :97
+        grad_weight = (g_2d.t().contiguous().to(ct) @ x_q.to(ct)).to(ctx.w_dtype)             # :104
+        grad_bias = g_2d.sum(0).to(ctx.b_dtype) if ctx.has_bias else None                   # :107
+        return grad_input, grad_weight, grad_bias, None, None, None, None
+
+
+# ------------------------------------------------------------------ module
+
+
+class HIF8Linear(nn.Linear):
+    """Drop-in ``nn.Linear`` with HiF8 qdq of input and weight
+    (hif8_linear.py:117-170; same constructor and forward).
+
+    Extras beyond the reference interface:
+      * ``prepack(drop_weight=False)`` stores the weight as 8-bit HiF8 codes once
+        (inference); without it the packed weight is rebuilt whenever the weight
+        tensor changes (version counter or storage), which matches the
+        reference's per-call re-quantisation.
+      * ``a_format`` = ``"bf16"`` (activation fake-quantised to bf16 x_q) or
+        ``"codes"`` (activation encoded to 8-bit codes and decoded in the GEMM).
+    """
+
+    def __init__(self, in_features: int, out_features: int, bias: bool = True,
+                 scale_max_forward: float = 15.0, scale_max_backward: float = 224.0,
+                 device=None, dtype=None):
+        super().__init__(in_features, out_features, bias, device=device, dtype=dtype)
+        self.scale_max_forward = scale_max_forward
+        self.scale_max_backward = scale_max_backward
+        self.a_format = "bf16"
+        self._packed: Optional[PackedWeight] = None
+        self._prepacked = False
+
+    def _packed_weight(self) -> PackedWeight:
+        w = self.weight
+        key = (w.data_ptr(), w._version, w.device)
+        p = self._packed
+        if self._prepacked and p is not None:
+            return p
+        if p is None or p.key != key or p.scale_max != float(self.scale_max_forward):
+            p = PackedWeight(w, self.scale_max_forward)
+            self._packed = p
+        return p
+
+    @torch.no_grad()
+    def prepack(self, drop_weight: bool = False) -> "HIF8Linear":
+        self._packed = PackedWeight(self.weight, self.scale_max_forward)
+        self._prepacked = True
+        if drop_weight:
+            self.weight = nn.Parameter(torch.empty(0, device=self.weight.device, dtype=self.weight.dtype),
+                                       requires_grad=False)
+        return self
+
+    def forward(self, x: Tensor) -> Tensor:
+        packed = self._packed_weight()
+        return _HIF8LinearFunction.apply(x, self.weight, self.bias, self.scale_max_forward,
+                                         self.scale_max_backward, packed, self.a_format)
+
+    def extra_repr(self) -> str:
+        return (f"in_features={self.in_features}, out_features={self.out_features}, "
+                f"bias={self.bias is not None}, "
+                f"scale_max_fwd={self.scale_max_forward}, "
+                f"scale_max_bwd={self.scale_max_backward}")
+
+
+def make_linear(quant: str, in_features: int, out_features: int, scale_max_forward: float = 15.0,
+                scale_max_backward: float = 224.0, bias: bool = True, **kw) -> nn.Module:
+    """``_make_linear`` (ospnext/modules/osp_next.py:42-58)."""
+    if quant == "hif8":
+        return HIF8Linear(in_features, out_features, bias=bias, scale_max_forward=scale_max_forward,
+                          scale_max_backward=scale_max_backward, **kw)
+    return nn.Linear(in_features, out_features, bias=bias, **kw)

@@ -1,0 +1,143 @@
+"""HiF8 quantise-dequantise API, mirroring OSP-Next's ``quant_cy_npu`` surface.
+
+* ``QType``               -- ``ospnext/quant_cy_npu/base/QType.py:5-43`` (only the
+  fields the ``'hif8'`` path reads).
+* ``quant_dequant_float`` -- ``ospnext/quant_cy_npu/base/QTensor.py:94-128``.
+* ``quant_func``          -- ``QTensor.py:131-144`` (straight-through estimator).
+* ``hif8_quant`` / ``hif8_quant_bf16`` -- the pybind entry points
+  ``npu_quant.hif8_quant(x, y)`` / ``npu_quant.hif8_quant_bf16(x, y)``
+  (``cusrc/npu_quant.cpp:19-39``): in-place into a caller-allocated ``y``.
+
+All arithmetic runs in the HIP library; tensors must live on the GPU.
+"""
+from __future__ import annotations
+
+from copy import deepcopy
+
+import torch
+from torch import Tensor
+from torch.autograd import Function
+
+from . import _lib
+
+
+class QType:
+    """Format descriptor (QType.py:5-43).  For ``'hif8'`` only ``desc`` and
+    ``q_dim`` matter: ``blk_size = blk_outer_size = 1`` means no padding."""
+
+    desc: str
+    exp_bits: int = -1
+    man_bits: int = -1
+    k_bits: int = -1
+    k_outer_bits: int = 0
+    blk_size: int = 1
+    blk_outer_size: int = 1
+    exp_max: int = -1
+    exp_min: int = -1
+    k_max: int = -1
+    fp_val_max: float = -1
+    q_dim: int = -1
+    man_shift_bit: int = -1
+    exp_offset: int = 0
+    do_carry: bool = True
+
+    def __init__(self, desc: str):
+        self.desc = desc
+
+    def dim_(self, dim: int) -> "QType":
+        self.q_dim = dim
+        return self
+
+    def dim(self, dim: int) -> "QType":
+        out = deepcopy(self)
+        out.q_dim = dim
+        return out
+
+    def copy(self) -> "QType":
+        return deepcopy(self)
+
+    def __repr__(self) -> str:
+        return f"QType: {self.desc}   Dim: {self.q_dim}  ExpOffset: {self.exp_offset}"
+
+
+def _qdq_inplace(x: Tensor, y: Tensor, semantics: int) -> None:
+    _lib.require_gpu_tensor(x, "x")
+    _lib.require_gpu_tensor(y, "y")
+    if x.dtype != y.dtype or x.numel() != y.numel():
+        raise ValueError("x and y must have the same dtype and number of elements")
+    n = x.numel()
+    if n == 0:
+        return
+    if x.data_ptr() % 16:
+        x = x.clone()
+    if y.data_ptr() % 16:
+        tmp = torch.empty_like(y)
+        _qdq_inplace(x, tmp, semantics)
+        y.copy_(tmp)
+        return
+    L = _lib.load()
+    s = _lib.stream_ptr(x.device)
+    if x.dtype == torch.bfloat16:
+        _lib.check(L.hif8_quant_bf16(x.data_ptr(), y.data_ptr(), n, semantics, s), "hif8_quant_bf16")
+    elif x.dtype == torch.float32:
+        _lib.check(L.hif8_quant_f32(x.data_ptr(), y.data_ptr(), n, semantics, s), "hif8_quant_f32")
+    else:
+        raise TypeError(f"unsupported dtype {x.dtype}")
+
+
+def hif8_quant(x: Tensor, y: Tensor) -> None:
+    """``npu_quant.hif8_quant`` (fp32, npu_quant.cpp:19-25): y <- qdq(x)."""
+    if x.dtype != torch.float32:
+        raise TypeError("hif8_quant takes float32 tensors")
+    _qdq_inplace(x, y, _lib.SEM_NPU)
+
+
+def hif8_quant_bf16(x: Tensor, y: Tensor) -> None:
+    """``npu_quant.hif8_quant_bf16`` (bf16, npu_quant.cpp:27-33): y <- qdq(x)."""
+    if x.dtype != torch.bfloat16:
+        raise TypeError("hif8_quant_bf16 takes bfloat16 tensors")
+    _qdq_inplace(x, y, _lib.SEM_NPU)
+
+
+@torch.no_grad()
+def quant_dequant_float(x: Tensor, Q: QType, force_py: bool = False, force_fp32: bool = False,
+                        **kwargs) -> Tensor:
+    """QTensor.py:94-128 for ``Q.desc == 'hif8'``.
+
+    ``force_py=False`` follows the NPU kernel (``hif8_quant_op.h``), ``True`` the
+    torch function ``quant_hif8`` (``QFuncs/hif8.py:6-23``).  The output has the
+    input's dtype (QTensor.py:126-127).  bf16 inputs are computed from their
+    exact fp32 values whether or not ``force_fp32`` is set; the reference's
+    bf16-precision torch route (force_py=True, force_fp32=False) is not
+    reproduced.  fp16 and other dtypes go through fp32 like QTensor.py:72-79.
+    """
+    if Q.desc in ("fp16", "bf16", "fp32"):
+        return x
+    if Q.desc != "hif8":
+        raise NotImplementedError(f"only the 'hif8' format is implemented, got {Q.desc!r}")
+    semantics = _lib.SEM_TORCH if force_py else _lib.SEM_NPU
+    dtype_ori = x.dtype
+    xc = x.contiguous()
+    if xc.dtype not in (torch.bfloat16, torch.float32):
+        xc = xc.to(torch.float32)
+    out = torch.empty_like(xc)
+    _qdq_inplace(xc, out, semantics)
+    if out.dtype != dtype_ori:
+        out = out.to(dtype_ori)
+    return out
+
+
+class QuantFunc(Function):
+    """Straight-through qdq (QTensor.py:131-140)."""
+
+    @staticmethod
+    def forward(ctx, x, Q, force_py, force_fp32):
+        return quant_dequant_float(x, Q, force_py, force_fp32)
+
+    @staticmethod
+    def backward(ctx, grad):
+        return grad, None, None, None
+
+
+def quant_func(x: Tensor, Q: QType, force_py: bool = False, force_fp32: bool = False) -> Tensor:
+    return QuantFunc.apply(x, Q, force_py, force_fp32)

@@ -1,0 +1,143 @@
+"""CPU tests of the product's host-side pieces (no GPU work):
+
+* the C-ABI library loads and exports every symbol include/hif8_mi355x.h declares,
+  and the Python binding declares the same set;
+* argument validation returns the documented status codes before any launch;
+* the kernels' shared HiF8 arithmetic (hif8_common.h), built for the host,
+  matches the oracle for every bf16 input, random fp32 inputs, every code, and
+  the LDS encode table.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+import subprocess
+
+import numpy as np
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "hif8_mi355x.h")
+
+
+def header_functions():
+    src = open(HEADER).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    return sorted(set(re.findall(r"\b(hif8_\w+)\s*\(", src)))
+
+
+def test_library_exports_every_declared_symbol(pkg):
+    L = pkg._lib.load()
+    names = header_functions()
+    assert len(names) >= 12
+    for n in names:
+        assert hasattr(L, n), n
+    assert set(names) == set(pkg._lib.SIGNATURES), "binding and header disagree"
+    out = subprocess.run(["nm", "-D", "--defined-only", pkg._lib.LIB_PATH], capture_output=True, text=True).stdout
+    exported = set(re.findall(r"\bT (hif8_\w+)", out))
+    assert set(names) <= exported
+
+
+def test_status_codes_without_gpu(pkg):
+    L = pkg._lib.load()
+    assert L.hif8_state_size() % 256 == 0
+    assert L.hif8_strerror(0) == b"ok"
+    fake = 0x100000      # aligned, never dereferenced: validation fails first
+    odd = 0x100001
+    assert L.hif8_state_init(None, None) == -1
+    assert L.hif8_absmax_scale(None, 0, 16, 15.0, fake, None) == -1
+    assert L.hif8_absmax_scale(fake, 0, 0, 15.0, fake, None) == -1
+    assert L.hif8_absmax_scale(fake, 7, 16, 15.0, fake, None) == -1
+    assert L.hif8_absmax_scale(odd, 0, 16, 15.0, fake, None) == -3
+    assert L.hif8_encode(fake, 0, 16, None, fake, None) == -1
+    assert L.hif8_fake_quant(fake, 0, 16, fake, fake, 5, None) == -1
+    assert L.hif8_fake_quant(fake, 0, 16, fake, odd, 0, None) == -3
+    assert L.hif8_quant_bf16(None, fake, 16, 0, None) == -1
+    assert L.hif8_decode(fake, -1, fake, 0, fake, None) == -1
+    # linear: bad format, missing state, K % 64, N % 8, alignment
+    args = dict(a=fake, fmt=0, ast=None, w=fake, wst=fake, b=None, y=fake, M=128, N=256, K=512)
+
+    def lin(**kw):
+        a = {**args, **kw}
+        return L.hif8_linear_fwd(a["a"], a["fmt"], a["ast"], a["w"], a["wst"], a["b"], a["y"], a["M"], a["N"],
+                                 a["K"], None)
+    assert lin(fmt=3) == -1
+    assert lin(fmt=1) == -1
+    assert lin(wst=None) == -1
+    assert lin(M=0) == -1
+    assert lin(K=100) == -2
+    assert lin(N=100) == -2
+    assert lin(y=odd) == -3
+    assert lin(b=fake + 2) == -3
+
+
+def test_python_layer_refuses_cpu_tensors(pkg):
+    torch = pytest.importorskip("torch")
+    x = torch.zeros(16, dtype=torch.bfloat16)
+    with pytest.raises(ValueError):
+        pkg.quant_dequant_float(x, pkg.QType("hif8"))
+    assert pkg.quant_dequant_float(x, pkg.QType("bf16")) is x
+
+
+@pytest.fixture(scope="module")
+def hostlib(tmp_path_factory):
+    out = tmp_path_factory.mktemp("hostchk") / "libhostchk.so"
+    src = os.path.join(ROOT, "tests", "host_encoder_check.cpp")
+    subprocess.run(["g++", "-O2", "-std=c++17", "-fPIC", "-shared", src, "-o", str(out)], check=True)
+    L = ctypes.CDLL(str(out))
+    p = ctypes.c_void_p
+    L.chk_encode_bits.argtypes = [p, p, ctypes.c_int64]
+    L.chk_decode_bits.argtypes = [p]
+    L.chk_table.argtypes = [p, p, p]
+    L.chk_table.restype = ctypes.c_int64
+    return L
+
+
+def _enc(L, bits32):
+    bits32 = np.ascontiguousarray(bits32, np.uint32)
+    c = np.empty(bits32.shape, np.uint8)
+    L.chk_encode_bits(bits32.ctypes.data, c.ctypes.data, bits32.size)
+    return c
+
+
+def test_device_encoder_matches_oracle_every_bf16(hostlib, R):
+    b = np.arange(65536, dtype=np.uint32)
+    xf = (b << 16).view(np.float32)
+    fin = ~np.isnan(xf)
+    got = _enc(hostlib, b << 16)
+    assert np.array_equal(got[fin], R.encode_npu(xf[fin]))
+    assert np.all(got[~fin] == 0x80)
+
+
+def test_device_encoder_matches_oracle_random_fp32(hostlib, R):
+    rng = np.random.default_rng(11)
+    u = rng.integers(0, 2 ** 32, 1_000_000, dtype=np.uint64).astype(np.uint32)
+    # concentrate half of them on the HiF8 range
+    e = rng.integers(-26, 18, 500_000)
+    v = (np.ldexp(rng.random(500_000) + 1, e) * rng.choice([-1, 1], 500_000)).astype(np.float32)
+    u = np.concatenate([u, v.view(np.uint32)])
+    xf = u.view(np.float32)
+    fin = ~np.isnan(xf)
+    assert np.array_equal(_enc(hostlib, u)[fin], R.encode_npu(xf[fin]))
+
+
+def test_device_decode_matches_oracle(hostlib, R):
+    y = np.empty(256, np.uint32)
+    hostlib.chk_decode_bits(y.ctypes.data)
+    d = R.decode_table()
+    nan = np.isnan(d)
+    assert np.array_equal(y[~nan], d[~nan].view(np.uint32))
+    assert np.all(np.isnan(y.view(np.float32)[nan]))
+
+
+def test_lds_encode_table(hostlib, R):
+    buf = np.zeros(1 << 16, np.uint8)
+    lo, hi = ctypes.c_uint32(), ctypes.c_uint32()
+    n = hostlib.chk_table(buf.ctypes.data, ctypes.byref(lo), ctypes.byref(hi))
+    tab = buf[:n]
+    # kernel lookup: magnitude bits clamped to [lo, hi], entry = magnitude code
+    u = np.arange(0, 0x7F81, dtype=np.uint32)      # every finite bf16 magnitude incl. Inf
+    idx = np.clip(u, lo.value, hi.value) - lo.value
+    xf = (u << 16).view(np.float32)
+    assert np.array_equal(tab[idx], R.encode_npu(xf) & 0x7F)

@@ -1,0 +1,409 @@
+"""Pins the CPU oracle (oracle/hif8_ref.py, oracle/hif8_npu_ref.c) to facts that do
+not come from retyping its own formulas:
+
+* brute force: the NPU qdq of every finite bf16 value is the nearest HiF8 value
+  (ties away from zero), with the overflow cut at 40960 (midpoint to the missing
+  1.5*2^15) -- a characterisation independent of the kernel's bit tricks;
+* exact rational arithmetic: QFuncs/hif8.py evaluated with Fractions and an
+  explicit fp32 rounding (exponent from bit length, not log2) matches the numpy
+  restatement bit for bit over every bf16 input and random fp32 inputs;
+* real torch: the scale expression ``scale_max / x.abs().amax().clamp(min=1e-8)``,
+  bf16 ``x*scale`` and ``q/scale``, and the whole ``_quant`` chain evaluated with
+  torch's own CPU kernels;
+* special points, invariants, code-table structure, the config-1 known answers
+  recorded when the reference was surveyed, and committed fixtures;
+* mutation checks: planting a plausible mistake in the oracle makes a pin fail.
+"""
+from __future__ import annotations
+
+import math
+from fractions import Fraction
+
+import numpy as np
+import pytest
+
+ALL_BF16 = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+
+
+# ----------------------------------------------------------------- helpers
+
+
+def round_fp32(q: Fraction) -> Fraction:
+    """Round a non-negative rational to float32, nearest-even, with subnormals."""
+    if q == 0:
+        return q
+    n, d = q.numerator, q.denominator
+    e = n.bit_length() - d.bit_length()
+    if Fraction(2) ** e > q:
+        e -= 1
+    e = max(e, -126)
+    quantum = Fraction(2) ** (e - 23)
+    k = q / quantum
+    fl = k.numerator // k.denominator
+    rem = k - fl
+    if rem > Fraction(1, 2) or (rem == Fraction(1, 2) and fl % 2 == 1):
+        fl += 1
+    return fl * quantum
+
+
+def floor_log2(q: Fraction) -> int:
+    n, d = q.numerator, q.denominator
+    e = n.bit_length() - d.bit_length()
+    return e - 1 if Fraction(2) ** e > q else e
+
+
+def torch_exact(xf: float) -> float:
+    """QFuncs/hif8.py:6-23 in exact rationals with every fp32 op rounded explicitly."""
+    if math.isnan(xf) or math.isinf(xf):
+        return math.nan
+    x = Fraction(xf)
+    a = abs(x)
+    sign = 1 if x > 0 else (-1 if x < 0 else 0)
+    v = round_fp32(a + Fraction(1, 2 ** 45))
+    E = floor_log2(v)
+    ae = abs(E)
+    mb = 3 if ae <= 3 else 2 if ae <= 7 else 1 if ae <= 15 else 0
+    t = round_fp32(a * Fraction(2) ** (mb - E))
+    u = round_fp32(t + Fraction(1, 2))
+    r = u.numerator // u.denominator
+    res = round_fp32(r * Fraction(2) ** (E - mb))
+    if sign == 0:
+        return 0.0
+    out = float(res)
+    return -out if sign < 0 else out  # r == 0 with x < 0 gives -0.0 as 0 * 2^k * -1 does
+
+
+def hif8_magnitudes(R) -> np.ndarray:
+    d = R.decode_table().astype(np.float64)
+    v = np.unique(np.abs(d[np.isfinite(d)]))
+    return v
+
+
+def nearest_hif8(R, xf: np.ndarray) -> np.ndarray:
+    """Brute force: nearest finite HiF8 value, ties away from zero, Inf from 40960."""
+    V = hif8_magnitudes(R)
+    a = np.abs(xf.astype(np.float64))
+    hi_i = np.clip(np.searchsorted(V, a, side="right"), 1, len(V) - 1)
+    lo, hi = V[hi_i - 1], V[hi_i]
+    mag = np.where(a - lo >= hi - a, hi, lo)
+    mag = np.where(a >= V[-1], V[-1], mag)
+    mag = np.where(a >= 40960.0, np.inf, mag)
+    out = np.where(np.signbit(xf) & (mag != 0), -mag, mag)
+    return out.astype(np.float32)
+
+
+def bits32(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.float32).view(np.uint32)
+
+
+# ------------------------------------------------------- special points
+
+
+def test_special_points(R):
+    x = np.array([1.0625, 15.75, 0.3, -1.0625, 2.5, 3.5, 0.0], np.float32)
+    want = np.array([1.125, 16.0, 0.3125, -1.125, 2.5, 3.5, 0.0], np.float32)
+    for sem in ("torch", "npu"):
+        assert np.array_equal(R.quant_hif8(x, sem), want), sem
+    big = np.array([40959.0, 40960.0, -40960.0, 49152.0, 2.0 ** -23, 1.5 * 2.0 ** -24], np.float32)
+    npu = R.quant_hif8_npu(big)
+    assert npu[0] == 32768.0 and np.isposinf(npu[1]) and np.isneginf(npu[2]) and np.isposinf(npu[3])
+    assert npu[4] == 2.0 ** -22 and npu[5] == 0.0
+    tor = R.quant_hif8_torch(big)
+    assert tor[1] == 49152.0 and tor[3] == 49152.0 and tor[4] == 2.0 ** -23
+
+
+# ------------------------------------------------------ NPU brute force
+
+
+def test_npu_equals_nearest_hif8_every_bf16(R):
+    xf = R.bf16_to_f32(ALL_BF16)
+    fin = ~np.isnan(xf)
+    got = R.quant_hif8_npu(xf[fin])
+    want = nearest_hif8(R, xf[fin])
+    bad = np.nonzero(bits32(got) != bits32(want))[0]
+    assert bad.size == 0, f"{bad.size} mismatches, first x={xf[fin][bad[:5]]}"
+
+
+def test_npu_nan_and_zero_follow_kernel_selects(R):
+    # hif8_quant_op.h:137-150: flushed values are +0; NaN fails both Inf guards -> -Inf
+    y = R.quant_hif8_npu(np.array([np.nan, -0.0, -1e-30], np.float32))
+    assert np.isneginf(y[0])
+    assert bits32(y[1:]).tolist() == [0, 0]
+
+
+def test_npu_random_fp32_equals_nearest(R):
+    rng = np.random.default_rng(7)
+    e = rng.integers(-30, 17, 200000)
+    m = rng.random(200000) + 1.0
+    xf = (np.ldexp(m, e) * rng.choice([-1, 1], 200000)).astype(np.float32)
+    got = R.quant_hif8_npu(xf)
+    want = nearest_hif8(R, xf)
+    assert np.array_equal(bits32(got), bits32(want))
+
+
+# ------------------------------------------------- torch-path exactness
+
+
+def test_torch_restatement_matches_exact_rationals_every_bf16(R):
+    xf = R.bf16_to_f32(ALL_BF16)
+    got = R.quant_hif8_torch(xf)
+    with np.errstate(over="ignore"):
+        want = np.array([torch_exact(float(v)) for v in xf], np.float32)
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan)
+    bad = np.nonzero(bits32(got[~nan]) != bits32(want[~nan]))[0]
+    assert bad.size == 0, f"{bad.size} mismatches, first x={xf[~nan][bad[:5]]}"
+
+
+def test_torch_restatement_matches_exact_rationals_random_fp32(R):
+    rng = np.random.default_rng(3)
+    u = rng.integers(0, 2 ** 32, 4000, dtype=np.uint64).astype(np.uint32)
+    xf = u.view(np.float32)
+    xf = xf[np.isfinite(xf)]
+    # plus values just below powers of two, where log2 rounding could bite
+    k = rng.integers(-60, 60, 2000)
+    near = (np.ldexp(1.0, k) * (1 - 2.0 ** -24)).astype(np.float32)
+    xf = np.concatenate([xf, near, -near])
+    got = R.quant_hif8_torch(xf)
+    with np.errstate(over="ignore"):
+        want = np.array([torch_exact(float(v)) for v in xf], np.float32)
+    assert np.array_equal(bits32(got), bits32(want))
+
+
+def test_torch_and_npu_agree_on_shared_range(R):
+    xf = R.bf16_to_f32(ALL_BF16)
+    a = np.abs(xf)
+    shared = (a == 0) | ((a >= 2.0 ** -22) & (a < 40960))
+    t = R.quant_hif8_torch(xf[shared])
+    n = R.quant_hif8_npu(xf[shared])
+    assert np.array_equal(bits32(t), bits32(n))
+    # and outside it they do differ (the tails are real)
+    tails = ~shared & np.isfinite(xf)
+    assert (bits32(R.quant_hif8_torch(xf[tails])) != bits32(R.quant_hif8_npu(xf[tails]))).any()
+
+
+def test_torch_literal_ops_match_numpy(R):
+    """The reference's own torch expression (QFuncs/hif8.py:6-23) on torch's CPU
+    kernels (oracle.quant_hif8_torch_cpu, also the CPU baseline) against the numpy
+    restatement: pins numpy's log2/pow/floor to torch's."""
+    torch = pytest.importorskip("torch")
+    xf = R.bf16_to_f32(ALL_BF16)
+    res = R.quant_hif8_torch_cpu(torch.from_numpy(xf.copy()))
+    got = R.quant_hif8_torch(xf)
+    r = res.numpy()
+    nan = np.isnan(r)
+    assert np.array_equal(nan, np.isnan(got))
+    assert np.array_equal(bits32(r[~nan]), bits32(got[~nan]))
+
+
+# ---------------------------------------------------------- invariants
+
+
+@pytest.mark.parametrize("sem", ["torch", "npu"])
+def test_invariants(R, sem):
+    xf = R.bf16_to_f32(ALL_BF16)
+    xf = xf[np.isfinite(xf)]
+    q = R.quant_hif8(xf, sem)
+    # odd symmetry (up to the sign of zero)
+    qn = R.quant_hif8(-xf, sem)
+    assert np.array_equal(q, -qn) or np.array_equal(np.abs(q), np.abs(qn))
+    assert np.all((q == -qn) | ((q == 0) & (qn == 0)))
+    # idempotence, except where the torch route's +2^-45 offset moves 2^-45 to
+    # 2^-44 (QFuncs/hif8.py:13) and -0 (from a negative underflow) to +0
+    fin = np.isfinite(q)
+    q2 = R.quant_hif8(q[fin], sem)
+    same = bits32(q2) == bits32(q[fin])
+    if sem == "torch":
+        exempt = (np.abs(q[fin]) == 2.0 ** -45) | (q[fin] == 0)
+        assert np.all(same | exempt) and np.all(q2[np.abs(q[fin]) == 2.0 ** -45] != 0)
+    else:
+        assert np.all(same)
+    # monotone non-decreasing
+    order = np.argsort(xf, kind="stable")
+    qs = q[order].astype(np.float64)
+    assert np.all(qs[1:] >= qs[:-1])
+    # at most 4 significant bits
+    m, _ = np.frexp(q[fin & (q != 0)].astype(np.float64))
+    assert np.all((np.abs(m) * 16) == np.round(np.abs(m) * 16))
+
+
+# ---------------------------------------------------------- code table
+
+
+def test_code_table_structure(R):
+    d = R.decode_table()
+    assert np.isnan(d[0x80]) and np.isposinf(d[0x6F]) and np.isneginf(d[0xEF]) and d[0] == 0
+    fin = np.isfinite(d)
+    assert len(np.unique(d[fin])) == 253  # 126 magnitudes x 2 signs + zero
+    assert np.abs(d[fin]).max() == 32768.0
+    assert np.min(np.abs(d[fin & (d != 0)])) == 2.0 ** -22
+    for c in range(256):
+        if c in (0x00, 0x80):
+            continue
+        assert d[c ^ 0x80] == -d[c]
+    # every finite non-NaN code round-trips
+    codes = np.arange(256, dtype=np.uint8)
+    keep = codes != 0x80
+    assert np.array_equal(R.encode_npu(d[keep]), codes[keep])
+    # exactly the value set of the NPU kernel on bf16 inputs
+    xf = R.bf16_to_f32(ALL_BF16)
+    qv = np.unique(R.quant_hif8_npu(xf[np.isfinite(xf)]))
+    assert np.array_equal(np.sort(qv), np.sort(np.unique(d[~np.isnan(d)])))
+
+
+def test_codes_decode_to_npu_qdq_every_bf16(R):
+    xf = R.bf16_to_f32(ALL_BF16)
+    fin = ~np.isnan(xf)
+    c = R.encode_npu(xf[fin])
+    assert np.array_equal(bits32(R.decode(c)), bits32(R.quant_hif8_npu(xf[fin])))
+
+
+# ------------------------------------------------- scale and bf16 ops vs torch
+
+
+def test_scale_matches_torch_every_bf16_amax(R):
+    torch = pytest.importorskip("torch")
+    a = np.arange(32768, dtype=np.uint16)
+    t = torch.from_numpy(a.view(np.int16)).view(torch.bfloat16)
+    for smax in (15.0, 224.0):
+        # hif8_linear.py:45-46, elementwise over every candidate amax
+        x_max = t.clamp(min=1e-8)
+        scale = smax / x_max
+        want = scale.view(torch.int16).numpy().view(np.uint16)
+        got = np.array([R.hif8_scale_bf16(int(v), smax) for v in a], np.uint16)
+        nan = (want & 0x7FFF) > 0x7F80
+        assert np.array_equal(got[~nan], want[~nan])
+        assert np.all((got[nan] & 0x7FFF) > 0x7F80)
+
+
+def test_scale_double_rounding_is_observable(R):
+    """A single-rounded scale (bf16(15/amax)) would be a plausible mistake: it
+    differs from the reference's bf16(bf16(1/amax)*15) on many inputs."""
+    a = np.arange(0x3C00, 0x4400, dtype=np.uint16)  # amax in [2^-7, 2^9)
+    af = R.bf16_to_f32(a)
+    single = R.f32_to_bf16(np.float32(15.0) / af)
+    double = np.array([R.hif8_scale_bf16(int(v), 15.0) for v in a], np.uint16)
+    frac = np.mean(single != double)
+    assert frac > 0.1, frac
+
+
+def test_bf16_mul_div_by_scalar_tensor_match_torch(R):
+    torch = pytest.importorskip("torch")
+    rng = np.random.default_rng(5)
+    x = rng.integers(0, 65536, 200000).astype(np.uint16)
+    x = x[(x & 0x7FFF) < 0x7F80]
+    xt = torch.from_numpy(x.view(np.int16)).view(torch.bfloat16)
+    for sbits in (0x4080, 0x407F, 0x4329, 0x3F81, 0x4B19):
+        s = torch.tensor(sbits, dtype=torch.int16).view(torch.bfloat16)
+        sf = R.bf16_to_f32(np.array([sbits], np.uint16))[0]
+        mul = (xt * s).view(torch.int16).numpy().view(np.uint16)
+        div = (xt / s).view(torch.int16).numpy().view(np.uint16)
+        with np.errstate(all="ignore"):
+            assert np.array_equal(mul, R.f32_to_bf16(R.bf16_to_f32(x) * sf))
+            assert np.array_equal(div, R.f32_to_bf16(R.bf16_to_f32(x) / sf))
+
+
+@pytest.mark.parametrize("sem", ["torch", "npu"])
+def test_quant_chain_matches_torch_expression(R, sem):
+    """hif8_linear.py:42-50 + QTensor.py:94-128 evaluated by torch ops, with the
+    qdq step supplied by the oracle (torch path: also evaluated by torch)."""
+    torch = pytest.importorskip("torch")
+    xb = R.c1_input(seed=9, shape=(257, 129))
+    x = torch.from_numpy(xb.view(np.int16)).view(torch.bfloat16)
+    x_max = x.abs().amax().clamp(min=1e-8)
+    scale = 15.0 / x_max
+    scaled = x * scale
+    xf = scaled.to(torch.float32)
+    if sem == "torch":
+        xu = torch.abs(xf)
+        e = torch.floor(torch.log2(xu + 2 ** -45))
+        abse = e.abs()
+        mb = torch.zeros_like(abse)
+        mb[abse <= 15] = 1
+        mb[abse <= 7] = 2
+        mb[abse <= 3] = 3
+        q = torch.floor(xu * 2.0 ** (-e + mb) + 0.5) * 2.0 ** (e - mb) * torch.sign(xf)
+    else:
+        q = torch.from_numpy(R.quant_hif8_npu(xf.numpy()))
+    xq = q.to(torch.bfloat16) / scale
+    want = xq.view(torch.int16).numpy().view(np.uint16)
+    got, s_bits = R.quant_bf16(xb, 15.0, sem)
+    assert s_bits == int(scale.view(torch.int16).item()) & 0xFFFF
+    assert np.array_equal(got, want)
+
+
+def test_torch_cpu_linear_path_matches_bit_emulation(R):
+    """The CPU-baseline route (torch ops) equals the bit-level bf16 emulation."""
+    torch = pytest.importorskip("torch")
+    xb = R.activation_input(4, 96, 64, n_outlier=4)
+    wb = R.weight_input(5, 48, 64)
+    x = torch.from_numpy(xb.view(np.int16)).view(torch.bfloat16)
+    xq, s = R.quant_torch_cpu(x, 15.0)
+    want, s_bits = R.quant_bf16(xb, 15.0, "torch")
+    assert np.array_equal(xq.view(torch.int16).numpy().view(np.uint16), want)
+    y = R.linear_torch_cpu(x, torch.from_numpy(wb.view(np.int16)).view(torch.bfloat16))
+    y_ref, _, _ = R.linear(xb, wb, None, 15.0, "torch", accumulate="torch")
+    assert np.array_equal(y.view(torch.int16).numpy().view(np.uint16), y_ref)
+
+
+# ------------------------------------------------------- known answers
+
+
+def test_config1_known_answers(R, golden):
+    """Recorded when the reference was surveyed: amax 3.75, scale 4.0, max|xs| 15,
+    41 scaled elements below 2^-22, 33 where the two semantics differ."""
+    x = R.c1_input(0)
+    a = R.absmax_bf16(x)
+    s = R.hif8_scale_bf16(a, 15.0)
+    assert R.bf16_to_f32(np.array([a], np.uint16))[0] == 3.75
+    assert R.bf16_to_f32(np.array([s], np.uint16))[0] == 4.0
+    xs = R.bf16_to_f32(R.f32_to_bf16(R.bf16_to_f32(x) * np.float32(4.0)))
+    assert np.abs(xs).max() == 15.0
+    assert int(((np.abs(xs) < 2.0 ** -22) & (xs != 0)).sum()) == 41
+    qt = R.quant_hif8_torch(xs)
+    qn = R.quant_hif8_npu(xs)
+    assert int((bits32(qt) != bits32(qn)).sum()) == 33
+    assert golden["c1_meta"]["amax_bits"] == a and golden["c1_meta"]["scale_bits"] == s
+
+
+def test_committed_fixtures_reproduce(R, golden):
+    ex = golden["ex"]
+    xf = R.bf16_to_f32(ALL_BF16)
+    assert np.array_equal(R.f32_to_bf16(R.quant_hif8_npu(xf)), ex["npu_qdq"])
+    assert np.array_equal(R.f32_to_bf16(R.quant_hif8_torch(xf)), ex["torch_qdq"])
+    fin = ~np.isnan(xf)
+    assert np.array_equal(R.encode_npu(xf[fin]), ex["codes"][fin])
+    sc = golden["scale"]
+    sample = np.arange(0, 32768, 97)
+    assert all(R.hif8_scale_bf16(int(a), 15.0) == int(sc["scale15"][a]) for a in sample)
+    c1 = golden["c1"]
+    x = R.c1_input(0).ravel()
+    assert np.array_equal(x[c1["idx"]], c1["x"])
+
+
+# --------------------------------------------------------- mutation checks
+
+
+def test_planted_mistakes_are_caught(R):
+    """Swap in plausible wrong oracles; the brute-force pin must reject each."""
+    xf = R.bf16_to_f32(ALL_BF16)
+    xf = xf[np.isfinite(xf)]
+    want = nearest_hif8(R, xf)
+
+    def ties_even(x):  # round-half-even instead of half-away
+        a = np.abs(x).astype(np.float64)
+        e = np.floor(np.log2(np.maximum(a, 2.0 ** -30)))
+        mb = np.where(np.abs(e) <= 3, 3, np.where(np.abs(e) <= 7, 2, np.where(np.abs(e) <= 15, 1, 0)))
+        step = 2.0 ** (e - mb)
+        return (np.sign(x) * np.round(a / step) * step).astype(np.float32)
+
+    def thresholds_off_by_one(x):
+        a = np.abs(x).astype(np.float64)
+        e = np.floor(np.log2(np.maximum(a, 2.0 ** -30)))
+        mb = np.where(np.abs(e) < 3, 3, np.where(np.abs(e) < 7, 2, np.where(np.abs(e) < 15, 1, 0)))
+        step = 2.0 ** (e - mb)
+        return (np.sign(x) * np.floor(a / step + 0.5) * step).astype(np.float32)
+
+    for wrong in (ties_even, thresholds_off_by_one):
+        sel = (np.abs(xf) > 2.0 ** -20) & (np.abs(xf) < 30000)
+        assert (bits32(wrong(xf[sel])) != bits32(want[sel])).any(), wrong.__name__
