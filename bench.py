@@ -43,28 +43,44 @@ def make_inputs(torch, M, K, N, seed=0, dev="cuda:0"):
 
 
 def time_linear(pkg, torch, x, packed, b, steps, warmup, a_format):
-    """Times steps of [amax+scale, quantise, fused GEMM]; returns per-phase ms lists."""
+    """Times steps of [amax+scale, quantise, fused GEMM]; returns per-phase ms lists.
+
+    a_format "tiled": x_q written in the GEMM operand layout + tiled fused GEMM
+    (the HIF8Linear inference path); "bf16"/"codes": row-major x_q / codes and
+    the row-major fused GEMM."""
     st = pkg.QuantState(x.device)
     L = pkg._lib.load()
     stream = pkg._lib.stream_ptr(x.device)
     M, K = x.shape
     N = packed.shape[0]
     y = torch.empty(M, N, dtype=torch.bfloat16, device=x.device)
-    use_codes = a_format == "codes"
-    a = torch.empty((M, K), dtype=torch.uint8 if use_codes else torch.bfloat16, device=x.device)
-    fmt = pkg._lib.A_CODES if use_codes else pkg._lib.A_BF16
+    if a_format == "tiled":
+        a = torch.empty(pkg.tiled_rows(M) * K, dtype=torch.bfloat16, device=x.device)
+    else:
+        a = torch.empty((M, K), dtype=torch.uint8 if a_format == "codes" else torch.bfloat16, device=x.device)
 
-    def step():
+    def amax():
         pkg._lib.check(L.hif8_absmax_scale(x.data_ptr(), 0, x.numel(), 15.0, st.ptr, stream), "amax")
-        if use_codes:
+
+    def quant():
+        if a_format == "tiled":
+            pkg._lib.check(L.hif8_fake_quant_tiled(x.data_ptr(), 0, M, K, st.ptr, a.data_ptr(), 0, stream), "qt")
+        elif a_format == "codes":
             pkg._lib.check(L.hif8_encode(x.data_ptr(), 0, x.numel(), st.ptr, a.data_ptr(), stream), "encode")
         else:
             pkg._lib.check(L.hif8_fake_quant(x.data_ptr(), 0, x.numel(), st.ptr, a.data_ptr(), 0, stream), "qdq")
-        pkg._lib.check(L.hif8_linear_fwd(a.data_ptr(), fmt, st.ptr, packed.codes.data_ptr(), packed.state.ptr,
-                                         b.data_ptr(), y.data_ptr(), M, N, K, stream), "linear")
+
+    def gemm():
+        if a_format == "tiled":
+            pkg._lib.check(L.hif8_linear_fwd_tiled(a.data_ptr(), packed.wt.data_ptr(), packed.state.ptr,
+                                                   b.data_ptr(), y.data_ptr(), M, N, K, stream), "linear")
+        else:
+            fmt = pkg._lib.A_CODES if a_format == "codes" else pkg._lib.A_BF16
+            pkg._lib.check(L.hif8_linear_fwd(a.data_ptr(), fmt, st.ptr, packed.codes.data_ptr(), packed.state.ptr,
+                                             b.data_ptr(), y.data_ptr(), M, N, K, stream), "linear")
 
     for _ in range(warmup):
-        step()
+        amax(); quant(); gemm()
     torch.cuda.synchronize()
     ev = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(steps)]
     torch.cuda.synchronize()
@@ -72,27 +88,32 @@ def time_linear(pkg, torch, x, packed, b, steps, warmup, a_format):
     for i in range(steps):
         e = ev[i]
         e[0].record()
-        pkg._lib.check(L.hif8_absmax_scale(x.data_ptr(), 0, x.numel(), 15.0, st.ptr, stream), "amax")
+        amax()
         e[1].record()
-        if use_codes:
-            pkg._lib.check(L.hif8_encode(x.data_ptr(), 0, x.numel(), st.ptr, a.data_ptr(), stream), "encode")
-        else:
-            pkg._lib.check(L.hif8_fake_quant(x.data_ptr(), 0, x.numel(), st.ptr, a.data_ptr(), 0, stream), "qdq")
+        quant()
         e[2].record()
-        pkg._lib.check(L.hif8_linear_fwd(a.data_ptr(), fmt, st.ptr, packed.codes.data_ptr(), packed.state.ptr,
-                                         b.data_ptr(), y.data_ptr(), M, N, K, stream), "linear")
+        gemm()
         e[3].record()
     torch.cuda.synchronize()
     wall = (time.perf_counter() - t0) * 1e3
-    amax = [e[0].elapsed_time(e[1]) for e in ev]
-    quant = [e[1].elapsed_time(e[2]) for e in ev]
-    gemm = [e[2].elapsed_time(e[3]) for e in ev]
-    return {"wall_ms": wall, "amax": amax, "quant": quant, "gemm": gemm, "y": y}
+    return {"wall_ms": wall, "amax": [e[0].elapsed_time(e[1]) for e in ev],
+            "quant": [e[1].elapsed_time(e[2]) for e in ev], "gemm": [e[2].elapsed_time(e[3]) for e in ev], "y": y}
 
 
 def median(v):
     s = sorted(v)
     return s[len(s) // 2]
+
+
+def _cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.machine()
 
 
 def cpu_baseline(torch, M, K, N, sample_rows=1024):
@@ -128,7 +149,7 @@ def cpu_baseline(torch, M, K, N, sample_rows=1024):
         "sample": (f"reference CPU path (torch ops, bf16 F.linear) on x[{sample_rows},{K}] x W[{N},{K}]: "
                    f"W qdq {t_w:.2f}s, x qdq {t_x:.3f}s, GEMM {t_g:.3f}s; full-M time extrapolated "
                    f"linearly to M={M}: {t_full:.1f}s"),
-        "cpu_model": platform.processor() or platform.machine(),
+        "cpu_model": _cpu_model(),
     }
 
 
@@ -137,7 +158,7 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--a-format", default="bf16", choices=["bf16", "codes"])
+    ap.add_argument("--a-format", default="bf16", choices=["tiled", "bf16", "codes"])
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--shapes", default="up", help="comma list of up,down,qkvo to time in addition")
     args = ap.parse_args()
@@ -260,12 +281,12 @@ def main():
         "data": "synthetic",
         "config": {
             "workload": ("Wan-14B 720P FFN-up HIF8Linear forward: x[75600,5120] bf16 -> amax+scale -> "
-                         f"{'encode' if args.a_format == 'codes' else 'fake-quant'} -> fused HiF8 dequant-GEMM "
+                         f"{'encode' if args.a_format == 'codes' else 'fake-quant'} ({args.a_format}) -> fused HiF8 dequant-GEMM "
                          "(W[13824,5120] packed 8-bit HiF8, bias) -> y bf16"),
             "M": M, "K": K, "N": N, "a_format": args.a_format, "scale_max": 15.0,
         },
         "roofline": {
-            "kernel": "k_linear (fused HiF8 dequant-GEMM)",
+            "kernel": "k_linear_tiled" if args.a_format == "tiled" else "k_linear",
             "bound": "mfma",
             "achieved": round(gemm_tflops, 2),
             "peak": PEAK_BF16_TFLOPS,

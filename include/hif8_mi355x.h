@@ -123,6 +123,38 @@ int hif8_linear_fwd(const void *a, int a_fmt, const void *a_state, const uint8_t
                     const void *w_state, const uint16_t *bias, uint16_t *y, int64_t M,
                     int64_t N, int64_t K, hif8_stream_t stream);
 
+/* ---------------------------------------------------------------------------
+ * GEMM-native operand layouts and the tiled fused linear (the fast path of
+ * hif8_linear.py:68-86).
+ *
+ * XT (activation x_q, bf16): blocks of 32 rows x 64 k, 4 KB each; block
+ *   (rb, ks) at byte (rb*K/64 + ks)*4096; its 1 KB sub-block kk holds at byte
+ *   16*l the eight values x_q[32rb + l%32][64ks + 16kk + 8(l/32) + 0..7].
+ *   Rows are padded with zeros to hif8_tiled_rows(M).
+ * WT (weight codes): the same blocking over [N,K] with one byte per code
+ *   (2 KB blocks, 512 B sub-blocks, 8 codes per lane); rows padded with code 0
+ *   to hif8_tiled_rows(N).
+ */
+
+/* Row count of a tiled buffer: rows rounded up to a multiple of 256. */
+int64_t hif8_tiled_rows(int64_t rows);
+
+/* Fake quant of a row-major [M,K] tensor (scale from state) written as bf16
+ * GEMM operands in the XT layout: the x_q of hif8_linear.py:47-48 (for fp32 x,
+ * its bf16 autocast rounding).  xt: hif8_tiled_rows(M)*K bf16.  K % 64 == 0. */
+int hif8_fake_quant_tiled(const void *x, int dtype, int64_t M, int64_t K, const void *state, uint16_t *xt,
+                          int semantics, hif8_stream_t stream);
+
+/* Permute row-major [N,K] weight codes into the WT layout (packed 8-bit weight
+ * storage of the fused GEMM).  wt: hif8_tiled_rows(N)*K bytes.  K % 64 == 0. */
+int hif8_tile_weight_codes(const uint8_t *codes, int64_t N, int64_t K, uint8_t *wt, hif8_stream_t stream);
+
+/* Fused HiF8 linear on the tiled layouts: y[M,N] = x_q @ w_q^T + bias
+ * (hif8_linear.py:86), bf16 MFMA, fp32 accumulation, bf16 output, row-major y.
+ * K % 64 == 0, N % 8 == 0; 16-byte aligned xt, wt, y. */
+int hif8_linear_fwd_tiled(const uint16_t *xt, const uint8_t *wt, const void *w_state, const uint16_t *bias,
+                          uint16_t *y, int64_t M, int64_t N, int64_t K, hif8_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -22,13 +22,18 @@ from .hif8_linear import (  # noqa: F401
     decode,
     encode,
     fake_quant,
+    fake_quant_tiled,
     linear_fwd,
+    linear_fwd_tiled,
     make_linear,
     quantize_activation,
+    tile_weight_codes,
+    tiled_rows,
 )
 
 __all__ = [
     "QType", "quant_dequant_float", "quant_func", "hif8_quant", "hif8_quant_bf16",
     "HIF8Linear", "PackedWeight", "QuantState", "_quant", "absmax_scale", "decode", "encode",
-    "fake_quant", "linear_fwd", "make_linear", "quantize_activation",
+    "fake_quant", "linear_fwd", "make_linear", "quantize_activation", "fake_quant_tiled",
+    "tile_weight_codes", "tiled_rows", "linear_fwd_tiled",
 ]

@@ -34,6 +34,10 @@ SIGNATURES = {
     "hif8_quant_f32": (_i, [_p, _p, _i64, _i, _p]),
     "hif8_quant_bf16": (_i, [_p, _p, _i64, _i, _p]),
     "hif8_linear_fwd": (_i, [_p, _i, _p, _p, _p, _p, _p, _i64, _i64, _i64, _p]),
+    "hif8_tiled_rows": (_i64, [_i64]),
+    "hif8_fake_quant_tiled": (_i, [_p, _i, _i64, _i64, _p, _p, _i, _p]),
+    "hif8_tile_weight_codes": (_i, [_p, _i64, _i64, _p, _p]),
+    "hif8_linear_fwd_tiled": (_i, [_p, _p, _p, _p, _p, _i64, _i64, _i64, _p]),
 }
 
 _lib = None

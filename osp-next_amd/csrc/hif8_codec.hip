@@ -163,17 +163,22 @@ __global__ __launch_bounds__(kTPB) void k_absmax(const void *__restrict__ xv, in
         const u32x4 *xq = (const u32x4 *)x;
         u16x2 acc = {0, 0};
         int64_t i = int64_t(blockIdx.x) * kTPB + tid;
-        for (; i + 3 * stride < nvec; i += 4 * stride) {
+        for (; i + 7 * stride < nvec; i += 8 * stride) {
             u32x4 v0 = xq[i];
             u32x4 v1 = xq[i + stride];
             u32x4 v2 = xq[i + 2 * stride];
             u32x4 v3 = xq[i + 3 * stride];
+            u32x4 v4 = xq[i + 4 * stride];
+            u32x4 v5 = xq[i + 5 * stride];
+            u32x4 v6 = xq[i + 6 * stride];
+            u32x4 v7 = xq[i + 7 * stride];
 #define HIF8_ACC(v)                                                                          \
     acc = __builtin_elementwise_max(acc, __builtin_bit_cast(u16x2, (v).x & 0x7FFF7FFFu));   \
     acc = __builtin_elementwise_max(acc, __builtin_bit_cast(u16x2, (v).y & 0x7FFF7FFFu));   \
     acc = __builtin_elementwise_max(acc, __builtin_bit_cast(u16x2, (v).z & 0x7FFF7FFFu));   \
     acc = __builtin_elementwise_max(acc, __builtin_bit_cast(u16x2, (v).w & 0x7FFF7FFFu));
             HIF8_ACC(v0) HIF8_ACC(v1) HIF8_ACC(v2) HIF8_ACC(v3)
+            HIF8_ACC(v4) HIF8_ACC(v5) HIF8_ACC(v6) HIF8_ACC(v7)
         }
         for (; i < nvec; i += stride) {
             u32x4 v0 = xq[i];
@@ -191,11 +196,15 @@ __global__ __launch_bounds__(kTPB) void k_absmax(const void *__restrict__ xv, in
         const u32x4 *xq = (const u32x4 *)x;
         int64_t i = int64_t(blockIdx.x) * kTPB + tid;
         uint32_t m0 = 0, m1 = 0;
-        for (; i + stride < nvec; i += 2 * stride) {
+        for (; i + 3 * stride < nvec; i += 4 * stride) {
             u32x4 v0 = xq[i];
             u32x4 v1 = xq[i + stride];
+            u32x4 v2 = xq[i + 2 * stride];
+            u32x4 v3 = xq[i + 3 * stride];
             m0 = max(m0, max(max(v0.x & 0x7FFFFFFFu, v0.y & 0x7FFFFFFFu), max(v0.z & 0x7FFFFFFFu, v0.w & 0x7FFFFFFFu)));
             m1 = max(m1, max(max(v1.x & 0x7FFFFFFFu, v1.y & 0x7FFFFFFFu), max(v1.z & 0x7FFFFFFFu, v1.w & 0x7FFFFFFFu)));
+            m0 = max(m0, max(max(v2.x & 0x7FFFFFFFu, v2.y & 0x7FFFFFFFu), max(v2.z & 0x7FFFFFFFu, v2.w & 0x7FFFFFFFu)));
+            m1 = max(m1, max(max(v3.x & 0x7FFFFFFFu, v3.y & 0x7FFFFFFFu), max(v3.z & 0x7FFFFFFFu, v3.w & 0x7FFFFFFFu)));
         }
         for (; i < nvec; i += stride) {
             u32x4 v0 = xq[i];
@@ -327,14 +336,27 @@ __global__ __launch_bounds__(kTPB) void k_quant(const void *__restrict__ xv, int
     }
 
     if (fast) {
+        // the next group's input is loaded one iteration ahead (two groups in flight)
+        u32x4 pre[4] = {};
+        if (g < ngrp) {
+            const u32x4 *xq = (const u32x4 *)xv;
+#pragma unroll
+            for (int j = 0; j < (DT == kBF16 ? 2 : 4); ++j) pre[j] = xq[(DT == kBF16 ? 2 : 4) * g + j];
+        }
         for (; g < ngrp; g += stride) {
             uint32_t codes[4];
             uint32_t wide[16];   // per element: magnitude bits of xs, and the full bits for fp32
             uint32_t xs_full[16];
-            if (DT == kBF16) {
+            u32x4 cur[4] = {pre[0], pre[1], pre[2], pre[3]};
+            if (g + stride < ngrp) {
                 const u32x4 *xq = (const u32x4 *)xv;
-                u32x4 a = xq[2 * g];
-                u32x4 b = xq[2 * g + 1];
+#pragma unroll
+                for (int j = 0; j < (DT == kBF16 ? 2 : 4); ++j)
+                    pre[j] = xq[(DT == kBF16 ? 2 : 4) * (g + stride) + j];
+            }
+            if (DT == kBF16) {
+                u32x4 a = cur[0];
+                u32x4 b = cur[1];
                 uint32_t p[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
@@ -352,10 +374,9 @@ __global__ __launch_bounds__(kTPB) void k_quant(const void *__restrict__ xv, int
                     codes[j] = apply_signs(mags, signs);
                 }
             } else {
-                const u32x4 *xq = (const u32x4 *)xv;
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
-                    u32x4 a = xq[4 * g + j];
+                    u32x4 a = cur[j];
                     uint32_t v[4] = {a.x, a.y, a.z, a.w};
                     uint32_t mags = 0;
 #pragma unroll
@@ -442,6 +463,160 @@ __global__ __launch_bounds__(kTPB) void k_quant(const void *__restrict__ xv, int
     }
 }
 
+// ------------------------------------------------ GEMM operand layouts
+
+// Activation tile layout of the fused GEMM ("XT"): blocks of 32 rows x 64 k
+// (4 KB of bf16); block (rb, ks) starts at byte (rb * K/64 + ks) * 4096 and its
+// sub-block kk (1 KB) holds, at byte 16*l, lane l's eight values
+//   X[32 rb + (l & 31)][64 ks + 16 kk + 8 (l >> 5) + 0..7],
+// i.e. the B operand of v_mfma_f32_32x32x16_bf16, so a wavefront fetches one
+// operand with a single fully coalesced 1 KB load.  Rows from M up to the padded
+// row count are zero.
+
+// 8 input elements -> 8 bf16 GEMM operands x_q (4 dwords), table route.
+template <int DT>
+__device__ __forceinline__ void quant8_operand(const uint32_t *in, float s, const uint8_t *lds,
+                                               const uint16_t *lut16, bool nan_guard, int sem,
+                                               uint32_t out[4])
+{
+    uint32_t codes[2], wide[8], full[8];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        uint32_t mags = 0, signs;
+        if (DT == kBF16) {
+            uint32_t p0 = in[2 * j], p1 = in[2 * j + 1];
+            uint32_t q01 = f2bf_pk(u2f(p0 << 16) * s, u2f(p0 & 0xFFFF0000u) * s);
+            uint32_t q23 = f2bf_pk(u2f(p1 << 16) * s, u2f(p1 & 0xFFFF0000u) * s);
+            uint32_t u[4] = {q01 & 0x7FFFu, (q01 >> 16) & 0x7FFFu, q23 & 0x7FFFu, (q23 >> 16) & 0x7FFFu};
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                wide[4 * j + t] = u[t];
+                full[4 * j + t] = u[t];
+                mags |= uint32_t(lds[clampu(u[t])]) << (8 * t);
+            }
+            signs = __builtin_amdgcn_perm(p1, p0, 0x07050301u) & 0x80808080u;
+        } else {
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                uint32_t xs = f2u(u2f(in[4 * j + t]) * s);
+                full[4 * j + t] = xs & 0x7FFFFFFFu;
+                uint32_t u = (xs >> 16) & 0x7FFFu;
+                wide[4 * j + t] = u;
+                mags |= uint32_t(lds[clampu(u)]) << (8 * t);
+            }
+            signs = (__builtin_amdgcn_perm(in[4 * j + 3], in[4 * j + 2], 0x07030C0Cu) & 0x80800000u) |
+                    (__builtin_amdgcn_perm(in[4 * j + 1], in[4 * j], 0x0C0C0703u) & 0x00008080u);
+        }
+        codes[j] = apply_signs(mags, signs);
+    }
+    if (nan_guard) {
+#pragma unroll
+        for (int t = 0; t < 8; ++t)
+            if (wide[t] > 0x7F80u) codes[t >> 2] = (codes[t >> 2] & ~(0xFFu << (8 * (t & 3)))) | (0x80u << (8 * (t & 3)));
+    }
+    uint32_t y[8];
+#pragma unroll
+    for (int t = 0; t < 8; ++t) y[t] = lut16[(codes[t >> 2] >> (8 * (t & 3))) & 0xFFu];
+    if (sem == kSemTorch) {
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+            uint32_t u = wide[t];
+            if ((full[t] != 0u && u < 0x3480u) || u >= 0x4720u) {
+                // the torch route differs here: redo this element exactly
+                uint32_t yb, code;
+                uint32_t xb = DT == kBF16 ? ((t & 1) ? (in[t >> 1] >> 16) : (in[t >> 1] & 0xFFFFu)) : in[t];
+                slow_elem<DT>(xb, s, kSemTorch, yb, code);
+                y[t] = DT == kBF16 ? yb : f2bf(u2f(yb));
+            }
+        }
+    }
+#pragma unroll
+    for (int t = 0; t < 4; ++t) out[t] = y[2 * t] | (y[2 * t + 1] << 16);
+}
+
+template <int DT>
+__global__ __launch_bounds__(kTPB) void k_quant_tiled(const void *__restrict__ xv, int M, int K, int Mpad,
+                                                       const State *__restrict__ st, uint8_t *__restrict__ xt,
+                                                       int sem)
+{
+    __shared__ __attribute__((aligned(16))) uint8_t lds[kLdsBytes];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const float s = st->scale;
+    const bool fast = st->fast != 0;
+    const bool nan_guard = st->finite == 0;
+    ((uint16_t *)(lds + kLdsLutBf16))[tid] = st->lut_bf16[tid];
+    {
+        const uint4 *src = (const uint4 *)&kEncTable;
+        uint4 *dst = (uint4 *)(lds + kTabLo);
+        for (uint32_t i = tid; i < sizeof(EncTable) / 16; i += kTPB) dst[i] = src[i];
+    }
+    __syncthreads();
+    const uint16_t *lut16 = (const uint16_t *)(lds + kLdsLutBf16);
+    const int KS = K >> 6;
+    const int64_t nblk = int64_t(Mpad >> 5) * KS;
+    const int64_t stride = int64_t(gridDim.x) * (kTPB / 64);
+    for (int64_t b = int64_t(blockIdx.x) * (kTPB / 64) + wave; b < nblk; b += stride) {
+        const int rb = int(b / KS), ks = int(b - int64_t(rb) * KS);
+        const int row = rb * 32 + (lane & 31);
+        uint8_t *dst = xt + b * 4096 + lane * 16;
+#pragma unroll
+        for (int kk = 0; kk < 4; ++kk) {
+            const int k = ks * 64 + kk * 16 + 8 * (lane >> 5);
+            uint32_t out[4] = {0, 0, 0, 0};
+            if (row < M) {
+                uint32_t in[8];
+                if (DT == kBF16) {
+                    u32x4 v = *(const u32x4 *)((const uint16_t *)xv + size_t(row) * K + k);
+                    in[0] = v.x; in[1] = v.y; in[2] = v.z; in[3] = v.w;
+                } else {
+                    const u32x4 *p = (const u32x4 *)((const float *)xv + size_t(row) * K + k);
+                    u32x4 v0 = p[0], v1 = p[1];
+                    in[0] = v0.x; in[1] = v0.y; in[2] = v0.z; in[3] = v0.w;
+                    in[4] = v1.x; in[5] = v1.y; in[6] = v1.z; in[7] = v1.w;
+                }
+                if (fast) {
+                    quant8_operand<DT>(in, s, lds, lut16, nan_guard, sem, out);
+                } else {
+                    uint32_t y[8];
+#pragma unroll
+                    for (int t = 0; t < 8; ++t) {
+                        uint32_t xb = DT == kBF16 ? ((t & 1) ? (in[t >> 1] >> 16) : (in[t >> 1] & 0xFFFFu)) : in[t];
+                        uint32_t yb, code;
+                        slow_elem<DT>(xb, s, sem, yb, code);
+                        y[t] = DT == kBF16 ? yb : f2bf(u2f(yb));
+                    }
+#pragma unroll
+                    for (int t = 0; t < 4; ++t) out[t] = y[2 * t] | (y[2 * t + 1] << 16);
+                }
+            }
+            *(u32x4 *)(dst + kk * 1024) = u32x4{out[0], out[1], out[2], out[3]};
+        }
+    }
+}
+
+// Weight code tile layout of the fused GEMM ("WT"): blocks of 32 rows x 64 k
+// (2 KB of codes); block (nb, ks) at byte (nb * K/64 + ks) * 2048; sub-block kk
+// (512 B) holds, at byte 8*l, lane l's eight codes
+//   W[32 nb + (l & 31)][64 ks + 16 kk + 8 (l >> 5) + 0..7]
+// -- the A operand of v_mfma_f32_32x32x16_bf16 once decoded.  Rows from N up to
+// the padded row count hold code 0 (value 0).
+__global__ __launch_bounds__(kTPB) void k_tile_wcodes(const uint8_t *__restrict__ codes, int N, int K, int Npad,
+                                                       uint8_t *__restrict__ wt)
+{
+    const int KS = K >> 6;
+    const int64_t ngrp = int64_t(Npad >> 5) * KS * 256;   // 8-code groups
+    for (int64_t g = int64_t(blockIdx.x) * kTPB + threadIdx.x; g < ngrp; g += int64_t(gridDim.x) * kTPB) {
+        const int lane = int(g & 63), kk = int((g >> 6) & 3);
+        const int64_t blk = g >> 8;
+        const int nb = int(blk / KS), ks = int(blk - int64_t(nb) * KS);
+        const int n = nb * 32 + (lane & 31);
+        const int k = ks * 64 + kk * 16 + 8 * (lane >> 5);
+        uint2 v = make_uint2(0u, 0u);
+        if (n < N) v = *(const uint2 *)(codes + size_t(n) * K + k);
+        *(uint2 *)(wt + g * 8) = v;
+    }
+}
+
 // ---------------------------------------------------------------- launch
 
 static int grid_for(int64_t units, int max_blocks)
@@ -512,7 +687,7 @@ int hif8_absmax_scale(const void *x, int dtype, int64_t n, float scale_max, void
     if (!x || !state || n <= 0 || (dtype != HIF8_DTYPE_BF16 && dtype != HIF8_DTYPE_F32)) return HIF8_ERR_ARG;
     if (!aligned16(x)) return HIF8_ERR_ALIGN;
     const int per_thread_vec = dtype == HIF8_DTYPE_BF16 ? 8 : 4;
-    int grid = grid_for((n + per_thread_vec * 4 - 1) / (per_thread_vec * 4), cu_count() * 8);
+    int grid = grid_for((n + per_thread_vec * 8 - 1) / (per_thread_vec * 8), cu_count() * 2);
     if (dtype == HIF8_DTYPE_BF16)
         hipLaunchKernelGGL(k_absmax<kBF16>, dim3(grid), dim3(kTPB), 0, (hipStream_t)stream, x, n, (State *)state, scale_max);
     else
@@ -576,6 +751,41 @@ int hif8_quant_f32(const float *x, float *y, int64_t n, int semantics, hif8_stre
 int hif8_quant_bf16(const uint16_t *x, uint16_t *y, int64_t n, int semantics, hif8_stream_t stream)
 {
     return launch_quant(x, HIF8_DTYPE_BF16, n, nullptr, y, 1, semantics, 0, stream);
+}
+
+int64_t hif8_tiled_rows(int64_t rows) { return rows <= 0 ? 0 : ((rows + 255) / 256) * 256; }
+
+int hif8_fake_quant_tiled(const void *x, int dtype, int64_t M, int64_t K, const void *state, uint16_t *xt,
+                          int semantics, hif8_stream_t stream)
+{
+    if (!x || !state || !xt || M <= 0 || K <= 0) return HIF8_ERR_ARG;
+    if (dtype != HIF8_DTYPE_BF16 && dtype != HIF8_DTYPE_F32) return HIF8_ERR_ARG;
+    if (semantics != HIF8_SEM_NPU && semantics != HIF8_SEM_TORCH) return HIF8_ERR_ARG;
+    if (K % 64 != 0 || M >= (int64_t(1) << 31) || K >= (int64_t(1) << 31)) return HIF8_ERR_SHAPE;
+    if (!aligned16(x) || !aligned16(xt)) return HIF8_ERR_ALIGN;
+    const int64_t Mpad = hif8_tiled_rows(M);
+    const int64_t blocks = (Mpad / 32) * (K / 64);
+    int grid = grid_for(blocks * 64, cu_count() * 8);
+    hipStream_t s = (hipStream_t)stream;
+    if (dtype == HIF8_DTYPE_BF16)
+        hipLaunchKernelGGL(k_quant_tiled<kBF16>, dim3(grid), dim3(kTPB), 0, s, x, int(M), int(K), int(Mpad),
+                           (const State *)state, (uint8_t *)xt, semantics);
+    else
+        hipLaunchKernelGGL(k_quant_tiled<kF32>, dim3(grid), dim3(kTPB), 0, s, x, int(M), int(K), int(Mpad),
+                           (const State *)state, (uint8_t *)xt, semantics);
+    return last_launch();
+}
+
+int hif8_tile_weight_codes(const uint8_t *codes, int64_t N, int64_t K, uint8_t *wt, hif8_stream_t stream)
+{
+    if (!codes || !wt || N <= 0 || K <= 0) return HIF8_ERR_ARG;
+    if (K % 64 != 0 || N >= (int64_t(1) << 31) || K >= (int64_t(1) << 31)) return HIF8_ERR_SHAPE;
+    if (!aligned16(codes) || !aligned16(wt)) return HIF8_ERR_ALIGN;
+    const int64_t Npad = hif8_tiled_rows(N);
+    int grid = grid_for((Npad / 32) * (K / 64) * 256, cu_count() * 8);
+    hipLaunchKernelGGL(k_tile_wcodes, dim3(grid), dim3(kTPB), 0, (hipStream_t)stream, codes, int(N), int(K),
+                       int(Npad), wt);
+    return last_launch();
 }
 
 }  // extern "C"

@@ -117,22 +117,51 @@ def _quant(x: Tensor, scale_max: float, semantics: int = _lib.SEM_NPU) -> Tuple[
     return xq.view(x.shape), st.scale().to(x.dtype)
 
 
+def tiled_rows(rows: int) -> int:
+    return int(_lib.load().hif8_tiled_rows(rows))
+
+
+def fake_quant_tiled(x2: Tensor, state: QuantState, semantics: int = _lib.SEM_NPU) -> Tensor:
+    """x_q of a row-major [M, K] tensor as bf16 GEMM operands in the XT tile layout
+    (flat bf16 buffer of tiled_rows(M) * K elements)."""
+    _lib.require_gpu_tensor(x2, "x")
+    x2 = _aligned(x2)
+    M, K = x2.shape
+    xt = torch.empty(tiled_rows(M) * K, dtype=torch.bfloat16, device=x2.device)
+    _lib.check(_lib.load().hif8_fake_quant_tiled(x2.data_ptr(), _lib.dtype_code(x2.dtype), M, K, state.ptr,
+                                                 xt.data_ptr(), semantics, _lib.stream_ptr(x2.device)),
+               "hif8_fake_quant_tiled")
+    return xt
+
+
+def tile_weight_codes(codes: Tensor) -> Tensor:
+    """Row-major [N, K] codes -> WT tile layout (flat uint8, tiled_rows(N) * K)."""
+    _lib.require_gpu_tensor(codes, "codes")
+    N, K = codes.shape
+    wt = torch.empty(tiled_rows(N) * K, dtype=torch.uint8, device=codes.device)
+    _lib.check(_lib.load().hif8_tile_weight_codes(codes.data_ptr(), N, K, wt.data_ptr(),
+                                                  _lib.stream_ptr(codes.device)), "hif8_tile_weight_codes")
+    return wt
+
+
 # ------------------------------------------------------------ packed weight
 
 
 class PackedWeight:
-    """8-bit HiF8 weight storage: codes [N, K] (uint8) + the weight's state.
+    """8-bit HiF8 weight storage: codes [N, K] (uint8) + the weight's state, and the
+    same codes in the fused GEMM's WT tile layout.
 
     Halves the bytes of a bf16 weight; ``dequantize()`` gives the reference's
     ``w_q`` exactly.
     """
 
-    def __init__(self, weight: Tensor, scale_max: float):
+    def __init__(self, weight: Tensor, scale_max: float, tiled: bool = True):
         w = weight.detach().contiguous()
         self.shape = tuple(w.shape)
         self.src_dtype = w.dtype
         self.state = absmax_scale(w, scale_max, QuantState(w.device))
         self.codes = encode(w, self.state)
+        self.wt = tile_weight_codes(self.codes) if (tiled and w.shape[1] % 64 == 0) else None
         self.scale_max = float(scale_max)
         self.key = (w.data_ptr(), weight._version, w.device)
 
@@ -158,6 +187,21 @@ def linear_fwd(a: Tensor, a_fmt: int, a_state: Optional[QuantState], w: PackedWe
     return y
 
 
+def linear_fwd_tiled(xt: Tensor, M: int, w: PackedWeight, bias: Optional[Tensor]) -> Tensor:
+    """hif8_linear_fwd_tiled: the fused GEMM on XT activations and WT codes."""
+    N, K = w.shape
+    if w.wt is None:
+        raise ValueError("packed weight has no tiled codes (K % 64 != 0)")
+    y = torch.empty((M, N), dtype=torch.bfloat16, device=xt.device)
+    b_ptr = None
+    if bias is not None:
+        bias = bias.detach().to(torch.bfloat16).contiguous()
+        b_ptr = bias.data_ptr()
+    _lib.check(_lib.load().hif8_linear_fwd_tiled(xt.data_ptr(), w.wt.data_ptr(), w.state.ptr, b_ptr, y.data_ptr(),
+                                                 M, N, K, _lib.stream_ptr(xt.device)), "hif8_linear_fwd_tiled")
+    return y
+
+
 def quantize_activation(x2: Tensor, scale_max: float, a_format: str):
     """Quantise a [M,K] activation for the fused GEMM: returns (a, a_fmt, state)."""
     st = absmax_scale(x2, scale_max, QuantState(x2.device))
@@ -167,6 +211,24 @@ def quantize_activation(x2: Tensor, scale_max: float, a_format: str):
 
 
 # --------------------------------------------------------------- autograd
+
+
+def hif8_linear_inference(x: Tensor, packed: PackedWeight, bias: Optional[Tensor],
+                          scale_max_forward: float = 15.0) -> Tensor:
+    """Forward without autograd on the tiled fast path: amax+scale, fake quant into
+    the GEMM operand layout, fused dequant-GEMM (three kernels)."""
+    if x.dtype not in (torch.bfloat16, torch.float32):
+        raise TypeError(f"HIF8Linear takes bfloat16 or float32 input, got {x.dtype}")
+    K = x.shape[-1]
+    x2 = x.reshape(-1, K).contiguous()
+    if packed.wt is None or packed.shape[0] % 8 != 0:
+        a, a_fmt, a_st = quantize_activation(x2, scale_max_forward, "bf16")
+        y = linear_fwd(a, a_fmt, a_st, packed, bias)
+    else:
+        st = absmax_scale(x2, scale_max_forward, QuantState(x2.device))
+        xt = fake_quant_tiled(x2, st)
+        y = linear_fwd_tiled(xt, x2.shape[0], packed, bias)
+    return y.view(*x.shape[:-1], y.shape[-1])
 
 
 class _HIF8LinearFunction(torch.autograd.Function):
@@ -181,9 +243,10 @@ class _HIF8LinearFunction(torch.autograd.Function):
         x2 = x.reshape(-1, K).contiguous()
         if packed is None:
             packed = PackedWeight(weight, scale_max_forward)
-        a, a_fmt, a_st = quantize_activation(x2, scale_max_forward, a_format)
+        needs_grad = any(ctx.needs_input_grad[:3])
+        a, a_fmt, a_st = quantize_activation(x2, scale_max_forward, "codes" if a_format == "codes" else "bf16")
         y = linear_fwd(a, a_fmt, a_st, packed, bias)
-        if any(ctx.needs_input_grad[:3]):
+        if needs_grad:
             ctx.a, ctx.a_fmt, ctx.a_st, ctx.packed = a, a_fmt, a_st, packed
             ctx.x_dtype, ctx.w_dtype = x.dtype, weight.dtype
             ctx.x_shape = x.shape
@@ -221,8 +284,10 @@ class HIF8Linear(nn.Linear):
         (inference); without it the packed weight is rebuilt whenever the weight
         tensor changes (version counter or storage), which matches the
         reference's per-call re-quantisation.
-      * ``a_format`` = ``"bf16"`` (activation fake-quantised to bf16 x_q) or
-        ``"codes"`` (activation encoded to 8-bit codes and decoded in the GEMM).
+      * ``a_format`` = ``"bf16"`` (default: row-major bf16 x_q and the row-major
+        fused GEMM), ``"tiled"`` (x_q written straight into the tiled GEMM's
+        operand layout, used when no gradient is needed) or ``"codes"`` (8-bit
+        activation codes decoded in the GEMM).
     """
 
     def __init__(self, in_features: int, out_features: int, bias: bool = True,
@@ -257,6 +322,10 @@ class HIF8Linear(nn.Linear):
 
     def forward(self, x: Tensor) -> Tensor:
         packed = self._packed_weight()
+        grad = torch.is_grad_enabled() and (x.requires_grad or self.weight.requires_grad
+                                            or (self.bias is not None and self.bias.requires_grad))
+        if not grad and self.a_format == "tiled":
+            return hif8_linear_inference(x, packed, self.bias, self.scale_max_forward)
         return _HIF8LinearFunction.apply(x, self.weight, self.bias, self.scale_max_forward,
                                          self.scale_max_backward, packed, self.a_format)
 
