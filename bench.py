@@ -286,7 +286,7 @@ def main():
             "M": M, "K": K, "N": N, "a_format": args.a_format, "scale_max": 15.0,
         },
         "roofline": {
-            "kernel": "k_linear_tiled" if args.a_format == "tiled" else "k_linear",
+            "kernel": {"tiled": "k_linear_tiled", "codes": "k_linear", "bf16": "k_linear_dtl"}[args.a_format],
             "bound": "mfma",
             "achieved": round(gemm_tflops, 2),
             "peak": PEAK_BF16_TFLOPS,

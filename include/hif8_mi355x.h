@@ -116,8 +116,8 @@ int hif8_quant_bf16(const uint16_t *x, uint16_t *y, int64_t n, int semantics,
  * bf16).  bf16 MFMA, fp32 accumulation, bias added in fp32, bf16 output (RNE).
  *   a: [M,K] row-major; w_codes: [N,K] row-major bytes; bias: [N] bf16 or NULL;
  *   y: [M,N] row-major bf16.
- * Shapes: K % 64 == 0, N % 8 == 0; M, N, K >= 1 and < 2^31.  16-byte aligned
- * a, w_codes and y.
+ * Shapes: K % 64 == 0, N % 8 == 0; M, N, K >= 1 and < 2^31, and K < 2^22 for
+ * bf16 activations.  16-byte aligned a, w_codes and y; 8-byte aligned bias.
  */
 int hif8_linear_fwd(const void *a, int a_fmt, const void *a_state, const uint8_t *w_codes,
                     const void *w_state, const uint16_t *bias, uint16_t *y, int64_t M,

@@ -1,7 +1,9 @@
 // Fused HiF8 dequant-GEMM for MI355X (gfx950):
 //   Y[M,N] = X_q[M,K] . W_q[N,K]^T + bias[N]
 // the F.linear(x_q, w_q, bias) of ospnext/modules/hif8_linear.py:86, with W
-// stored as packed 8-bit HiF8 codes.
+// stored as packed 8-bit HiF8 codes.  hif8_linear_fwd runs bf16 activations on
+// k_linear_dtl (hif8_gemm_dtl.hip); this kernel serves activations given as
+// HiF8 codes (HIF8_A_CODES), which it decodes like W.
 //
 // Design
 //   - Workgroup tile 256 (m) x 256 (n) x 64 (k), 512 threads = 8 waves, two per
@@ -251,9 +253,7 @@ extern "C" int hif8_linear_fwd(const void *a, int a_fmt, const void *a_state, co
     if (tiles >= (int64_t(1) << 31)) return HIF8_ERR_SHAPE;
     hipStream_t s = (hipStream_t)stream;
     if (a_fmt == HIF8_A_BF16)
-        hipLaunchKernelGGL(k_linear<HIF8_A_BF16>, dim3(unsigned(tiles)), dim3(kThreads), 0, s, a,
-                           (const State *)a_state, w_codes, (const State *)w_state, bias, y, int(M), int(N),
-                           int(K), tiles_m, tiles_n);
+        return launch_linear_dtl((const uint16_t *)a, w_codes, (const State *)w_state, bias, y, M, N, K, stream);
     else
         hipLaunchKernelGGL(k_linear<HIF8_A_CODES>, dim3(unsigned(tiles)), dim3(kThreads), 0, s, a,
                            (const State *)a_state, w_codes, (const State *)w_state, bias, y, int(M), int(N),

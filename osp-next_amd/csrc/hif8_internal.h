@@ -28,4 +28,9 @@ struct alignas(256) State {
 
 static_assert(sizeof(State) % 256 == 0, "state size");
 
+// Fused GEMM for bf16 activations (hif8_gemm_dtl.hip); the caller has checked shapes and
+// alignment as hif8_linear_fwd documents.
+int launch_linear_dtl(const uint16_t *x, const uint8_t *w_codes, const State *w_st, const uint16_t *bias,
+                      uint16_t *y, int64_t M, int64_t N, int64_t K, hif8_stream_t stream);
+
 }  // namespace hif8

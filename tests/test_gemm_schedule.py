@@ -1,0 +1,79 @@
+"""CPU checks of the fused GEMM's generated main loop (hif8_gemm_dtl.hip).
+
+- hif8_gemm_schedule.inc is what gen_gemm_schedule.py generates;
+- compiled for gfx950, the kernel spills nothing, uses the full 160 KB LDS array, and its
+  main loop passes the in-flight-register and VALU->MFMA checks of isa_check.py with the
+  expected instruction census (128 MFMA, 200 LDS loads, 24 global->LDS loads per 2 k-steps).
+"""
+import importlib.util
+import os
+import re
+import shutil
+import subprocess
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+CSRC = os.path.join(ROOT, "osp-next_amd", "csrc")
+HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+
+
+def test_schedule_include_is_generated():
+    spec = importlib.util.spec_from_file_location("gen_gemm_schedule", os.path.join(CSRC, "gen_gemm_schedule.py"))
+    gen = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(gen)
+    with open(os.path.join(CSRC, "hif8_gemm_schedule.inc")) as f:
+        assert f.read() == gen.generate()
+
+
+@pytest.fixture(scope="module")
+def dtl_asm(tmp_path_factory):
+    if not os.path.exists(HIPCC):
+        pytest.skip("hipcc not available")
+    out = tmp_path_factory.mktemp("isa") / "dtl.s"
+    cmd = [HIPCC, "-O3", "-std=c++17", "--offload-arch=gfx950", "-Xclang", "-target-feature", "-Xclang",
+           "-packed-fp32-ops", "--cuda-device-only", "-S", os.path.join(CSRC, "hif8_gemm_dtl.hip"), "-o", str(out),
+           "-Rpass-analysis=kernel-resource-usage"]
+    r = subprocess.run(cmd, capture_output=True, text=True, timeout=600)
+    assert r.returncode == 0, r.stderr[-2000:]
+    return out.read_text(), r.stderr
+
+
+def test_resources(dtl_asm):
+    _, remarks = dtl_asm
+    assert re.search(r"VGPRs Spill: 0", remarks)
+    assert re.search(r"SGPRs Spill: 0", remarks)
+    assert re.search(r"LDS Size \[bytes/block\]: 163840", remarks)
+    assert "ScratchSize [bytes/lane]: 0" in remarks
+
+
+def test_main_loop_hazards(dtl_asm):
+    import isa_check
+    body = isa_check.mfma_loop(dtl_asm[0])
+    kinds = isa_check.census(body)
+    assert kinds.get("mfma") == 128 and kinds.get("lds_load") == 200 and kinds.get("lds_dma") == 24, kinds
+    errors = isa_check.check_body(body)
+    assert not errors, "\n".join(errors[:20])
+
+
+def test_checker_catches_planted_mistakes():
+    """The checker must flag a read of an in-flight LDS load and a VALU->MFMA gap of 1."""
+    import isa_check
+    body = isa_check.parse([
+        "ds_read_b128 v[4:7], v1 offset:0",
+        "v_mfma_f32_32x32x16_bf16 a[0:15], v[4:7], v[8:11], a[0:15]",
+        "s_waitcnt lgkmcnt(0)",
+        "v_perm_b32 v12, v2, v3, s0",
+        "v_mfma_f32_32x32x16_bf16 a[16:31], v[12:15], v[8:11], a[16:31]",
+    ])
+    errs = isa_check.check_body(body)
+    assert any("in flight" in e for e in errs)
+    assert any("after a VALU write" in e for e in errs)
+    ok = isa_check.parse([
+        "ds_read_b128 v[4:7], v1 offset:0",
+        "s_waitcnt lgkmcnt(0)",
+        "v_perm_b32 v12, v2, v3, s0",
+        "s_nop 2",
+        "v_mfma_f32_32x32x16_bf16 a[0:15], v[4:7], v[12:15], a[0:15]",
+    ])
+    assert not isa_check.check_body(ok)

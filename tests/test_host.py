@@ -70,6 +70,7 @@ def test_status_codes_without_gpu(pkg):
     assert lin(N=100) == -2
     assert lin(y=odd) == -3
     assert lin(b=fake + 2) == -3
+    assert lin(K=1 << 22) == -2          # bf16 activations: K < 2^22 (32-bit buffer offsets)
 
 
 def test_python_layer_refuses_cpu_tensors(pkg):
