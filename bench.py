@@ -100,6 +100,23 @@ def time_linear(pkg, torch, x, packed, b, steps, warmup, a_format):
             "quant": [e[1].elapsed_time(e[2]) for e in ev], "gemm": [e[2].elapsed_time(e[3]) for e in ev], "y": y}
 
 
+TRAFFIC_DOC = os.path.join(ROOT, "profiles", "hif8_kernels_14b_720p_hbm_traffic.md")
+
+
+def measured_traffic(kernel: str):
+    """HBM-side bytes per launch of `kernel` at the 14B FFN-up shape, as recorded from the two
+    rocprofv3 PMC passes (FETCH_SIZE, WRITE_SIZE) whose commands and calibration the summary
+    file gives; None if the summary has no figure for it."""
+    try:
+        with open(TRAFFIC_DOC) as f:
+            for line in f:
+                if line.startswith(f"traffic_bytes_per_launch {kernel}:"):
+                    return int(line.split(":")[1])
+    except OSError:
+        pass
+    return None
+
+
 def median(v):
     s = sorted(v)
     return s[len(s) // 2]
@@ -161,6 +178,9 @@ def main():
     ap.add_argument("--a-format", default="bf16", choices=["tiled", "bf16", "codes"])
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--shapes", default="up", help="comma list of up,down,qkvo to time in addition")
+    ap.add_argument("--pmc-calibration", action="store_true",
+                    help="also run one plain copy of x (774,144,000 B read + written): the reference "
+                         "kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py: this build targets one GPU (no collectives); run with --gpus 1", file=sys.stderr)
@@ -177,6 +197,11 @@ def main():
     log(f"[bench] inputs M={M} K={K} N={N}")
     x, w, b = make_inputs(torch, M, K, N)
     packed = pkg.PackedWeight(w, 15.0)
+    if args.pmc_calibration:
+        xc = torch.empty_like(x)
+        xc.copy_(x)
+        torch.cuda.synchronize()
+        del xc
     torch.cuda.synchronize()
     log("[bench] timing FFN-up step")
     r = time_linear(pkg, torch, x, packed, b, args.steps, args.warmup, args.a_format)
@@ -266,6 +291,7 @@ def main():
         except Exception as ex:
             cpu = {"error": str(ex)}
 
+    kernel_name = {"tiled": "k_linear_tiled", "codes": "k_linear", "bf16": "k_linear_dtl"}[args.a_format]
     out = {
         "metric": METRIC,
         "value": round(value, 2),
@@ -286,13 +312,14 @@ def main():
             "M": M, "K": K, "N": N, "a_format": args.a_format, "scale_max": 15.0,
         },
         "roofline": {
-            "kernel": {"tiled": "k_linear_tiled", "codes": "k_linear", "bf16": "k_linear_dtl"}[args.a_format],
+            "kernel": kernel_name,
             "bound": "mfma",
             "achieved": round(gemm_tflops, 2),
             "peak": PEAK_BF16_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(gemm_tflops / PEAK_BF16_TFLOPS, 4),
-            "traffic": None,
+            "traffic": measured_traffic(kernel_name) if args.a_format == "bf16" else None,
+            "traffic_source": "profiles/hif8_kernels_14b_720p_hbm_traffic.md (rocprofv3 FETCH_SIZE x2 + WRITE_SIZE)",
             "gemm_ms": round(gemm_ms, 4),
         },
         "phases_ms": {"amax": round(amax_ms, 4), "quant": round(quant_ms, 4), "gemm": round(gemm_ms, 4),

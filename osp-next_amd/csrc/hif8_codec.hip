@@ -147,6 +147,19 @@ __global__ __launch_bounds__(256) void k_set_scale(State *st, int dtype, float s
 
 constexpr int kTPB = 256;
 
+// Streaming access: the codec reads each input element once, so its global loads carry
+// the non-temporal hint (measured on the 774 MB 14B activation: amax 4.98 -> 6.5 TB/s).
+// Code output (1 B/element) is stored the same way; bf16/fp32 qdq output is stored
+// normally, which measured faster for it.
+template <typename T> __device__ __forceinline__ T ld_stream(const T *p)
+{
+    return __builtin_nontemporal_load(p);
+}
+template <typename T> __device__ __forceinline__ void st_stream(T *p, const T &v)
+{
+    __builtin_nontemporal_store(v, p);
+}
+
 // One pass of |x| max.  Magnitude bit patterns order like the values and put
 // NaN above Inf, so an unsigned max propagates NaN as torch's amax does.
 template <int DT>
@@ -164,14 +177,14 @@ __global__ __launch_bounds__(kTPB) void k_absmax(const void *__restrict__ xv, in
         u16x2 acc = {0, 0};
         int64_t i = int64_t(blockIdx.x) * kTPB + tid;
         for (; i + 7 * stride < nvec; i += 8 * stride) {
-            u32x4 v0 = xq[i];
-            u32x4 v1 = xq[i + stride];
-            u32x4 v2 = xq[i + 2 * stride];
-            u32x4 v3 = xq[i + 3 * stride];
-            u32x4 v4 = xq[i + 4 * stride];
-            u32x4 v5 = xq[i + 5 * stride];
-            u32x4 v6 = xq[i + 6 * stride];
-            u32x4 v7 = xq[i + 7 * stride];
+            u32x4 v0 = ld_stream(&xq[i]);
+            u32x4 v1 = ld_stream(&xq[i + stride]);
+            u32x4 v2 = ld_stream(&xq[i + 2 * stride]);
+            u32x4 v3 = ld_stream(&xq[i + 3 * stride]);
+            u32x4 v4 = ld_stream(&xq[i + 4 * stride]);
+            u32x4 v5 = ld_stream(&xq[i + 5 * stride]);
+            u32x4 v6 = ld_stream(&xq[i + 6 * stride]);
+            u32x4 v7 = ld_stream(&xq[i + 7 * stride]);
 #define HIF8_ACC(v)                                                                          \
     acc = __builtin_elementwise_max(acc, __builtin_bit_cast(u16x2, (v).x & 0x7FFF7FFFu));   \
     acc = __builtin_elementwise_max(acc, __builtin_bit_cast(u16x2, (v).y & 0x7FFF7FFFu));   \
@@ -197,10 +210,10 @@ __global__ __launch_bounds__(kTPB) void k_absmax(const void *__restrict__ xv, in
         int64_t i = int64_t(blockIdx.x) * kTPB + tid;
         uint32_t m0 = 0, m1 = 0;
         for (; i + 3 * stride < nvec; i += 4 * stride) {
-            u32x4 v0 = xq[i];
-            u32x4 v1 = xq[i + stride];
-            u32x4 v2 = xq[i + 2 * stride];
-            u32x4 v3 = xq[i + 3 * stride];
+            u32x4 v0 = ld_stream(&xq[i]);
+            u32x4 v1 = ld_stream(&xq[i + stride]);
+            u32x4 v2 = ld_stream(&xq[i + 2 * stride]);
+            u32x4 v3 = ld_stream(&xq[i + 3 * stride]);
             m0 = max(m0, max(max(v0.x & 0x7FFFFFFFu, v0.y & 0x7FFFFFFFu), max(v0.z & 0x7FFFFFFFu, v0.w & 0x7FFFFFFFu)));
             m1 = max(m1, max(max(v1.x & 0x7FFFFFFFu, v1.y & 0x7FFFFFFFu), max(v1.z & 0x7FFFFFFFu, v1.w & 0x7FFFFFFFu)));
             m0 = max(m0, max(max(v2.x & 0x7FFFFFFFu, v2.y & 0x7FFFFFFFu), max(v2.z & 0x7FFFFFFFu, v2.w & 0x7FFFFFFFu)));
@@ -341,7 +354,7 @@ __global__ __launch_bounds__(kTPB) void k_quant(const void *__restrict__ xv, int
         if (g < ngrp) {
             const u32x4 *xq = (const u32x4 *)xv;
 #pragma unroll
-            for (int j = 0; j < (DT == kBF16 ? 2 : 4); ++j) pre[j] = xq[(DT == kBF16 ? 2 : 4) * g + j];
+            for (int j = 0; j < (DT == kBF16 ? 2 : 4); ++j) pre[j] = ld_stream(&xq[(DT == kBF16 ? 2 : 4) * g + j]);
         }
         for (; g < ngrp; g += stride) {
             uint32_t codes[4];
@@ -352,7 +365,7 @@ __global__ __launch_bounds__(kTPB) void k_quant(const void *__restrict__ xv, int
                 const u32x4 *xq = (const u32x4 *)xv;
 #pragma unroll
                 for (int j = 0; j < (DT == kBF16 ? 2 : 4); ++j)
-                    pre[j] = xq[(DT == kBF16 ? 2 : 4) * (g + stride) + j];
+                    pre[j] = ld_stream(&xq[(DT == kBF16 ? 2 : 4) * (g + stride) + j]);
             }
             if (DT == kBF16) {
                 u32x4 a = cur[0];
@@ -403,7 +416,7 @@ __global__ __launch_bounds__(kTPB) void k_quant(const void *__restrict__ xv, int
                 }
             }
             if (MODE == 0) {
-                ((uint4 *)outv)[g] = make_uint4(codes[0], codes[1], codes[2], codes[3]);
+                st_stream(&((u32x4 *)outv)[g], u32x4{codes[0], codes[1], codes[2], codes[3]});
                 continue;
             }
             // qdq output through the decode table
@@ -432,13 +445,13 @@ __global__ __launch_bounds__(kTPB) void k_quant(const void *__restrict__ xv, int
                 }
             }
             if (DT == kBF16) {
-                uint4 *out = (uint4 *)outv;
-                out[2 * g] = make_uint4(y[0] | (y[1] << 16), y[2] | (y[3] << 16), y[4] | (y[5] << 16), y[6] | (y[7] << 16));
-                out[2 * g + 1] = make_uint4(y[8] | (y[9] << 16), y[10] | (y[11] << 16), y[12] | (y[13] << 16), y[14] | (y[15] << 16));
+                u32x4 *out = (u32x4 *)outv;
+                out[2 * g] = u32x4{y[0] | (y[1] << 16), y[2] | (y[3] << 16), y[4] | (y[5] << 16), y[6] | (y[7] << 16)};
+                out[2 * g + 1] = u32x4{y[8] | (y[9] << 16), y[10] | (y[11] << 16), y[12] | (y[13] << 16), y[14] | (y[15] << 16)};
             } else {
-                uint4 *out = (uint4 *)outv;
+                u32x4 *out = (u32x4 *)outv;
 #pragma unroll
-                for (int j = 0; j < 4; ++j) out[4 * g + j] = make_uint4(y[4 * j], y[4 * j + 1], y[4 * j + 2], y[4 * j + 3]);
+                for (int j = 0; j < 4; ++j) out[4 * g + j] = u32x4{y[4 * j], y[4 * j + 1], y[4 * j + 2], y[4 * j + 3]};
             }
         }
     } else {
@@ -619,6 +632,12 @@ __global__ __launch_bounds__(kTPB) void k_tile_wcodes(const uint8_t *__restrict_
 
 // ---------------------------------------------------------------- launch
 
+// Workgroups per CU (measured on the 14B activation): amax streams best with one
+// (4 waves per CU, 8 x 16 B loads in flight per lane); encode with 4, qdq with 8.
+constexpr int kAmaxWgPerCu = 1;
+constexpr int kEncodeWgPerCu = 4;
+constexpr int kQdqWgPerCu = 8;
+
 static int grid_for(int64_t units, int max_blocks)
 {
     int64_t b = (units + kTPB - 1) / kTPB;
@@ -687,7 +706,7 @@ int hif8_absmax_scale(const void *x, int dtype, int64_t n, float scale_max, void
     if (!x || !state || n <= 0 || (dtype != HIF8_DTYPE_BF16 && dtype != HIF8_DTYPE_F32)) return HIF8_ERR_ARG;
     if (!aligned16(x)) return HIF8_ERR_ALIGN;
     const int per_thread_vec = dtype == HIF8_DTYPE_BF16 ? 8 : 4;
-    int grid = grid_for((n + per_thread_vec * 8 - 1) / (per_thread_vec * 8), cu_count() * 2);
+    int grid = grid_for((n + per_thread_vec * 8 - 1) / (per_thread_vec * 8), cu_count() * kAmaxWgPerCu);
     if (dtype == HIF8_DTYPE_BF16)
         hipLaunchKernelGGL(k_absmax<kBF16>, dim3(grid), dim3(kTPB), 0, (hipStream_t)stream, x, n, (State *)state, scale_max);
     else
@@ -709,7 +728,7 @@ static int launch_quant(const void *x, int dtype, int64_t n, const void *state, 
     if (dtype != HIF8_DTYPE_BF16 && dtype != HIF8_DTYPE_F32) return HIF8_ERR_ARG;
     if (sem != HIF8_SEM_NPU && sem != HIF8_SEM_TORCH) return HIF8_ERR_ARG;
     if (!aligned16(x) || !aligned16(out)) return HIF8_ERR_ALIGN;
-    int grid = grid_for((n + 15) / 16, cu_count() * 8);
+    int grid = grid_for((n + 15) / 16, cu_count() * (mode == 0 ? kEncodeWgPerCu : kQdqWgPerCu));
     hipStream_t s = (hipStream_t)stream;
     const State *st = (const State *)state;
 #define HIF8_LAUNCH(DT, MODE) \
