@@ -5,7 +5,8 @@ schedule.  The compiler cannot see the latency of asm LDS loads, so two rules ar
 over three passes of the loop body (the state carries across the back edge):
   - no instruction reads or overwrites a register that an LDS load still in flight will
     write (LDS loads complete in issue order: s_waitcnt lgkmcnt(n) retires all but the n
-    most recent);
+    most recent).  A d16 load that preserves half of its destination reads that register
+    at issue, so a d16 merge into a register with a load still in flight is flagged too;
   - an MFMA does not read a register written by a VALU instruction fewer than 3 wait states
     earlier (s_nop n counts n+1).
 """
@@ -87,7 +88,9 @@ def check_body(body, passes=3):
             pend = set().union(*lds_q) if lds_q else set()
             vpend = set().union(*vm_q) if vm_q else set()
             if kind == 'lds_load':
-                bad = ((src - dst) & pend) | (dst & vpend)
+                # a plain load may be issued over a register an older LDS load still writes
+                # (in-order completion); a d16 merge reads its destination at issue
+                bad = (src & pend) | (dst & vpend)
             else:
                 bad = (src | dst) & (pend | vpend)
             if bad and p > 0:

@@ -69,6 +69,11 @@ def test_checker_catches_planted_mistakes():
     errs = isa_check.check_body(body)
     assert any("in flight" in e for e in errs)
     assert any("after a VALU write" in e for e in errs)
+    merge = isa_check.parse([
+        "ds_read_u16 v20, v1 offset:0",
+        "ds_read_u16_d16_hi v20, v2 offset:0",
+    ])
+    assert any("in flight" in e for e in isa_check.check_body(merge))
     ok = isa_check.parse([
         "ds_read_b128 v[4:7], v1 offset:0",
         "s_waitcnt lgkmcnt(0)",
