@@ -155,6 +155,16 @@ int hif8_tile_weight_codes(const uint8_t *codes, int64_t N, int64_t K, uint8_t *
 int hif8_linear_fwd_tiled(const uint16_t *xt, const uint8_t *wt, const void *w_state, const uint16_t *bias,
                           uint16_t *y, int64_t M, int64_t N, int64_t K, hif8_stream_t stream);
 
+/* ---------------------------------------------------------------------------
+ * Backward support.  The reference's dgrad is grad_q @ w_q (hif8_linear.py:97), a
+ * product with the weight's [out, in] rows as the reduction dimension.  The fused
+ * GEMM reduces over its weight operand's rows, so dgrad runs hif8_linear_fwd on
+ * grad_q (bf16 [M, out]) and the transposed codes [in, out] with the weight's state.
+ * This entry point has no reference counterpart (the reference never holds codes):
+ * it writes out[c][r] = codes[r][c] for a [rows, cols] byte matrix.
+ */
+int hif8_transpose_codes(const uint8_t *codes, int64_t rows, int64_t cols, uint8_t *out, hif8_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

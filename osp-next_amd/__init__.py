@@ -7,6 +7,8 @@ Public surface, mirroring the reference:
   QType, quant_dequant_float, quant_func            (ospnext/quant_cy_npu/base/QTensor.py)
   hif8_quant, hif8_quant_bf16                       (cusrc/npu_quant.cpp pybind entry points)
   HIF8Linear, _quant, make_linear                   (ospnext/modules/hif8_linear.py, osp_next.py)
+  hif8_attention_with_mask, _HIF8QKVQuantFunction   (ospnext/modules/hif8_attention.py)
+  QLinear, replace_linear                           (quant_cy_npu/layers/QLinear.py, utils/utils.py)
 plus the tensor-level HIP ops (absmax_scale, encode, fake_quant, decode,
 linear_fwd), QuantState and PackedWeight.
 """
@@ -29,11 +31,33 @@ from .hif8_linear import (  # noqa: F401
     quantize_activation,
     tile_weight_codes,
     tiled_rows,
+    transpose_codes,
+    linear_dgrad,
+    dgrad_fused_ok,
+)
+from .hif8_attention import (  # noqa: F401
+    _HIF8QKVQuantFunction,
+    attention_with_mask,
+    hif8_attention_with_mask,
+    scaled_dot_product_attention_with_mask,
+)
+from .qlinear import (  # noqa: F401
+    LinearForward,
+    LinearForwardFast,
+    QLinear,
+    load_packed,
+    pack_state_dict,
+    packed_from_codes,
+    replace_linear,
+    save_packed,
 )
 
 __all__ = [
     "QType", "quant_dequant_float", "quant_func", "hif8_quant", "hif8_quant_bf16",
     "HIF8Linear", "PackedWeight", "QuantState", "_quant", "absmax_scale", "decode", "encode",
     "fake_quant", "linear_fwd", "make_linear", "quantize_activation", "fake_quant_tiled",
-    "tile_weight_codes", "tiled_rows", "linear_fwd_tiled",
+    "tile_weight_codes", "tiled_rows", "linear_fwd_tiled", "transpose_codes", "linear_dgrad", "dgrad_fused_ok",
+    "_HIF8QKVQuantFunction", "attention_with_mask", "hif8_attention_with_mask",
+    "scaled_dot_product_attention_with_mask", "LinearForward", "LinearForwardFast", "QLinear", "replace_linear",
+    "save_packed", "load_packed", "pack_state_dict", "packed_from_codes",
 ]

@@ -38,6 +38,7 @@ SIGNATURES = {
     "hif8_fake_quant_tiled": (_i, [_p, _i, _i64, _i64, _p, _p, _i, _p]),
     "hif8_tile_weight_codes": (_i, [_p, _i64, _i64, _p, _p]),
     "hif8_linear_fwd_tiled": (_i, [_p, _p, _p, _p, _p, _i64, _i64, _i64, _p]),
+    "hif8_transpose_codes": (_i, [_p, _i64, _i64, _p, _p]),
 }
 
 _lib = None

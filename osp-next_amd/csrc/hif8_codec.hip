@@ -630,6 +630,50 @@ __global__ __launch_bounds__(kTPB) void k_tile_wcodes(const uint8_t *__restrict_
     }
 }
 
+// Byte-matrix transpose, codes [R][C] -> [C][R]: the packed weight W^T that the fused GEMM
+// reads as its weight operand for dgrad (grad_q @ w_q, hif8_linear.py:97).  64 x 64 tiles
+// through LDS; interior tiles of 16-byte aligned matrices move 16 bytes per lane.
+__global__ __launch_bounds__(kTPB) void k_transpose_codes(const uint8_t *__restrict__ in, int64_t R, int64_t C,
+                                                          uint8_t *__restrict__ out, int64_t tiles_c, int vec)
+{
+    __shared__ uint32_t tile[64][17];  // 64 rows x 64 bytes, one pad dword per row
+    const int64_t t = blockIdx.x;
+    const int64_t tr = t / tiles_c, tc = t - tr * tiles_c;
+    const int64_t r0 = tr * 64, c0 = tc * 64;
+    const int tid = threadIdx.x;
+    const int rr = tid >> 2, q = tid & 3;  // this lane: row rr of the tile, bytes 16q .. 16q+15
+    const bool full = vec && r0 + 64 <= R && c0 + 64 <= C;
+    {
+        const int64_t r = r0 + rr, c = c0 + 16 * q;
+        uint32_t w[4] = {0u, 0u, 0u, 0u};
+        if (full) {
+            const uint4 v = *(const uint4 *)(in + r * C + c);
+            w[0] = v.x; w[1] = v.y; w[2] = v.z; w[3] = v.w;
+        } else if (r < R) {
+            for (int j = 0; j < 16; ++j)
+                if (c + j < C) w[j >> 2] |= uint32_t(in[r * C + c + j]) << (8 * (j & 3));
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) tile[rr][4 * q + j] = w[j];
+    }
+    __syncthreads();
+    // output row c0 + rr holds input column rr: bytes from input rows 16q .. 16q+15
+    uint32_t o[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+        const int src_row = 16 * q + j;
+        const uint32_t b = (tile[src_row][rr >> 2] >> (8 * (rr & 3))) & 0xFFu;
+        o[j >> 2] |= b << (8 * (j & 3));
+    }
+    const int64_t orow = c0 + rr, ocol = r0 + 16 * q;
+    if (full) {
+        *(uint4 *)(out + orow * R + ocol) = make_uint4(o[0], o[1], o[2], o[3]);
+    } else if (orow < C) {
+        for (int j = 0; j < 16; ++j)
+            if (ocol + j < R) out[orow * R + ocol + j] = uint8_t(o[j >> 2] >> (8 * (j & 3)));
+    }
+}
+
 // ---------------------------------------------------------------- launch
 
 // Workgroups per CU (measured on the 14B activation): amax streams best with one
@@ -804,6 +848,18 @@ int hif8_tile_weight_codes(const uint8_t *codes, int64_t N, int64_t K, uint8_t *
     int grid = grid_for((Npad / 32) * (K / 64) * 256, cu_count() * 8);
     hipLaunchKernelGGL(k_tile_wcodes, dim3(grid), dim3(kTPB), 0, (hipStream_t)stream, codes, int(N), int(K),
                        int(Npad), wt);
+    return last_launch();
+}
+
+int hif8_transpose_codes(const uint8_t *codes, int64_t rows, int64_t cols, uint8_t *out, hif8_stream_t stream)
+{
+    if (!codes || !out || rows <= 0 || cols <= 0) return HIF8_ERR_ARG;
+    if (rows >= (int64_t(1) << 31) || cols >= (int64_t(1) << 31)) return HIF8_ERR_SHAPE;
+    const int64_t tiles_r = (rows + 63) / 64, tiles_c = (cols + 63) / 64;
+    if (tiles_r * tiles_c >= (int64_t(1) << 31)) return HIF8_ERR_SHAPE;
+    const int vec = (rows % 16 == 0 && cols % 16 == 0 && aligned16(codes) && aligned16(out)) ? 1 : 0;
+    hipLaunchKernelGGL(k_transpose_codes, dim3(unsigned(tiles_r * tiles_c)), dim3(kTPB), 0, (hipStream_t)stream,
+                       codes, rows, cols, out, tiles_c, vec);
     return last_launch();
 }
 

@@ -12,8 +12,10 @@ the fused dequant-GEMM ``hif8_linear_fwd``.  The dequantised operands are
 bit-identical to the reference's; only the fp32 accumulation order differs.
 
 Backward (hif8_linear.py:88-111) quantises the incoming gradient with
-``scale_max_backward`` through the same HIP kernels and forms the products
-with torch matmuls on the decoded operands.
+``scale_max_backward`` through the same HIP kernels.  dgrad ``grad_q @ w_q``
+runs on the fused GEMM against the transposed weight codes when the gradient
+and weight are bf16 (the reference's autocast case); wgrad ``g^T @ x_q`` is a
+plain bf16 product on already-decoded operands and goes to the vendor GEMM.
 """
 from __future__ import annotations
 
@@ -164,9 +166,63 @@ class PackedWeight:
         self.wt = tile_weight_codes(self.codes) if (tiled and w.shape[1] % 64 == 0) else None
         self.scale_max = float(scale_max)
         self.key = (w.data_ptr(), weight._version, w.device)
+        self._codes_t: Optional[Tensor] = None
 
     def dequantize(self, dtype: Optional[torch.dtype] = None) -> Tensor:
         return decode(self.codes, self.state, dtype or self.src_dtype)
+
+    def codes_t(self) -> Tensor:
+        """The codes transposed, [K, N] (built once): the dgrad weight operand."""
+        if self._codes_t is None:
+            self._codes_t = transpose_codes(self.codes)
+        return self._codes_t
+
+
+def transpose_codes(codes: Tensor) -> Tensor:
+    """[R, C] uint8 -> [C, R] (hif8_transpose_codes)."""
+    _lib.require_gpu_tensor(codes, "codes")
+    R, C = codes.shape
+    out = torch.empty((C, R), dtype=torch.uint8, device=codes.device)
+    _lib.check(_lib.load().hif8_transpose_codes(codes.data_ptr(), R, C, out.data_ptr(), _lib.stream_ptr(codes.device)),
+               "hif8_transpose_codes")
+    return out
+
+
+def dgrad_fused_ok(grad_q: Tensor, w: "PackedWeight") -> bool:
+    """Shapes and dtypes the fused dgrad takes: bf16 gradient and weight, the weight's
+    out dim (the reduction) a multiple of 64 and its in dim a multiple of 8."""
+    N, K = w.shape
+    return (grad_q.dtype == torch.bfloat16 and w.src_dtype == torch.bfloat16 and N % 64 == 0 and K % 8 == 0
+            and N < (1 << 22))
+
+
+def linear_dgrad(grad_q2: Tensor, w: "PackedWeight") -> Tensor:
+    """grad_q [M, N] @ w_q [N, K] -> [M, K] bf16 on the fused GEMM (hif8_linear.py:97)."""
+    M, N = grad_q2.shape
+    K = w.shape[1]
+    g = _aligned(grad_q2.contiguous())
+    y = torch.empty((M, K), dtype=torch.bfloat16, device=g.device)
+    _lib.check(_lib.load().hif8_linear_fwd(g.data_ptr(), _lib.A_BF16, None, w.codes_t().data_ptr(), w.state.ptr,
+                                           None, y.data_ptr(), M, K, N, _lib.stream_ptr(g.device)),
+               "hif8_linear_fwd (dgrad)")
+    return y
+
+
+def fused_shape_ok(N: int, K: int) -> bool:
+    """Shapes hif8_linear_fwd takes: in_features K % 64 == 0, out_features N % 8 == 0."""
+    return K % 64 == 0 and N % 8 == 0 and K < (1 << 22)
+
+
+def linear_any(a: Tensor, a_fmt: int, a_state: Optional[QuantState], w: PackedWeight,
+               bias: Optional[Tensor]) -> Tensor:
+    """y = x_q @ w_q^T + bias in bf16 for any shape: the fused GEMM where it applies, else
+    the vendor bf16 GEMM on the same dequantised operands (decoded on the GPU)."""
+    N, K = w.shape
+    if fused_shape_ok(N, K):
+        return linear_fwd(a, a_fmt, a_state, w, bias)
+    xq = a if a_fmt == _lib.A_BF16 else decode(a, a_state, torch.bfloat16)
+    b = bias.detach().to(torch.bfloat16) if bias is not None else None
+    return torch.nn.functional.linear(xq.to(torch.bfloat16), w.dequantize(torch.bfloat16), b)
 
 
 def linear_fwd(a: Tensor, a_fmt: int, a_state: Optional[QuantState], w: PackedWeight,
@@ -223,7 +279,7 @@ def hif8_linear_inference(x: Tensor, packed: PackedWeight, bias: Optional[Tensor
     x2 = x.reshape(-1, K).contiguous()
     if packed.wt is None or packed.shape[0] % 8 != 0:
         a, a_fmt, a_st = quantize_activation(x2, scale_max_forward, "bf16")
-        y = linear_fwd(a, a_fmt, a_st, packed, bias)
+        y = linear_any(a, a_fmt, a_st, packed, bias)
     else:
         st = absmax_scale(x2, scale_max_forward, QuantState(x2.device))
         xt = fake_quant_tiled(x2, st)
@@ -245,7 +301,7 @@ class _HIF8LinearFunction(torch.autograd.Function):
             packed = PackedWeight(weight, scale_max_forward)
         needs_grad = any(ctx.needs_input_grad[:3])
         a, a_fmt, a_st = quantize_activation(x2, scale_max_forward, "codes" if a_format == "codes" else "bf16")
-        y = linear_fwd(a, a_fmt, a_st, packed, bias)
+        y = linear_any(a, a_fmt, a_st, packed, bias)
         if needs_grad:
             ctx.a, ctx.a_fmt, ctx.a_st, ctx.packed = a, a_fmt, a_st, packed
             ctx.x_dtype, ctx.w_dtype = x.dtype, weight.dtype
@@ -262,12 +318,16 @@ class _HIF8LinearFunction(torch.autograd.Function):
             x_q = decode(ctx.a, ctx.a_st, torch.bfloat16 if ctx.x_dtype == torch.bfloat16 else torch.float32)
         else:
             x_q = ctx.a
-        w_q = ctx.packed.dequantize(ctx.w_dtype)
         grad_q, _ = _quant(grad_output.contiguous(), ctx.smb)            # :93
         g_2d = grad_q.reshape(-1, grad_q.shape[-1])
-        ct = torch.promote_types(g_2d.dtype, w_q.dtype)
-        grad_input = (g_2d.to(ct) @ w_q.to(ct).contiguous()).to(ctx.x_dtype).view(ctx.x_shape)  # :97
-        grad_weight = (g_2d.t().contiguous().to(ct) @ x_q.to(ct)).to(ctx.w_dtype)             # :104
+        if dgrad_fused_ok(g_2d, ctx.packed):                              # :97, grad_q @ w_q
+            grad_input = linear_dgrad(g_2d, ctx.packed).to(ctx.x_dtype).view(ctx.x_shape)
+        else:
+            w_q = ctx.packed.dequantize(ctx.w_dtype)
+            ct = torch.promote_types(g_2d.dtype, w_q.dtype)
+            grad_input = (g_2d.to(ct) @ w_q.to(ct).contiguous()).to(ctx.x_dtype).view(ctx.x_shape)
+        ctw = torch.promote_types(g_2d.dtype, x_q.dtype)                  # :104, g^T @ x_q
+        grad_weight = (g_2d.t().contiguous().to(ctw) @ x_q.to(ctw)).to(ctx.w_dtype)
         grad_bias = g_2d.sum(0).to(ctx.b_dtype) if ctx.has_bias else None                   # :107
         return grad_input, grad_weight, grad_bias, None, None, None, None
 

@@ -1,0 +1,119 @@
+"""GPU parity of the backward path (hif8_linear.py:88-111): the code transpose, the fused
+dgrad grad_q @ w_q on the transposed codes, and HIF8Linear's gradients.
+
+Oracle: the gradient quantisation is checked bit for bit against the CPU restatement;
+products against fp32 torch on the same (bit-exact) quantised operands, with the
+tolerance of the forward tests (max element error relative to max(|ref|, 1e-2 rms)
+<= 1e-2, normwise <= 4e-3)."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda:0"
+TOL_ELEM = 1e-2
+TOL_NORM = 4e-3
+
+
+def rel_errors(y, y_ref):
+    y, y_ref = y.double(), y_ref.double()
+    rms = y_ref.square().mean().sqrt()
+    floor = torch.clamp(y_ref.abs(), min=1e-2 * float(rms))
+    return float(((y - y_ref).abs() / floor).max()), float((y - y_ref).norm() / y_ref.norm())
+
+
+@pytest.mark.parametrize("R,C", [(1, 1), (17, 33), (64, 64), (100, 300), (513, 1024), (1536, 8960), (640, 48)])
+def test_transpose_codes(pkg, R, C):
+    g = torch.Generator(device="cpu").manual_seed(R * 7 + C)
+    codes = torch.randint(0, 256, (R, C), generator=g, dtype=torch.int32).to(torch.uint8)
+    out = pkg.transpose_codes(codes.to(DEV))
+    assert out.shape == (C, R)
+    assert torch.equal(out.cpu(), codes.t().contiguous())
+
+
+@pytest.mark.parametrize("M,N,K", [(256, 256, 256), (300, 320, 264), (1000, 1536, 1536), (777, 5120, 1024),
+                                   (129, 64, 8)])
+def test_fused_dgrad_vs_fp32(pkg, R, M, N, K):
+    """grad_q [M, N] @ w_q [N, K] on the fused GEMM (transposed codes, the weight's table)."""
+    g = torch.Generator(device="cpu").manual_seed(M + N + K)
+    w = (torch.randn(N, K, generator=g) * 0.02).to(torch.bfloat16).to(DEV)
+    gy = torch.randn(M, N, generator=g).to(torch.bfloat16).to(DEV)
+    packed = pkg.PackedWeight(w, 15.0)
+    gq, _ = pkg._quant(gy, 224.0)
+    assert pkg.dgrad_fused_ok(gq, packed)
+    gx = pkg.linear_dgrad(gq, packed)
+    ref = gq.float() @ packed.dequantize().float()
+    elem, norm = rel_errors(gx, ref)
+    assert elem <= TOL_ELEM and norm <= TOL_NORM, (elem, norm)
+
+
+def test_gradient_quant_is_bit_exact(pkg, R):
+    """_quant(grad, 224) (hif8_linear.py:93) against the CPU restatement."""
+    g = torch.Generator(device="cpu").manual_seed(3)
+    gy = (torch.randn(333, 520, generator=g) * 1e-3).to(torch.bfloat16)
+    gq, _ = pkg._quant(gy.to(DEV), 224.0)
+    want, _ = R.quant_bf16(gy.view(torch.int16).numpy().view(np.uint16), 224.0, "npu")
+    assert np.array_equal(gq.cpu().view(torch.int16).numpy().view(np.uint16), want)
+
+
+@pytest.mark.parametrize("M,K,N,bias", [(384, 256, 320, True), (1000, 1536, 8960, False), (257, 512, 100, True)])
+def test_hif8linear_backward(pkg, M, K, N, bias):
+    """HIF8Linear gradients vs the reference formula in fp32 on the same quantised tensors.
+    N = 100 takes the vendor-GEMM dgrad (N % 64 != 0); the others the fused dgrad."""
+    g = torch.Generator(device="cpu").manual_seed(M + K + N)
+    shape = (2, M // 2, K) if M % 2 == 0 else (M, K)
+    x = torch.randn(shape, generator=g).to(torch.bfloat16).to(DEV).requires_grad_(True)
+    lin = pkg.HIF8Linear(K, N, bias=bias, device=DEV, dtype=torch.bfloat16)
+    y = lin(x)
+    gy = torch.randn(y.shape, generator=g).to(torch.bfloat16).to(DEV)
+    y.backward(gy)
+    xq, _ = pkg._quant(x.detach(), 15.0)
+    wq, _ = pkg._quant(lin.weight.detach(), 15.0)
+    gq, _ = pkg._quant(gy, 224.0)
+    g2, x2 = gq.reshape(-1, N).float(), xq.reshape(-1, K).float()
+    gx = (g2 @ wq.float()).view(x.shape)
+    gw = g2.t() @ x2
+    checks = [(x.grad, gx), (lin.weight.grad, gw)]
+    if bias:
+        checks.append((lin.bias.grad, g2.sum(0)))
+    for got, want in checks:
+        assert got.dtype == torch.bfloat16
+        elem, norm = rel_errors(got, want)
+        assert elem <= TOL_ELEM and norm <= TOL_NORM, (got.shape, elem, norm)
+
+
+def test_fp32_input_gradients_promote_like_the_reference(pkg):
+    """fp32 x (self-attention o) with a bf16 weight: dgrad in the promoted fp32, wgrad
+    g^T @ x_q with x_q fp32 (hif8_linear.py:97,104), grads cast to the inputs' dtypes."""
+    M, K, N = 300, 256, 192
+    g = torch.Generator(device="cpu").manual_seed(11)
+    x = torch.randn(M, K, generator=g).to(DEV).requires_grad_(True)
+    lin = pkg.HIF8Linear(K, N, bias=False, device=DEV, dtype=torch.bfloat16)
+    y = lin(x)
+    gy = torch.randn(y.shape, generator=g).to(torch.bfloat16).to(DEV)
+    y.backward(gy)
+    assert x.grad.dtype == torch.float32 and lin.weight.grad.dtype == torch.bfloat16
+    xq, _ = pkg._quant(x.detach(), 15.0)
+    wq, _ = pkg._quant(lin.weight.detach(), 15.0)
+    gq, _ = pkg._quant(gy, 224.0)
+    for got, want in ((x.grad, gq.float() @ wq.float()), (lin.weight.grad, gq.float().t() @ xq.float())):
+        elem, norm = rel_errors(got, want)
+        assert elem <= TOL_ELEM and norm <= TOL_NORM, (elem, norm)
+
+
+def test_dgrad_config2_shape(pkg):
+    """1.3B 480P FFN-down backward shape: grad [32760, 1536] @ w_q [1536, 8960], sampled rows."""
+    M, N, K = 32760, 1536, 8960
+    g = torch.Generator(device="cpu").manual_seed(4)
+    w = (torch.randn(N, K, generator=g) * 0.02).to(torch.bfloat16).to(DEV)
+    gy = torch.randn(M, N, generator=g).to(torch.bfloat16).to(DEV)
+    packed = pkg.PackedWeight(w, 15.0)
+    gq, _ = pkg._quant(gy, 224.0)
+    gx = pkg.linear_dgrad(gq, packed)
+    rows = torch.cat([torch.randint(0, M, (256,), generator=g), torch.arange(M - 40, M)]).to(DEV)
+    ref = gq[rows].float() @ packed.dequantize().float()
+    elem, norm = rel_errors(gx[rows], ref)
+    assert elem <= TOL_ELEM and norm <= TOL_NORM, (elem, norm)

@@ -191,3 +191,21 @@ def test_hif8linear_backward_matches_reference_formula(pkg):
     for got, want in ((x.grad, gx), (lin.weight.grad, gw), (lin.bias.grad, gb)):
         elem, norm = rel_errors(got, want)
         assert norm <= 1e-2, norm
+
+
+@pytest.mark.parametrize("K,N", [(100, 36), (64, 100), (130, 257), (40, 8)])
+def test_hif8linear_shapes_outside_the_fused_gemm(pkg, R, K, N):
+    """in_features % 64 != 0 or out_features % 8 != 0: the layer still works (vendor bf16 GEMM
+    on the same dequantised operands; none of the model's linears has such a shape)."""
+    g = torch.Generator(device="cpu").manual_seed(K * 3 + N)
+    x = torch.randn(3, 41, K, generator=g).to(torch.bfloat16).to(DEV)
+    lin = pkg.HIF8Linear(K, N, bias=True, device=DEV, dtype=torch.bfloat16)
+    with torch.no_grad():
+        lin.bias.normal_(0, 0.1)
+        y = lin(x)
+    assert y.shape == (3, 41, N) and y.dtype == torch.bfloat16
+    xq, _ = pkg._quant(x, 15.0)
+    wq, _ = pkg._quant(lin.weight, 15.0)
+    y_ref = ref_linear_fp32(xq.view(-1, K), wq, lin.bias).view(3, 41, N)
+    elem, norm = rel_errors(y, y_ref)
+    assert elem <= TOL_ELEM and norm <= TOL_NORM
