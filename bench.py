@@ -117,6 +117,38 @@ def measured_traffic(kernel: str):
     return None
 
 
+def time_ffn(pkg, torch, x, reps):
+    """The 14B FFN (osp_next.py:873-877) on x: HIF8FFN's fused route (GELU + amax in the
+    up-projection's epilogue) against the plain sequence HIF8Linear -> GELU -> HIF8Linear."""
+    dim, ffn = x.shape[1], 13824
+    torch.manual_seed(3)
+    mod = pkg.HIF8FFN(dim, ffn, device=x.device, dtype=torch.bfloat16)
+    with torch.no_grad():
+        for p in mod.parameters():
+            p.normal_(0, 0.02)
+    mod[0].prepack(drop_weight=False)
+    mod[2].prepack(drop_weight=False)
+    out = {}
+    with torch.no_grad():
+        for label, fn in (("fused", lambda: mod(x)), ("sequence", lambda: torch.nn.Sequential.forward(mod, x))):
+            for _ in range(2):
+                fn()
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(reps):
+                fn()
+            e1.record()
+            torch.cuda.synchronize()
+            out[f"{label}_ms"] = round(e0.elapsed_time(e1) / reps, 4)
+    flops = 2.0 * 2 * x.shape[0] * dim * ffn
+    out["fused_TFLOPs"] = round(flops / (out["fused_ms"] * 1e-3) / 1e12, 1)
+    out["speedup"] = round(out["sequence_ms"] / out["fused_ms"], 4)
+    out["what"] = "FFN 5120->13824->5120 on x[75600,5120] bf16, prepacked weights, no autograd"
+    del mod
+    return out
+
+
 def median(v):
     s = sorted(v)
     return s[len(s) // 2]
@@ -177,7 +209,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--a-format", default="bf16", choices=["tiled", "bf16", "codes"])
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--shapes", default="up", help="comma list of up,down,qkvo to time in addition")
+    ap.add_argument("--shapes", default="up", help="comma list of up,down,qkvo,ffn to time in addition")
     ap.add_argument("--pmc-calibration", action="store_true",
                     help="also run one plain copy of x (774,144,000 B read + written): the reference "
                          "kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE")
@@ -251,7 +283,9 @@ def main():
     del codes
 
     extra_shapes = {}
-    for name in [s for s in args.shapes.split(",") if s and s != "up"]:
+    if "ffn" in args.shapes.split(","):
+        extra_shapes["ffn"] = time_ffn(pkg, torch, x, max(3, args.steps // 2))
+    for name in [s for s in args.shapes.split(",") if s and s not in ("up", "ffn")]:
         n_, k_ = {"down": (5120, 13824), "qkvo": (5120, 5120)}[name]
         xs, ws, bs = make_inputs(torch, M, k_, n_, seed=1)
         ps = pkg.PackedWeight(ws, 15.0)

@@ -123,6 +123,18 @@ int hif8_linear_fwd(const void *a, int a_fmt, const void *a_state, const uint8_t
                     const void *w_state, const uint16_t *bias, uint16_t *y, int64_t M,
                     int64_t N, int64_t K, hif8_stream_t stream);
 
+/* Producer fusion for nn.Sequential(HIF8Linear, GELU(tanh), HIF8Linear)
+ * (osp_next.py:873-877): hif8_linear_fwd with bf16 activations whose epilogue applies
+ *   y = rnd_bf16(gelu_tanh(rnd_bf16(x_q @ w_q^T + bias)))
+ * (nn.GELU(approximate="tanh") on the bf16 linear output, in fp32) and folds amax|y| into
+ * y_state with the scale rule for scale_max, as hif8_absmax_scale(y) would: the next
+ * linear's _quant (hif8_linear.py:45-48) then needs only hif8_fake_quant(y, y_state).
+ * y_state must have been initialised (hif8_state_init); shapes as hif8_linear_fwd.
+ * No single reference function: it fuses three reference steps. */
+int hif8_linear_fwd_gelu_amax(const void *a, const uint8_t *w_codes, const void *w_state, const uint16_t *bias,
+                              uint16_t *y, int64_t M, int64_t N, int64_t K, float scale_max, void *y_state,
+                              hif8_stream_t stream);
+
 /* ---------------------------------------------------------------------------
  * GEMM-native operand layouts and the tiled fused linear (the fast path of
  * hif8_linear.py:68-86).

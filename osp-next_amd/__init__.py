@@ -34,7 +34,11 @@ from .hif8_linear import (  # noqa: F401
     transpose_codes,
     linear_dgrad,
     dgrad_fused_ok,
+    fused_shape_ok,
+    linear_any,
+    linear_fwd_gelu_amax,
 )
+from .ffn import HIF8FFN  # noqa: F401
 from .hif8_attention import (  # noqa: F401
     _HIF8QKVQuantFunction,
     attention_with_mask,
@@ -59,5 +63,6 @@ __all__ = [
     "tile_weight_codes", "tiled_rows", "linear_fwd_tiled", "transpose_codes", "linear_dgrad", "dgrad_fused_ok",
     "_HIF8QKVQuantFunction", "attention_with_mask", "hif8_attention_with_mask",
     "scaled_dot_product_attention_with_mask", "LinearForward", "LinearForwardFast", "QLinear", "replace_linear",
-    "save_packed", "load_packed", "pack_state_dict", "packed_from_codes",
+    "save_packed", "load_packed", "pack_state_dict", "packed_from_codes", "fused_shape_ok", "linear_any",
+    "linear_fwd_gelu_amax", "HIF8FFN",
 ]

@@ -17,6 +17,7 @@
 
 #include "hif8_common.h"
 #include "hif8_internal.h"
+#include "hif8_state_dev.h"
 
 namespace hif8 {
 
@@ -25,18 +26,6 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 __constant__ EncTable kEncTable = make_enc_table();
 
 // ---------------------------------------------------------------- helpers
-
-__device__ __forceinline__ uint32_t f2u(float f) { return __builtin_bit_cast(uint32_t, f); }
-__device__ __forceinline__ float u2f(uint32_t u) { return __builtin_bit_cast(float, u); }
-__device__ __forceinline__ float bf2f(uint32_t b) { return u2f(b << 16); }
-
-// float -> bf16 bits, round-to-nearest-even, NaN -> 0x7FC0 (c10::BFloat16).
-__device__ __forceinline__ uint32_t f2bf(float f)
-{
-    uint32_t u = f2u(f);
-    if ((u & 0x7FFFFFFFu) > 0x7F800000u) return 0x7FC0u;
-    return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
-}
 
 // Packed RNE convert of two finite floats (v_cvt_pk_bf16_f32).
 __device__ __forceinline__ uint32_t f2bf_pk(float lo, float hi)
@@ -84,37 +73,6 @@ __device__ __forceinline__ void slow_elem(uint32_t xbits, float s, int sem, uint
         float q = sem == kSemTorch ? qdq_torch(xs) : qdq_npu(xs);
         ybits = f2u(q / s);
     }
-}
-
-// Scale rule of hif8_linear.py:45-46 for the dtype; returns scale as fp32.
-__device__ float scale_from_amax(uint32_t amax_bits, int dtype, float smax, bool &fast)
-{
-    float a, s;
-    if (dtype == kBF16) {
-        uint32_t ab = amax_bits & 0x7FFFu;
-        if (ab <= 0x7F80u) ab = ab > 0x322Cu ? ab : 0x322Cu;   // clamp(min=bf16(1e-8))
-        a = bf2f(ab);
-        float r = bf2f(f2bf(1.0f / a));                      // reciprocal()   (bf16)
-        s = bf2f(f2bf(r * smax));                            // * scale_max    (bf16)
-    } else {
-        a = u2f(amax_bits & 0x7FFFFFFFu);
-        if (!__builtin_isnan(a)) a = a > 1e-8f ? a : 1e-8f;
-        float r = 1.0f / a;
-        s = r * smax;
-    }
-    fast = __builtin_isfinite(a) && __builtin_isfinite(s) && s > 0.0f;
-    return s;
-}
-
-// Fill the decode tables of st for scale s (one entry per thread, 256 threads).
-// bf16 tensors: x_q = rnd_bf16(q / s) with q exact in bf16 (QTensor.py:126-127
-// then the bf16 division of hif8_linear.py:48).  fp32 tensors: x_q = q / s in
-// fp32, and the bf16 GEMM operand is its autocast rounding.
-__device__ void fill_luts(State *st, float s, uint32_t c)
-{
-    float y = u2f(decode_bits(c)) / s;
-    st->lut_f32[c] = y;
-    st->lut_bf16[c] = uint16_t(f2bf(y));
 }
 
 // ---------------------------------------------------------------- kernels
@@ -229,34 +187,11 @@ __global__ __launch_bounds__(kTPB) void k_absmax(const void *__restrict__ xv, in
     }
     // wavefront reduction, then across the 4 waves through LDS
     for (int o = 32; o > 0; o >>= 1) m = max(m, (uint32_t)__shfl_xor((int)m, o, 64));
-    __shared__ uint32_t red[kTPB / 64];
-    __shared__ uint32_t last;
+    __shared__ uint32_t red[kTPB / 64 + 2];
     if ((tid & 63) == 0) red[tid >> 6] = m;
     __syncthreads();
-    if (tid == 0) {
-        m = max(max(red[0], red[1]), max(red[2], red[3]));
-        __hip_atomic_fetch_max(&st->amax_acc, m, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        uint32_t prev = __hip_atomic_fetch_add(&st->counter, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-        last = (prev == gridDim.x - 1) ? 1u : 0u;
-    }
-    __syncthreads();
-    if (!last) return;
-    // last workgroup: read and reset the accumulators, compute scale and tables
-    __shared__ float s_sh;
-    if (tid == 0) {
-        uint32_t a = __hip_atomic_exchange(&st->amax_acc, 0u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(&st->counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        bool fast;
-        float s = scale_from_amax(a, DT, smax, fast);
-        st->amax_bits = a;
-        st->scale = s;
-        st->fast = fast ? 1u : 0u;
-        st->finite = fast ? 1u : 0u;   // amax finite => every element finite
-        st->dtype = uint32_t(DT);
-        s_sh = s;
-    }
-    __syncthreads();
-    fill_luts(st, s_sh, uint32_t(tid));
+    m = max(max(red[0], red[1]), max(red[2], red[3]));
+    fold_amax(st, m, gridDim.x, DT, smax, red + kTPB / 64);
 }
 
 // LDS map of the quantise kernels: [0,512) bf16 decode table, [1024,2048) fp32

@@ -235,6 +235,20 @@ __global__ __launch_bounds__(kThreads, 1) void k_linear(
 
 using namespace hif8;
 
+extern "C" int hif8_linear_fwd_gelu_amax(const void *a, const uint8_t *w_codes, const void *w_state,
+                                         const uint16_t *bias, uint16_t *y, int64_t M, int64_t N, int64_t K,
+                                         float scale_max, void *y_state, hif8_stream_t stream)
+{
+    if (!a || !w_codes || !w_state || !y || !y_state) return HIF8_ERR_ARG;
+    if (M <= 0 || N <= 0 || K <= 0) return HIF8_ERR_ARG;
+    if (M >= (int64_t(1) << 31) || N >= (int64_t(1) << 31) || K >= (int64_t(1) << 31)) return HIF8_ERR_SHAPE;
+    if (K % kBK != 0 || N % 8 != 0) return HIF8_ERR_SHAPE;
+    if (((uintptr_t)a | (uintptr_t)w_codes | (uintptr_t)y) & 15u) return HIF8_ERR_ALIGN;
+    if (bias && ((uintptr_t)bias & 7u)) return HIF8_ERR_ALIGN;
+    return launch_linear_dtl((const uint16_t *)a, w_codes, (const State *)w_state, bias, y, M, N, K, stream,
+                             (State *)y_state, scale_max);
+}
+
 extern "C" int hif8_linear_fwd(const void *a, int a_fmt, const void *a_state, const uint8_t *w_codes,
                                const void *w_state, const uint16_t *bias, uint16_t *y, int64_t M, int64_t N,
                                int64_t K, hif8_stream_t stream)

@@ -29,8 +29,9 @@ struct alignas(256) State {
 static_assert(sizeof(State) % 256 == 0, "state size");
 
 // Fused GEMM for bf16 activations (hif8_gemm_dtl.hip); the caller has checked shapes and
-// alignment as hif8_linear_fwd documents.
+// alignment as hif8_linear_fwd documents.  With y_st, the GELU + amax epilogue.
 int launch_linear_dtl(const uint16_t *x, const uint8_t *w_codes, const State *w_st, const uint16_t *bias,
-                      uint16_t *y, int64_t M, int64_t N, int64_t K, hif8_stream_t stream);
+                      uint16_t *y, int64_t M, int64_t N, int64_t K, hif8_stream_t stream, State *y_st = nullptr,
+                      float y_smax = 0.0f);
 
 }  // namespace hif8

@@ -1,0 +1,54 @@
+"""The DiT block's feed-forward network with producer fusion.
+
+``HIF8FFN`` is ``nn.Sequential(HIF8Linear(dim, ffn_dim), nn.GELU(approximate="tanh"),
+HIF8Linear(ffn_dim, dim))`` -- ``ospnext/modules/osp_next.py:873-877`` -- with the same
+children and state-dict keys.  Without autograd, a bf16 input takes the fused route:
+
+    up:    hif8_linear_fwd_gelu_amax   y = gelu(x_q @ w_up^T + b_up), amax|y| and its scale
+    down:  hif8_fake_quant(y) with that scale (no amax pass), then the fused GEMM
+
+which removes the standalone GELU pass and the down-projection's amax pass (the
+reference reads and writes y for GELU and reads it again for amax|y|).  With autograd,
+or for inputs and shapes the fused kernels do not take, it runs the plain sequence.
+"""
+from __future__ import annotations
+
+import torch
+import torch.nn as nn
+from torch import Tensor
+
+from . import _lib
+from .hif8_linear import (HIF8Linear, QuantState, fake_quant, fused_shape_ok, linear_any,
+                          linear_fwd_gelu_amax, quantize_activation)
+
+
+class HIF8FFN(nn.Sequential):
+    def __init__(self, dim: int, ffn_dim: int, scale_max_forward: float = 15.0, scale_max_backward: float = 224.0,
+                 bias: bool = True, device=None, dtype=None):
+        super().__init__(
+            HIF8Linear(dim, ffn_dim, bias=bias, scale_max_forward=scale_max_forward,
+                       scale_max_backward=scale_max_backward, device=device, dtype=dtype),
+            nn.GELU(approximate="tanh"),
+            HIF8Linear(ffn_dim, dim, bias=bias, scale_max_forward=scale_max_forward,
+                       scale_max_backward=scale_max_backward, device=device, dtype=dtype),
+        )
+
+    def fused_ok(self, x: Tensor) -> bool:
+        up, down = self[0], self[2]
+        grad = torch.is_grad_enabled() and (x.requires_grad or any(p.requires_grad for p in self.parameters()))
+        return (not grad and x.dtype == torch.bfloat16 and x.is_cuda and up.a_format != "codes"
+                and fused_shape_ok(up.out_features, up.in_features)
+                and fused_shape_ok(down.out_features, down.in_features))
+
+    def forward(self, x: Tensor) -> Tensor:
+        if not self.fused_ok(x):
+            return super().forward(x)
+        up, down = self[0], self[2]
+        K = x.shape[-1]
+        x2 = x.reshape(-1, K).contiguous()
+        a, a_fmt, _ = quantize_activation(x2, up.scale_max_forward, "bf16")
+        y_st = QuantState(x2.device)
+        y = linear_fwd_gelu_amax(a, up._packed_weight(), up.bias, y_st, down.scale_max_forward)
+        yq = fake_quant(y, y_st)
+        out = linear_any(yq, _lib.A_BF16, None, down._packed_weight(), down.bias)
+        return out.view(*x.shape[:-1], out.shape[-1])

@@ -243,6 +243,27 @@ def linear_fwd(a: Tensor, a_fmt: int, a_state: Optional[QuantState], w: PackedWe
     return y
 
 
+def linear_fwd_gelu_amax(a: Tensor, w: PackedWeight, bias: Optional[Tensor], y_state: QuantState,
+                         scale_max: float) -> Tensor:
+    """hif8_linear_fwd_gelu_amax: y = gelu_tanh(x_q @ w_q^T + bias) in bf16 (bf16 x_q), with amax|y|
+    and its scale for ``scale_max`` left in ``y_state``."""
+    M, K = a.shape
+    N = w.shape[0]
+    if w.shape[1] != K:
+        raise ValueError(f"in_features mismatch: x has {K}, weight has {w.shape[1]}")
+    if a.dtype != torch.bfloat16:
+        raise TypeError("the GELU + amax epilogue takes bf16 activations")
+    y = torch.empty((M, N), dtype=torch.bfloat16, device=a.device)
+    b_ptr = None
+    if bias is not None:
+        bias = bias.detach().to(torch.bfloat16).contiguous()
+        b_ptr = bias.data_ptr()
+    _lib.check(_lib.load().hif8_linear_fwd_gelu_amax(a.data_ptr(), w.codes.data_ptr(), w.state.ptr, b_ptr,
+                                                     y.data_ptr(), M, N, K, float(scale_max), y_state.ptr,
+                                                     _lib.stream_ptr(a.device)), "hif8_linear_fwd_gelu_amax")
+    return y
+
+
 def linear_fwd_tiled(xt: Tensor, M: int, w: PackedWeight, bias: Optional[Tensor]) -> Tensor:
     """hif8_linear_fwd_tiled: the fused GEMM on XT activations and WT codes."""
     N, K = w.shape

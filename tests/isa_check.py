@@ -110,16 +110,23 @@ def check_body(body, passes=3):
     return errors
 
 
-def mfma_loop(asm_text):
-    """Body of the first loop that contains MFMAs, as parsed instructions."""
+def mfma_loops(asm_text):
+    """Bodies of every loop that contains MFMAs (one per kernel instantiation), parsed."""
     lines = asm_text.splitlines()
+    out = []
     for s, line in enumerate(lines):
         if 'Loop Header' not in line:
             continue
         e = next(i for i in range(s + 1, len(lines)) if re.search(r's_cbranch_scc|s_cbranch_vcc', lines[i]))
         if any('v_mfma' in x for x in lines[s:e]):
-            return parse(lines[s + 1:e])
-    return []
+            out.append(parse(lines[s + 1:e]))
+    return out
+
+
+def mfma_loop(asm_text):
+    """Body of the first loop that contains MFMAs, as parsed instructions."""
+    loops = mfma_loops(asm_text)
+    return loops[0] if loops else []
 
 
 def census(body):

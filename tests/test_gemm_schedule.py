@@ -40,20 +40,25 @@ def dtl_asm(tmp_path_factory):
 
 
 def test_resources(dtl_asm):
+    """Both instantiations (plain and GELU + amax epilogue)."""
     _, remarks = dtl_asm
-    assert re.search(r"VGPRs Spill: 0", remarks)
-    assert re.search(r"SGPRs Spill: 0", remarks)
-    assert re.search(r"LDS Size \[bytes/block\]: 163840", remarks)
-    assert "ScratchSize [bytes/lane]: 0" in remarks
+    spills = re.findall(r"(?:VGPRs|SGPRs) Spill: (\d+)", remarks)
+    lds = re.findall(r"LDS Size \[bytes/block\]: (\d+)", remarks)
+    scratch = re.findall(r"ScratchSize \[bytes/lane\]: (\d+)", remarks)
+    assert len(lds) == 2 and set(lds) == {"163840"}, lds
+    assert spills and set(spills) == {"0"}, spills
+    assert scratch and set(scratch) == {"0"}, scratch
 
 
 def test_main_loop_hazards(dtl_asm):
     import isa_check
-    body = isa_check.mfma_loop(dtl_asm[0])
-    kinds = isa_check.census(body)
-    assert kinds.get("mfma") == 128 and kinds.get("lds_load") == 200 and kinds.get("lds_dma") == 24, kinds
-    errors = isa_check.check_body(body)
-    assert not errors, "\n".join(errors[:20])
+    loops = isa_check.mfma_loops(dtl_asm[0])
+    assert len(loops) == 2
+    for body in loops:
+        kinds = isa_check.census(body)
+        assert kinds.get("mfma") == 128 and kinds.get("lds_load") == 200 and kinds.get("lds_dma") == 24, kinds
+        errors = isa_check.check_body(body)
+        assert not errors, "\n".join(errors[:20])
 
 
 def test_checker_catches_planted_mistakes():
