@@ -177,6 +177,37 @@ int hif8_linear_fwd_tiled(const uint16_t *xt, const uint8_t *wt, const void *w_s
  */
 int hif8_transpose_codes(const uint8_t *codes, int64_t rows, int64_t cols, uint8_t *out, hif8_stream_t stream);
 
+/* ---------------------------------------------------------------------------
+ * Producer fusion for the modulated LayerNorm in front of the self-attention q/k/v
+ * and FFN-up projections: block_forward's
+ *     y = norm(x) * (1 + scale) + shift                  (osp_next.py:941, :954)
+ * with norm the WanLayerNorm (want2v.py:96-106: fp32 layer norm over the last dim,
+ * no affine, eps, result cast to bf16), the product and sum bf16 tensor ops, and
+ * then _quant(y) of each consuming HIF8Linear (hif8_linear.py:42-50).  No single
+ * reference function: it fuses these steps, and the three identical _quant(y) of
+ * q, k and v become one.
+ *
+ * x is bf16 [rows, dim] (dim % 8 == 0, dim <= 8192); shift and scale are bf16
+ * [rows / rows_per_batch, dim] (row r uses modulation row r / rows_per_batch), or
+ * NULL for zeros (then y = norm(x)).  stats is a float [rows * 2] buffer (8-byte
+ * aligned) for each row's (mean, rstd); x, shift, scale, x_q and y are 16-byte
+ * aligned.
+ *
+ * hif8_modln_amax: writes stats and folds amax|y| into state with the scale rule
+ *   for scale_max, as hif8_absmax_scale(y) would (state initialised).
+ * hif8_modln_fake_quant: x_q = qdq(y * s) / s in bf16 with that state, as
+ *   hif8_fake_quant(y, state, semantics) would; y is also written when non-NULL.
+ * The row statistics are fp32 two-pass sums, so y may differ from another fp32
+ * layer norm's by one bf16 unit where the fp32 result rounds at a tie boundary;
+ * x_q is exactly the qdq of the y this library computes.
+ */
+int hif8_modln_amax(const uint16_t *x, const uint16_t *shift, const uint16_t *scale, int64_t rows, int64_t dim,
+                    int64_t rows_per_batch, float eps, float *stats, float scale_max, void *state,
+                    hif8_stream_t stream);
+int hif8_modln_fake_quant(const uint16_t *x, const uint16_t *shift, const uint16_t *scale, int64_t rows,
+                          int64_t dim, int64_t rows_per_batch, const float *stats, const void *state,
+                          int semantics, uint16_t *x_q, uint16_t *y, hif8_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -18,6 +18,9 @@ What it restates (citations are into the reference tree):
   (``QTensor.py:94-128``, ``force_fp32=True``): ``xs = x*scale``; fp32 qdq; cast
   back to the input dtype; ``/ scale``.
 * ``linear``            -- ``hif8_linear.py:68-86``: ``F.linear(_quant(x), _quant(W), b)``.
+* ``modulated_layer_norm_bf16`` -- the producer of the q/k/v and FFN-up inputs,
+  ``norm(x) * (1 + scale) + shift`` (``osp_next.py:941``, ``:954``) with the WanLayerNorm
+  (``want2v.py:96-106``); its ``_quant`` is ``quant_bf16`` above.
 
 bf16 arithmetic is emulated bit-exactly: every bf16 op of the reference is an
 fp32 op followed by round-to-nearest-even (torch CPU's ``c10::BFloat16``).
@@ -255,6 +258,43 @@ def linear(x_bits, w_bits, b_bits=None, scale_max: float = 15.0, semantics: str 
         y = F.linear(xt, wt, bt)
         return y.view(torch.int16).numpy().view(np.uint16), xq, wq
     raise ValueError(accumulate)
+
+
+# ------------------------------------------- modulated LayerNorm (producer)
+
+
+def layer_norm_bf16(x_bits, eps: float = 1e-6):
+    """WanLayerNorm (``ospnext/modules/want2v.py:96-106``) of a bf16 [rows, dim] tensor:
+    ``layer_norm(x.float(), eps)`` without affine, ``.type_as(x)``.  The normalisation is
+    evaluated in float64 (mean, biased variance, ``(x - mean) / sqrt(var + eps)``) and rounded
+    to fp32 and then to bf16: the exact result to well below one bf16 unit, where an fp32
+    implementation can differ only at a rounding boundary."""
+    x = bf16_to_f32(x_bits).astype(np.float64)
+    mean = x.mean(axis=-1, keepdims=True)
+    var = np.square(x - mean).mean(axis=-1, keepdims=True)
+    with np.errstate(all="ignore"):
+        n = (x - mean) / np.sqrt(var + np.float64(F32(eps)))
+    return f32_to_bf16(n.astype(F32))
+
+
+def modulated_layer_norm_bf16(x_bits, shift_bits=None, scale_bits=None, rows_per_batch=None, eps: float = 1e-6):
+    """``norm(x) * (1 + scale) + shift`` of ``block_forward`` (``osp_next.py:941``, ``:954``) with
+    bf16 tensors: ``n = layer_norm_bf16(x)``, ``t = bf16(1 + scale)``, ``u = bf16(n * t)``,
+    ``y = bf16(u + shift)`` (each bf16 tensor op an fp32 op rounded to bf16).  ``shift`` and
+    ``scale`` are [batches, dim]; row r uses modulation row ``r // rows_per_batch``; None is 0."""
+    x_bits = np.asarray(x_bits, dtype=np.uint16)
+    rows, dim = x_bits.shape
+    rpb = rows if rows_per_batch is None else rows_per_batch
+    n = layer_norm_bf16(x_bits, eps)
+    bidx = np.arange(rows) // rpb
+    zero = np.zeros((int(bidx.max()) + 1, dim), np.uint16)
+    sh = zero if shift_bits is None else np.asarray(shift_bits, np.uint16).reshape(-1, dim)
+    sc = zero if scale_bits is None else np.asarray(scale_bits, np.uint16).reshape(-1, dim)
+    with np.errstate(all="ignore"):
+        t = f32_to_bf16(F32(1.0) + bf16_to_f32(sc))
+        u = f32_to_bf16(bf16_to_f32(n) * bf16_to_f32(t)[bidx])
+        y = f32_to_bf16(bf16_to_f32(u) + bf16_to_f32(sh)[bidx])
+    return y
 
 
 # ------------------------------------------------------------- input recipes

@@ -9,6 +9,7 @@ Public surface, mirroring the reference:
   HIF8Linear, _quant, make_linear                   (ospnext/modules/hif8_linear.py, osp_next.py)
   hif8_attention_with_mask, _HIF8QKVQuantFunction   (ospnext/modules/hif8_attention.py)
   QLinear, replace_linear                           (quant_cy_npu/layers/QLinear.py, utils/utils.py)
+  WanLayerNorm                                      (ospnext/modules/want2v.py)
 plus the tensor-level HIP ops (absmax_scale, encode, fake_quant, decode,
 linear_fwd), QuantState and PackedWeight.
 """
@@ -39,6 +40,7 @@ from .hif8_linear import (  # noqa: F401
     linear_fwd_gelu_amax,
 )
 from .ffn import HIF8FFN  # noqa: F401
+from .norm import WanLayerNorm, modulate, modulated_norm_quant, qkv_from_modulated_norm  # noqa: F401
 from .hif8_attention import (  # noqa: F401
     _HIF8QKVQuantFunction,
     attention_with_mask,
@@ -64,5 +66,6 @@ __all__ = [
     "_HIF8QKVQuantFunction", "attention_with_mask", "hif8_attention_with_mask",
     "scaled_dot_product_attention_with_mask", "LinearForward", "LinearForwardFast", "QLinear", "replace_linear",
     "save_packed", "load_packed", "pack_state_dict", "packed_from_codes", "fused_shape_ok", "linear_any",
-    "linear_fwd_gelu_amax", "HIF8FFN",
+    "linear_fwd_gelu_amax", "HIF8FFN", "WanLayerNorm", "modulate", "modulated_norm_quant",
+    "qkv_from_modulated_norm",
 ]

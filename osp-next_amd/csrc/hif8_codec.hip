@@ -18,62 +18,11 @@
 #include "hif8_common.h"
 #include "hif8_internal.h"
 #include "hif8_state_dev.h"
+#include "hif8_qdq_dev.h"
 
 namespace hif8 {
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
-
-__constant__ EncTable kEncTable = make_enc_table();
-
-// ---------------------------------------------------------------- helpers
-
-// Packed RNE convert of two finite floats (v_cvt_pk_bf16_f32).
-__device__ __forceinline__ uint32_t f2bf_pk(float lo, float hi)
-{
-    typedef float f32x2 __attribute__((ext_vector_type(2)));
-    typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-    f32x2 v = {lo, hi};
-    bf16x2 r = __builtin_convertvector(v, bf16x2);
-    return __builtin_bit_cast(uint32_t, r);
-}
-
-// QFuncs/hif8.py:6-23 on one fp32 value, with the same fp32 operations.
-// floor(log2(v)) of the normal value v = |x| + 2^-45 is taken from its exponent
-// field; torch's log2 agrees with it wherever the result can differ.
-__device__ float qdq_torch(float x)
-{
-    float xu = fabsf(x);
-    float sign = float(x > 0.0f) - float(x < 0.0f);
-    if (!(xu <= 3.402823466e38f)) return __builtin_nanf("");   // NaN, Inf -> NaN
-    float v = xu + 0x1p-45f;
-    int e = int((f2u(v) >> 23) & 0xFF) - 127;
-    int ae = e < 0 ? -e : e;
-    int mb = ae <= 3 ? 3 : ae <= 7 ? 2 : ae <= 15 ? 1 : 0;
-    float t = xu * __builtin_ldexpf(1.0f, mb - e);
-    float r = __builtin_floorf(t + 0.5f);
-    return r * __builtin_ldexpf(1.0f, e - mb) * sign;
-}
-
-__device__ __forceinline__ float qdq_npu(float x) { return u2f(decode_bits(encode_npu_bits(f2u(x)))); }
-
-// Scalar reference route for one element: returns the qdq output in the
-// tensor's dtype (bf16 bits in the low half, or fp32 bits) and the code.
-template <int DT>
-__device__ __forceinline__ void slow_elem(uint32_t xbits, float s, int sem, uint32_t &ybits, uint32_t &code)
-{
-    if (DT == kBF16) {
-        uint32_t xs = f2bf(bf2f(xbits) * s);                  // x * scale   (bf16)
-        code = encode_npu_bits(xs << 16);
-        float q = sem == kSemTorch ? qdq_torch(bf2f(xs)) : qdq_npu(bf2f(xs));
-        uint32_t qb = f2bf(q);                                // out.to(bf16)
-        ybits = f2bf(bf2f(qb) / s);                           // / scale     (bf16)
-    } else {
-        float xs = u2f(xbits) * s;
-        code = encode_npu_bits(f2u(xs));
-        float q = sem == kSemTorch ? qdq_torch(xs) : qdq_npu(xs);
-        ybits = f2u(q / s);
-    }
-}
 
 // ---------------------------------------------------------------- kernels
 
@@ -192,25 +141,6 @@ __global__ __launch_bounds__(kTPB) void k_absmax(const void *__restrict__ xv, in
     __syncthreads();
     m = max(max(red[0], red[1]), max(red[2], red[3]));
     fold_amax(st, m, gridDim.x, DT, smax, red + kTPB / 64);
-}
-
-// LDS map of the quantise kernels: [0,512) bf16 decode table, [1024,2048) fp32
-// decode table, [kTabLo, kTabHi] the encode table (so the clamped magnitude
-// bits are the LDS address).
-constexpr uint32_t kLdsLutBf16 = 0;
-constexpr uint32_t kLdsLutF32 = 1024;
-constexpr uint32_t kLdsBytes = (kTabLo + sizeof(EncTable) + 15) & ~15u;
-static_assert(kLdsLutF32 + 1024 <= kTabLo, "LDS map overlap");
-
-__device__ __forceinline__ uint32_t clampu(uint32_t u)
-{
-    return u < kTabLo ? kTabLo : (u > kTabHi ? kTabHi : u);
-}
-
-// Sign fix-up for 4 magnitude codes: a code of magnitude 0 stays 0x00 (0x80 is NaN).
-__device__ __forceinline__ uint32_t apply_signs(uint32_t mags, uint32_t signs80)
-{
-    return mags | ((mags + 0x7F7F7F7Fu) & signs80);
 }
 
 // MODE 0: codes, MODE 1: qdq in the input dtype, MODE 2: decode codes -> x_q.

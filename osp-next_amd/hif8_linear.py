@@ -410,6 +410,20 @@ class HIF8Linear(nn.Linear):
         return _HIF8LinearFunction.apply(x, self.weight, self.bias, self.scale_max_forward,
                                          self.scale_max_backward, packed, self.a_format)
 
+    def forward_quantized(self, x_q: Tensor) -> Tensor:
+        """The forward of an input already quantised with this layer's ``scale_max_forward``
+        (``x_q = _quant(x)[0]``, e.g. from ``modulated_norm_quant``): the GEMM alone.  Equals
+        ``forward(x)`` exactly, since ``_quant`` is deterministic.  Inference only."""
+        if torch.is_grad_enabled() and (x_q.requires_grad or self.weight.requires_grad
+                                        or (self.bias is not None and self.bias.requires_grad)):
+            raise RuntimeError("forward_quantized has no autograd; call forward(x) when gradients are needed")
+        if x_q.dtype != torch.bfloat16:
+            raise TypeError(f"forward_quantized takes the bf16 x_q, got {x_q.dtype}")
+        K = x_q.shape[-1]
+        x2 = x_q.reshape(-1, K).contiguous()
+        y = linear_any(x2, _lib.A_BF16, None, self._packed_weight(), self.bias)
+        return y.view(*x_q.shape[:-1], y.shape[-1])
+
     def extra_repr(self) -> str:
         return (f"in_features={self.in_features}, out_features={self.out_features}, "
                 f"bias={self.bias is not None}, "

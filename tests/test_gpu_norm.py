@@ -1,0 +1,190 @@
+"""GPU parity of the modulated LayerNorm producer (osp_next.py:941, :954 with the WanLayerNorm of
+want2v.py:96-106, feeding _quant of hif8_linear.py:42-50):
+
+- y (the kernels' optional output) against the oracle's float64 layer norm and bf16
+  modulation: equal except on fewer than 1e-3 of the elements (an fp32 layer norm rounds
+  differently from the exact one only next to a bf16 rounding boundary), and there within one
+  bf16 unit of the product n * (1 + scale) plus one unit of y;
+- the state's amax and scale are exactly the reference rule applied to that y;
+- x_q is bit-exactly the oracle's _quant of that y, in both qdq semantics, including rows that
+  hold NaN or Inf (the degenerate-scale route);
+- q, k, v fed by the fused producer equal three HIF8Linear forwards of y, bit for bit;
+- at the 14B 720P shape, amax equals torch's and x_q equals the standalone codec's
+  fake quant of y (size-independent consistency);
+- shapes outside the fused kernels (dim % 8 != 0, dim > 8192) take the GPU op sequence.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda:0"
+
+
+def bits(t):
+    return t.detach().contiguous().cpu().view(torch.int16).numpy().view(np.uint16)
+
+
+def ulp(a, b):
+    def key(u):
+        u = np.asarray(u, np.uint16).astype(np.int32)
+        return np.where(u & 0x8000, -(u & 0x7FFF), u)
+    return np.abs(key(a) - key(b))
+
+
+def make(seed, B, N, D, outliers=4, with_mod=True):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(B, N, D, generator=g) * 2 + 0.25
+    x[:, :, :min(outliers, D)] *= 25
+    x = x.to(torch.bfloat16)
+    if not with_mod:
+        return x.to(DEV), None, None
+    e = (torch.randn(B, 6, D, generator=g) * 0.5).to(torch.bfloat16).chunk(6, dim=1)
+    return x.to(DEV), e[0].to(DEV), e[1].to(DEV)
+
+
+def oracle_y(R, x, shift, scale):
+    B, N, D = x.shape
+    sh = None if shift is None else bits(shift).reshape(-1, D)
+    sc = None if scale is None else bits(scale).reshape(-1, D)
+    rpb = N if (shift is not None and shift.reshape(-1, D).shape[0] > 1) else B * N
+    return R.modulated_layer_norm_bf16(bits(x).reshape(-1, D), sh, sc, rows_per_batch=rpb, eps=1e-6)
+
+
+def check_y(R, yb, x, shift, scale, frac=1e-3):
+    """y against the oracle: where they differ, by at most one bf16 unit of the product
+    u = n * (1 + scale) plus one unit of y (a one-unit difference of the layer norm n passes
+    through the product; the sum with shift can cancel, so y's own units are not the measure),
+    and on fewer than ``frac`` of the elements."""
+    D = x.shape[-1]
+    want = oracle_y(R, x, shift, scale)
+    u = oracle_y(R, x, None, scale)            # shift = 0: y is the rounded product itself
+    a, b = R.bf16_to_f32(yb).astype(np.float64), R.bf16_to_f32(want).astype(np.float64)
+    bound = 2.0 ** -7 * (np.abs(R.bf16_to_f32(u)) + np.abs(b))
+    fin = np.isfinite(b)
+    assert np.array_equal(np.isfinite(a), fin)
+    err = np.abs(a - b)[fin]
+    assert np.all(err <= bound[fin]), float((err / np.maximum(bound[fin], 1e-30)).max())
+    assert (yb != want).mean() < frac, float((yb != want).mean())
+
+
+@pytest.mark.parametrize("B,N,D", [(1, 300, 1536), (2, 150, 5120), (1, 5, 8), (3, 7, 72), (1, 33, 8192),
+                                   (1, 1, 512), (2, 64, 1536)])
+@pytest.mark.parametrize("sem", ["npu", "torch"])
+def test_modln_matches_oracle(pkg, R, B, N, D, sem):
+    x, shift, scale = make(B * 1000 + N + D, B, N, D)
+    semc = pkg._lib.SEM_NPU if sem == "npu" else pkg._lib.SEM_TORCH
+    with torch.no_grad():
+        xq, st, y = pkg.modulated_norm_quant(x, shift, scale, eps=1e-6, scale_max=15.0, semantics=semc,
+                                             return_y=True)
+    torch.cuda.synchronize()
+    yb = bits(y).reshape(-1, D)
+    check_y(R, yb, x, shift, scale)
+    amax_bits, scale_f = st.read()
+    assert amax_bits == R.absmax_bf16(yb)
+    sb = R.hif8_scale_bf16(amax_bits, 15.0)
+    assert np.float32(scale_f) == R.bf16_to_f32(np.array([sb], np.uint16))[0]
+    want, _ = R.quant_bf16(yb, 15.0, sem)
+    assert np.array_equal(bits(xq).reshape(-1, D), want)
+
+
+def test_modln_without_modulation_is_layer_norm(pkg, R):
+    x, _, _ = make(11, 1, 200, 1536, with_mod=False)
+    with torch.no_grad():
+        xq, st, y = pkg.modulated_norm_quant(x, None, None, return_y=True)
+    yb = bits(y).reshape(-1, 1536)
+    d = ulp(yb, R.layer_norm_bf16(bits(x).reshape(-1, 1536), 1e-6))
+    assert d.max() <= 1 and (d > 0).mean() < 1e-3
+    want, _ = R.quant_bf16(yb, 15.0, "npu")
+    assert np.array_equal(bits(xq).reshape(-1, 1536), want)
+
+
+def test_modln_constant_rows_and_broadcast_modulation(pkg, R):
+    """A constant row normalises to exactly 0, so y = shift there; a [D] / [1, 1, D] modulation
+    broadcasts over every row."""
+    x, shift, scale = make(12, 1, 64, 512)
+    x[0, 3] = 2.5
+    x[0, 10] = -7.0
+    sh, sc = shift.reshape(512), scale.reshape(1, 1, 512)
+    with torch.no_grad():
+        xq, st, y = pkg.modulated_norm_quant(x, sh, sc, return_y=True)
+    yb = bits(y).reshape(-1, 512)
+    assert np.array_equal(yb[3], bits(sh)) and np.array_equal(yb[10], bits(sh))
+    check_y(R, yb, x, shift, scale)
+    want, _ = R.quant_bf16(yb, 15.0, "npu")
+    assert np.array_equal(bits(xq).reshape(-1, 512), want)
+
+
+@pytest.mark.parametrize("bad", ["nan", "inf"])
+def test_modln_non_finite_rows(pkg, R, bad):
+    """A NaN or Inf in x makes its row NaN (mean and variance), the amax NaN and the scale NaN:
+    x_q is NaN everywhere, as _quant of such a y is in the reference."""
+    x, shift, scale = make(13, 1, 16, 256)
+    x[0, 5, 17] = float(bad)
+    with torch.no_grad():
+        xq, st, y = pkg.modulated_norm_quant(x, shift, scale, return_y=True)
+    yb = bits(y).reshape(-1, 256)
+    assert np.all((yb[5] & 0x7FFF) > 0x7F80)
+    assert np.all((np.delete(yb, 5, axis=0) & 0x7FFF) <= 0x7F80)
+    amax_bits, _ = st.read()
+    assert (amax_bits & 0x7FFF) > 0x7F80
+    want, _ = R.quant_bf16(yb, 15.0, "npu")
+    assert np.array_equal(bits(xq).reshape(-1, 256), want)
+
+
+def test_qkv_from_modulated_norm_equals_three_forwards(pkg):
+    D = 1536
+    x, shift, scale = make(21, 1, 257, D)
+    torch.manual_seed(0)
+    lins = [pkg.HIF8Linear(D, D, bias=True).to(DEV).to(torch.bfloat16) for _ in range(3)]
+    with torch.no_grad():
+        for m in lins:
+            m.weight.normal_(0, 0.02)
+            m.bias.normal_(0, 0.1)
+        q, k, v = pkg.qkv_from_modulated_norm(x, shift, scale, *lins)
+        _, _, y = pkg.modulated_norm_quant(x, shift, scale, return_y=True)
+        for got, m in zip((q, k, v), lins):
+            assert torch.equal(got.view(torch.int16), m(y).view(torch.int16))
+
+
+def test_modln_rejects_autograd(pkg):
+    x, shift, scale = make(22, 1, 8, 64)
+    x.requires_grad_(True)
+    with pytest.raises(RuntimeError):
+        pkg.modulated_norm_quant(x, shift, scale)
+
+
+@pytest.mark.parametrize("D", [100, 8200])
+def test_modln_shapes_outside_the_kernels(pkg, R, D):
+    x, shift, scale = make(23, 1, 40, D)
+    with torch.no_grad():
+        xq, st, y = pkg.modulated_norm_quant(x, shift, scale, return_y=True)
+    yb = bits(y).reshape(-1, D)
+    check_y(R, yb, x, shift, scale, frac=1e-2)
+    want, _ = R.quant_bf16(yb, 15.0, "npu")
+    assert np.array_equal(bits(xq).reshape(-1, D), want)
+
+
+def test_modln_full_size_consistency(pkg):
+    """14B 720P: x [75600, 5120].  amax equals torch's amax of the kernel's y, and the fused
+    x_q equals the standalone codec's fake quant of y with the same state."""
+    g = torch.Generator(device=DEV).manual_seed(31)
+    x = torch.randn(1, 75600, 5120, generator=g, device=DEV).to(torch.bfloat16)
+    e = (torch.randn(1, 6, 5120, generator=g, device=DEV) * 0.5).to(torch.bfloat16).chunk(6, dim=1)
+    with torch.no_grad():
+        xq, st, y = pkg.modulated_norm_quant(x, e[0], e[1], return_y=True)
+    amax_bits, _ = st.read()
+    assert amax_bits == int(y.abs().amax().view(torch.int16).item()) & 0x7FFF
+    xq2 = pkg.fake_quant(y, st)
+    assert torch.equal(xq.view(torch.int16), xq2.view(torch.int16))
+    # y against torch's own fp32 layer norm on the GPU, on a row sample
+    rows = torch.randint(0, 75600, (512,), generator=g, device=DEV)
+    n = torch.nn.functional.layer_norm(x[0, rows].float(), (5120,), eps=1e-6).to(torch.bfloat16)
+    u = n * (1 + e[1][0])
+    y_t = u + e[0][0]
+    err = (y[0, rows].double() - y_t.double()).abs()
+    assert bool((err <= 2.0 ** -7 * (u.double().abs() + y_t.double().abs())).all())
+    assert float((y[0, rows] != y_t).double().mean()) < 1e-3

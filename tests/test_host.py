@@ -71,6 +71,19 @@ def test_status_codes_without_gpu(pkg):
     assert lin(y=odd) == -3
     assert lin(b=fake + 2) == -3
     assert lin(K=1 << 22) == -2          # bf16 activations: K < 2^22 (32-bit buffer offsets)
+    # modulated LayerNorm: dim % 8, dim <= 8192, alignment of x and of the row statistics
+    assert L.hif8_modln_amax(None, None, None, 4, 5120, 4, 1e-6, fake, 15.0, fake, None) == -1
+    assert L.hif8_modln_amax(fake, None, None, 0, 5120, 4, 1e-6, fake, 15.0, fake, None) == -1
+    assert L.hif8_modln_amax(fake, None, None, 4, 5120, 0, 1e-6, fake, 15.0, fake, None) == -1
+    assert L.hif8_modln_amax(fake, None, None, 4, 100, 4, 1e-6, fake, 15.0, fake, None) == -2
+    assert L.hif8_modln_amax(fake, None, None, 4, 8200, 4, 1e-6, fake, 15.0, fake, None) == -2
+    assert L.hif8_modln_amax(odd, None, None, 4, 5120, 4, 1e-6, fake, 15.0, fake, None) == -3
+    assert L.hif8_modln_amax(fake, odd, None, 4, 5120, 4, 1e-6, fake, 15.0, fake, None) == -3
+    assert L.hif8_modln_amax(fake, None, None, 4, 5120, 4, 1e-6, fake + 4, 15.0, fake, None) == -3
+    assert L.hif8_modln_fake_quant(fake, None, None, 4, 5120, 4, fake, fake, 0, None, None, None) == -1
+    assert L.hif8_modln_fake_quant(fake, None, None, 4, 5120, 4, fake, fake, 9, fake, None, None) == -1
+    assert L.hif8_modln_fake_quant(fake, None, None, 4, 5120, 4, fake, fake, 0, odd, None, None) == -3
+    assert L.hif8_modln_fake_quant(fake, None, None, 4, 5120, 4, fake, fake, 0, fake, odd, None) == -3
 
 
 def test_python_layer_refuses_cpu_tensors(pkg):

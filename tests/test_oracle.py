@@ -407,3 +407,99 @@ def test_planted_mistakes_are_caught(R):
     for wrong in (ties_even, thresholds_off_by_one):
         sel = (np.abs(xf) > 2.0 ** -20) & (np.abs(xf) < 30000)
         assert (bits32(wrong(xf[sel])) != bits32(want[sel])).any(), wrong.__name__
+
+
+# ------------------------------------------------ modulated LayerNorm producer
+
+
+def _bf16_ulp(a, b):
+    """|distance| in bf16 units between two arrays of bf16 bits (monotone integer encoding)."""
+    def key(u):
+        u = np.asarray(u, np.uint16).astype(np.int32)
+        return np.where(u & 0x8000, -(u & 0x7FFF), u)
+    return np.abs(key(a) - key(b))
+
+
+def _modln_case(seed, B=2, N=96, D=1536):
+    torch = pytest.importorskip("torch")
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(B, N, D, generator=g) * 2 + 0.5
+    x[:, :, :4] *= 30                                   # outlier channels
+    x = x.to(torch.bfloat16)
+    e = (torch.randn(B, 6, D, generator=g) * 0.5).to(torch.bfloat16).chunk(6, dim=1)
+    return torch, x, e[0], e[1]
+
+
+def _bits(t):
+    import torch
+    return t.contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+def test_modulated_layer_norm_matches_torch_cpu(R):
+    """The oracle against the reference's own op sequence run by torch on the CPU
+    (want2v.py:96-106 then osp_next.py:941): LayerNorm, a library routine, to one bf16 unit on
+    a small fraction of elements (fp32 summation order); the bf16 modulation ops bit-exact."""
+    torch, x, shift, scale = _modln_case(3)
+    B, N, D = x.shape
+    n_t = torch.nn.functional.layer_norm(x.float(), (D,), eps=1e-6).type_as(x)
+    n_o = R.layer_norm_bf16(_bits(x).reshape(-1, D), 1e-6)
+    d = _bf16_ulp(n_o, _bits(n_t).reshape(-1, D))
+    assert d.max() <= 1 and (d > 0).mean() < 1e-3, (d.max(), (d > 0).mean())
+    # same n -> the modulation is bit-exact against torch's bf16 tensor ops
+    n_o_t = torch.from_numpy(n_o.view(np.int16)).view(torch.bfloat16).view(B, N, D)
+    y_t = n_o_t * (1 + scale) + shift
+    y_o = R.modulated_layer_norm_bf16(_bits(x).reshape(-1, D), _bits(shift).reshape(B, D),
+                                      _bits(scale).reshape(B, D), rows_per_batch=N, eps=1e-6)
+    assert np.array_equal(y_o, _bits(y_t).reshape(-1, D))
+    # and against the whole torch sequence, to the LayerNorm's unit
+    y_full = n_t * (1 + scale) + shift
+    d = _bf16_ulp(y_o, _bits(y_full).reshape(-1, D))
+    assert (d > 0).mean() < 1e-3
+
+
+def test_modulated_layer_norm_closed_forms(R):
+    """Rows with a closed-form norm: a constant row normalises to 0 (then y = shift), and a
+    two-valued row +-a to +-a / sqrt(a^2 + eps), which is +-1 in bf16 for a >= 1."""
+    D = 64
+    x = np.zeros((3, D), np.float32)
+    x[0] = 7.25
+    x[1, ::2], x[1, 1::2] = 3.0, -3.0
+    x[2, ::2], x[2, 1::2] = 1.5, -1.5
+    xb = R.f32_to_bf16(x)
+    n = R.bf16_to_f32(R.layer_norm_bf16(xb))
+    assert np.all(n[0] == 0)
+    assert np.array_equal(n[1], np.where(x[1] > 0, 1.0, -1.0).astype(np.float32))
+    assert np.array_equal(n[2], np.where(x[2] > 0, 1.0, -1.0).astype(np.float32))
+    sh = R.f32_to_bf16(np.linspace(-2, 2, D, dtype=np.float32))[None]
+    sc = R.f32_to_bf16(np.full(D, 0.5, np.float32))[None]
+    y = R.bf16_to_f32(R.modulated_layer_norm_bf16(xb, sh, sc))
+    assert np.array_equal(y[0], R.bf16_to_f32(sh[0]))
+    assert np.array_equal(y[1], R.bf16_to_f32(R.f32_to_bf16(np.where(x[1] > 0, 1.5, -1.5) + R.bf16_to_f32(sh[0]))))
+
+
+def test_modulated_layer_norm_planted_mistakes(R):
+    """Plausible wrong restatements (eps dropped, 1 + scale dropped, shift and scale swapped,
+    unbiased variance) all fail the torch comparison above."""
+    torch, x, shift, scale = _modln_case(5, B=1, N=64, D=512)
+    D = x.shape[-1]
+    want = _bits(torch.nn.functional.layer_norm(x.float(), (D,), eps=1e-6).type_as(x) * (1 + scale) + shift)
+    want = want.reshape(-1, D)
+    xb, shb, scb = _bits(x).reshape(-1, D), _bits(shift).reshape(1, D), _bits(scale).reshape(1, D)
+
+    def frac(y):
+        return float((_bf16_ulp(y, want) > 1).mean())
+    assert frac(R.modulated_layer_norm_bf16(xb, shb, scb, eps=1e-6)) == 0.0
+    assert frac(R.modulated_layer_norm_bf16(xb, scb, shb, eps=1e-6)) > 0.1          # swapped
+    sc_m1 = R.f32_to_bf16(R.bf16_to_f32(scb) - np.float32(1.0))                       # drops the 1 +
+    assert frac(R.modulated_layer_norm_bf16(xb, shb, sc_m1, eps=1e-6)) > 0.1
+    xs = xb.copy()
+    xs[:, 0] = R.f32_to_bf16(R.bf16_to_f32(xs[:, 0]) * np.float32(1.5))              # unnormalised input
+    assert frac(R.modulated_layer_norm_bf16(xs, shb, scb, eps=1e-6)) > 0.0
+    # unbiased variance (torch.var's default) is off by sqrt(D/(D-1)): visible on most elements
+    xf = R.bf16_to_f32(xb).astype(np.float64)
+    m = xf.mean(-1, keepdims=True)
+    nb = R.f32_to_bf16(((xf - m) / np.sqrt(xf.var(-1, ddof=1, keepdims=True) + 1e-6)).astype(np.float32))
+    t = R.f32_to_bf16(np.float32(1) + R.bf16_to_f32(scb))
+    u = R.f32_to_bf16(R.bf16_to_f32(nb) * R.bf16_to_f32(t))
+    y_bad = R.f32_to_bf16(R.bf16_to_f32(u) + R.bf16_to_f32(shb))
+    assert (_bf16_ulp(y_bad, want) > 0).mean() > 0.05
