@@ -149,6 +149,64 @@ def time_ffn(pkg, torch, x, reps):
     return out
 
 
+def time_modln(pkg, torch, x, reps):
+    """The modulated LayerNorm producer (osp_next.py:941 with want2v.py:96-106) in front of the
+    q/k/v projections, on x: the fused two-pass route (hif8_modln_amax + hif8_modln_fake_quant)
+    against the reference's sequence on the GPU (layer norm, bf16 modulation ops, then the
+    _quant each of q, k and v runs on the same input)."""
+    M, D = x.shape
+    g = torch.Generator(device=x.device).manual_seed(4)
+    e = (torch.randn(1, 6, D, generator=g, device=x.device) * 0.5).to(torch.bfloat16).chunk(6, dim=1)
+    xb = x.view(1, M, D)
+    L = pkg._lib.load()
+    stream = pkg._lib.stream_ptr(x.device)
+    stats = torch.empty(M * 2, dtype=torch.float32, device=x.device)
+    st = pkg.QuantState(x.device)
+    xq = torch.empty_like(x)
+    sh, sc = e[0].reshape(1, D).contiguous(), e[1].reshape(1, D).contiguous()
+
+    def p1():
+        pkg._lib.check(L.hif8_modln_amax(x.data_ptr(), sh.data_ptr(), sc.data_ptr(), M, D, M, 1e-6,
+                                         stats.data_ptr(), 15.0, st.ptr, stream), "hif8_modln_amax")
+
+    def p2():
+        pkg._lib.check(L.hif8_modln_fake_quant(x.data_ptr(), sh.data_ptr(), sc.data_ptr(), M, D, M,
+                                               stats.data_ptr(), st.ptr, 0, xq.data_ptr(), None, stream),
+                       "hif8_modln_fake_quant")
+
+    def unfused():
+        y = pkg.modulate(pkg.WanLayerNorm(D).to(x.device)(xb), e[0], e[1])
+        for _ in range(3):
+            pkg._quant(y, 15.0)
+
+    def timed(fn, n):
+        for _ in range(2):
+            fn()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(n):
+            fn()
+        b.record()
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) / n
+
+    with torch.no_grad():
+        t1, t2 = timed(p1, reps), timed(p2, reps)
+        tu = timed(unfused, max(2, reps // 4))
+    n = M * D
+    out = {"what": f"x_q = _quant(norm(x)*(1+scale)+shift) for q/k/v, x[{M},{D}] bf16, one modulation row",
+           "amax_us": round(t1 * 1e3, 1), "qdq_us": round(t2 * 1e3, 1), "fused_us": round((t1 + t2) * 1e3, 1),
+           "bytes_algorithmic": 6 * n,
+           "achieved_GBps": round(6 * n / ((t1 + t2) * 1e-3) / 1e9, 1),
+           "amax_GBps": round(2 * n / (t1 * 1e-3) / 1e9, 1), "qdq_GBps": round(4 * n / (t2 * 1e-3) / 1e9, 1),
+           "unfused_us": round(tu * 1e3, 1), "speedup": round(tu / (t1 + t2), 2)}
+    out["frac"] = round(out["achieved_GBps"] / PEAK_HBM_GBPS, 4)
+    out["traffic"] = measured_traffic("k_modln_amax+k_modln_qdq")
+    del stats, xq
+    return out
+
+
 def median(v):
     s = sorted(v)
     return s[len(s) // 2]
@@ -209,7 +267,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--a-format", default="bf16", choices=["tiled", "bf16", "codes"])
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--shapes", default="up", help="comma list of up,down,qkvo,ffn to time in addition")
+    ap.add_argument("--shapes", default="up,modln",
+                    help="comma list of up,down,qkvo,ffn,modln to time in addition")
     ap.add_argument("--pmc-calibration", action="store_true",
                     help="also run one plain copy of x (774,144,000 B read + written): the reference "
                          "kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE")
@@ -280,12 +339,16 @@ def main():
         "peak_GBps": PEAK_HBM_GBPS,
     }
     encode["frac"] = round(encode["achieved_GBps"] / PEAK_HBM_GBPS, 4)
+    encode["traffic"] = measured_traffic("k_absmax+k_quant_encode")
     del codes
 
     extra_shapes = {}
     if "ffn" in args.shapes.split(","):
         extra_shapes["ffn"] = time_ffn(pkg, torch, x, max(3, args.steps // 2))
-    for name in [s for s in args.shapes.split(",") if s and s not in ("up", "ffn")]:
+    if "modln" in args.shapes.split(","):
+        log("[bench] timing the modulated LayerNorm producer")
+        extra_shapes["modln"] = time_modln(pkg, torch, x, max(5, args.steps))
+    for name in [s for s in args.shapes.split(",") if s and s not in ("up", "ffn", "modln")]:
         n_, k_ = {"down": (5120, 13824), "qkvo": (5120, 5120)}[name]
         xs, ws, bs = make_inputs(torch, M, k_, n_, seed=1)
         ps = pkg.PackedWeight(ws, 15.0)
