@@ -207,6 +207,46 @@ def time_modln(pkg, torch, x, reps):
     return out
 
 
+def time_qkv(pkg, torch, x, reps):
+    """The self-attention q/k/v projections (osp_next.py:742-744, 3 x [5120 -> 5120]) on the same
+    x_q: one grouped launch (hif8_linear_fwd_grouped) against three single-weight launches."""
+    M, K = x.shape
+    g = torch.Generator(device=x.device).manual_seed(5)
+    packs, biases = [], []
+    for _ in range(3):
+        w = (torch.randn(K, K, generator=g, device=x.device) * 0.02).to(torch.bfloat16)
+        packs.append(pkg.PackedWeight(w, 15.0))
+        biases.append((torch.randn(K, generator=g, device=x.device) * 0.1).to(torch.bfloat16))
+        del w
+    gw = pkg.GroupedWeight(packs, biases)
+    a, fmt, st = pkg.quantize_activation(x, 15.0, "bf16")
+
+    def grouped():
+        return pkg.linear_fwd_grouped(a, gw)
+
+    def separate():
+        return [pkg.linear_fwd(a, fmt, st, p, b) for p, b in zip(packs, biases)]
+
+    out = {}
+    for label, fn in (("grouped", grouped), ("separate", separate)):
+        for _ in range(2):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        out[f"{label}_ms"] = round(e0.elapsed_time(e1) / reps, 4)
+    flops = 3 * 2.0 * M * K * K
+    out["grouped_TFLOPs"] = round(flops / (out["grouped_ms"] * 1e-3) / 1e12, 1)
+    out["separate_TFLOPs"] = round(flops / (out["separate_ms"] * 1e-3) / 1e12, 1)
+    out["what"] = f"q, k, v [5120 -> 5120] on x_q[{M},{K}], one grouped launch vs three launches"
+    del gw, packs, a
+    return out
+
+
 def median(v):
     s = sorted(v)
     return s[len(s) // 2]
@@ -267,8 +307,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--a-format", default="bf16", choices=["tiled", "bf16", "codes"])
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--shapes", default="up,modln",
-                    help="comma list of up,down,qkvo,ffn,modln to time in addition")
+    ap.add_argument("--shapes", default="up,modln,qkv",
+                    help="comma list of up,down,qkvo,ffn,modln,qkv to time in addition")
     ap.add_argument("--pmc-calibration", action="store_true",
                     help="also run one plain copy of x (774,144,000 B read + written): the reference "
                          "kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE")
@@ -348,7 +388,10 @@ def main():
     if "modln" in args.shapes.split(","):
         log("[bench] timing the modulated LayerNorm producer")
         extra_shapes["modln"] = time_modln(pkg, torch, x, max(5, args.steps))
-    for name in [s for s in args.shapes.split(",") if s and s not in ("up", "ffn", "modln")]:
+    if "qkv" in args.shapes.split(","):
+        log("[bench] timing the grouped q/k/v projections")
+        extra_shapes["qkv"] = time_qkv(pkg, torch, x, max(3, args.steps // 4))
+    for name in [s for s in args.shapes.split(",") if s and s not in ("up", "ffn", "modln", "qkv")]:
         n_, k_ = {"down": (5120, 13824), "qkvo": (5120, 5120)}[name]
         xs, ws, bs = make_inputs(torch, M, k_, n_, seed=1)
         ps = pkg.PackedWeight(ws, 15.0)

@@ -123,6 +123,22 @@ int hif8_linear_fwd(const void *a, int a_fmt, const void *a_state, const uint8_t
                     const void *w_state, const uint16_t *bias, uint16_t *y, int64_t M,
                     int64_t N, int64_t K, hif8_stream_t stream);
 
+/* Several HIF8Linear layers on the same quantised input in one launch: the self-attention
+ * q, k, v projections of osp_next.py:742-744 (each an F.linear(x_q, w_q, b) of
+ * hif8_linear.py:86 on the same x_q), or any such set.  Each group i is its own weight
+ * (its own state, hence its own scale) and output:
+ *     ys[i][M, ns[i]] = x_q[M, K] . w_q_i[ns[i], K]^T + bias_i
+ * a is bf16 x_q; w_codes holds the groups' codes concatenated along the output features
+ * ([sum ns, K]); bias is NULL or the groups' biases concatenated ([sum ns]).  w_states, ys
+ * and ns are host arrays of `groups` entries (1 <= groups <= 8).  Every ns[i] is a multiple
+ * of 8 and, except the last, of 256 (a tile never spans two groups).  K % 64 == 0,
+ * K < 2^22; a, w_codes and each ys[i] 16-byte aligned, bias 8-byte aligned.  The result of
+ * each group equals hif8_linear_fwd of that group alone, bit for bit.
+ * No single reference function: it merges the reference's separate linears of one input. */
+int hif8_linear_fwd_grouped(const void *a, const uint8_t *w_codes, const void *const *w_states,
+                            const uint16_t *bias, uint16_t *const *ys, const int64_t *ns, int groups,
+                            int64_t M, int64_t K, hif8_stream_t stream);
+
 /* Producer fusion for nn.Sequential(HIF8Linear, GELU(tanh), HIF8Linear)
  * (osp_next.py:873-877): hif8_linear_fwd with bf16 activations whose epilogue applies
  *   y = rnd_bf16(gelu_tanh(rnd_bf16(x_q @ w_q^T + bias)))

@@ -38,9 +38,12 @@ from .hif8_linear import (  # noqa: F401
     fused_shape_ok,
     linear_any,
     linear_fwd_gelu_amax,
+    GroupedWeight,
+    grouped_ok,
+    linear_fwd_grouped,
 )
 from .ffn import HIF8FFN  # noqa: F401
-from .norm import WanLayerNorm, modulate, modulated_norm_quant, qkv_from_modulated_norm  # noqa: F401
+from .norm import WanLayerNorm, grouped_weight, modulate, modulated_norm_quant, qkv_from_modulated_norm  # noqa: F401
 from .hif8_attention import (  # noqa: F401
     _HIF8QKVQuantFunction,
     attention_with_mask,
@@ -67,5 +70,5 @@ __all__ = [
     "scaled_dot_product_attention_with_mask", "LinearForward", "LinearForwardFast", "QLinear", "replace_linear",
     "save_packed", "load_packed", "pack_state_dict", "packed_from_codes", "fused_shape_ok", "linear_any",
     "linear_fwd_gelu_amax", "HIF8FFN", "WanLayerNorm", "modulate", "modulated_norm_quant",
-    "qkv_from_modulated_norm",
+    "qkv_from_modulated_norm", "GroupedWeight", "grouped_ok", "linear_fwd_grouped", "grouped_weight",
 ]

@@ -28,10 +28,25 @@ struct alignas(256) State {
 
 static_assert(sizeof(State) % 256 == 0, "state size");
 
+// The output features of a fused GEMM as consecutive groups, each its own weight (codes
+// concatenated along N, one state each) and output buffer [M, cols]: several linears on the
+// same activation in one launch.  Every group but the last covers whole 256-wide tiles.
+constexpr int kMaxGroups = 8;
+struct Groups {
+    int n;                        // number of groups (1 for a single linear)
+    int tile_end[kMaxGroups];     // exclusive end of each group in 256-wide n-tiles
+    int cols[kMaxGroups];         // output features of each group (its output row stride)
+    const State *st[kMaxGroups];  // decode state of each group's weight
+    uint16_t *y[kMaxGroups];      // output of each group
+};
+
 // Fused GEMM for bf16 activations (hif8_gemm_dtl.hip); the caller has checked shapes and
 // alignment as hif8_linear_fwd documents.  With y_st, the GELU + amax epilogue.
 int launch_linear_dtl(const uint16_t *x, const uint8_t *w_codes, const State *w_st, const uint16_t *bias,
                       uint16_t *y, int64_t M, int64_t N, int64_t K, hif8_stream_t stream, State *y_st = nullptr,
                       float y_smax = 0.0f);
+// The grouped form: N is the total of the groups' features.
+int launch_linear_dtl_groups(const uint16_t *x, const uint8_t *w_codes, const Groups &g, const uint16_t *bias,
+                             int64_t M, int64_t N, int64_t K, hif8_stream_t stream);
 
 }  // namespace hif8

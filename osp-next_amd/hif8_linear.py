@@ -19,7 +19,8 @@ plain bf16 product on already-decoded operands and goes to the vendor GEMM.
 """
 from __future__ import annotations
 
-from typing import Optional, Tuple
+import ctypes
+from typing import List, Optional, Tuple
 
 import torch
 import torch.nn as nn
@@ -241,6 +242,61 @@ def linear_fwd(a: Tensor, a_fmt: int, a_state: Optional[QuantState], w: PackedWe
                                            w.codes.data_ptr(), w.state.ptr, b_ptr or None, y.data_ptr(),
                                            M, N, K, _lib.stream_ptr(a.device)), "hif8_linear_fwd")
     return y
+
+
+MAX_GROUPS = 8
+
+
+def grouped_ok(packs: "List[PackedWeight]") -> bool:
+    """Weights hif8_linear_fwd_grouped takes together: same in_features (K % 64 == 0), every
+    out_features a multiple of 256 except the last (a multiple of 8), at most 8 of them."""
+    if not 1 <= len(packs) <= MAX_GROUPS:
+        return False
+    K = packs[0].shape[1]
+    if any(p.shape[1] != K for p in packs) or not fused_shape_ok(packs[-1].shape[0], K):
+        return False
+    return all(p.shape[0] % 256 == 0 for p in packs[:-1])
+
+
+class GroupedWeight:
+    """The weights of several HIF8Linear layers that read the same input, concatenated along the
+    output features (codes, and biases with zeros for a layer without one) for one launch of
+    hif8_linear_fwd_grouped.  Built from the layers' packed weights; ``key`` identifies them."""
+
+    def __init__(self, packs: "List[PackedWeight]", biases: "List[Optional[Tensor]]", key=None):
+        if not grouped_ok(packs):
+            raise ValueError("weights do not fit one grouped launch (see grouped_ok)")
+        self.packs = list(packs)
+        self.ns = [p.shape[0] for p in packs]
+        self.K = packs[0].shape[1]
+        self.codes = torch.cat([p.codes for p in packs], 0).contiguous()
+        if any(b is not None for b in biases):
+            dev = self.codes.device
+            self.bias = torch.cat([b.detach().to(torch.bfloat16).reshape(-1) if b is not None
+                                   else torch.zeros(n, dtype=torch.bfloat16, device=dev)
+                                   for b, n in zip(biases, self.ns)]).contiguous()
+        else:
+            self.bias = None
+        self.key = key
+
+
+def linear_fwd_grouped(a: Tensor, gw: GroupedWeight) -> "List[Tensor]":
+    """hif8_linear_fwd_grouped: ``[a @ w_q_i^T + b_i for each group]`` in one launch, each equal
+    bit for bit to linear_fwd of that weight alone.  ``a`` is the bf16 x_q [M, K]."""
+    M, K = a.shape
+    if K != gw.K:
+        raise ValueError(f"in_features mismatch: x has {K}, weights have {gw.K}")
+    if a.dtype != torch.bfloat16:
+        raise TypeError("the grouped GEMM takes the bf16 x_q")
+    ys = [torch.empty((M, n), dtype=torch.bfloat16, device=a.device) for n in gw.ns]
+    g = len(ys)
+    states = (ctypes.c_void_p * g)(*[p.state.ptr for p in gw.packs])
+    outs = (ctypes.c_void_p * g)(*[y.data_ptr() for y in ys])
+    ns = (ctypes.c_int64 * g)(*gw.ns)
+    _lib.check(_lib.load().hif8_linear_fwd_grouped(a.data_ptr(), gw.codes.data_ptr(), states,
+                                                   gw.bias.data_ptr() if gw.bias is not None else None, outs, ns,
+                                                   g, M, K, _lib.stream_ptr(a.device)), "hif8_linear_fwd_grouped")
+    return ys
 
 
 def linear_fwd_gelu_amax(a: Tensor, w: PackedWeight, bias: Optional[Tensor], y_state: QuantState,

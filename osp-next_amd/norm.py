@@ -21,7 +21,8 @@ import torch.nn as nn
 from torch import Tensor
 
 from . import _lib
-from .hif8_linear import HIF8Linear, QuantState, absmax_scale, fake_quant
+from .hif8_linear import (GroupedWeight, HIF8Linear, QuantState, absmax_scale, fake_quant, grouped_ok,
+                          linear_fwd_grouped)
 
 MAX_DIM = 8192
 
@@ -111,9 +112,32 @@ def modulated_norm_quant(x: Tensor, shift: Optional[Tensor] = None, scale: Optio
 def qkv_from_modulated_norm(x: Tensor, shift: Optional[Tensor], scale: Optional[Tensor], q: HIF8Linear,
                             k: HIF8Linear, v: HIF8Linear, eps: float = 1e-6) -> Tuple[Tensor, Tensor, Tensor]:
     """``q(y), k(y), v(y)`` for ``y = norm(x) * (1 + scale) + shift`` (osp_next.py:742-744 fed by :941)
-    with y quantised once.  Inference only; the three layers must share ``scale_max_forward``."""
+    with y quantised once and the three products in one grouped launch when the shapes allow
+    (each output bit-identical to the layer's own forward).  Inference only; the three layers
+    must share ``scale_max_forward``."""
     smf = q.scale_max_forward
     if k.scale_max_forward != smf or v.scale_max_forward != smf:
         raise ValueError("q, k and v quantise their input with different scale_max_forward")
     xq, _ = modulated_norm_quant(x, shift, scale, eps, smf)
-    return q.forward_quantized(xq), k.forward_quantized(xq), v.forward_quantized(xq)
+    gw = grouped_weight((q, k, v))
+    if gw is None:
+        return q.forward_quantized(xq), k.forward_quantized(xq), v.forward_quantized(xq)
+    K = xq.shape[-1]
+    ys = linear_fwd_grouped(xq.reshape(-1, K).contiguous(), gw)
+    return tuple(y.view(*xq.shape[:-1], y.shape[-1]) for y in ys)
+
+
+def grouped_weight(layers) -> Optional[GroupedWeight]:
+    """The layers' weights concatenated for one grouped launch (cached on the first layer and
+    rebuilt when any packed weight or bias changes), or None when they do not fit one."""
+    packs = [m._packed_weight() for m in layers]
+    if not grouped_ok(packs):
+        return None
+    key = tuple((id(p), None if m.bias is None else (m.bias.data_ptr(), m.bias._version))
+                for p, m in zip(packs, layers))
+    cached = getattr(layers[0], "_grouped_cache", None)
+    if cached is not None and cached.key == key:
+        return cached
+    gw = GroupedWeight(packs, [m.bias for m in layers], key)
+    layers[0]._grouped_cache = gw
+    return gw

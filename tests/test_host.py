@@ -71,6 +71,24 @@ def test_status_codes_without_gpu(pkg):
     assert lin(y=odd) == -3
     assert lin(b=fake + 2) == -3
     assert lin(K=1 << 22) == -2          # bf16 activations: K < 2^22 (32-bit buffer offsets)
+    # grouped linear: group count, shapes of the groups, alignment
+    P = ctypes.c_void_p
+    I64 = ctypes.c_int64
+
+    def grp(ns, sts=None, ys=None, a=fake, w=fake, b=None, K=512):
+        g = len(ns)
+        sts = (P * g)(*([fake] * g if sts is None else sts))
+        ys = (P * g)(*([fake] * g if ys is None else ys))
+        return L.hif8_linear_fwd_grouped(a, w, sts, b, ys, (I64 * g)(*ns), g, 128, K, None)
+    assert grp([256, 256, 264], a=None) == -1
+    assert L.hif8_linear_fwd_grouped(fake, fake, None, None, None, None, 0, 128, 512, None) == -1
+    assert grp([256] * 9) == -2                        # at most 8 groups
+    assert grp([264, 256]) == -2                       # all but the last a multiple of 256
+    assert grp([256, 260]) == -2                       # the last a multiple of 8
+    assert grp([256, 256], K=100) == -2
+    assert grp([256, 256], sts=[fake, None]) == -1
+    assert grp([256, 256], ys=[fake, odd]) == -3
+    assert grp([256, 256], b=fake + 2) == -3
     # modulated LayerNorm: dim % 8, dim <= 8192, alignment of x and of the row statistics
     assert L.hif8_modln_amax(None, None, None, 4, 5120, 4, 1e-6, fake, 15.0, fake, None) == -1
     assert L.hif8_modln_amax(fake, None, None, 0, 5120, 4, 1e-6, fake, 15.0, fake, None) == -1
