@@ -247,6 +247,116 @@ def time_qkv(pkg, torch, x, reps):
     return out
 
 
+def _dit_inputs(torch, dev, g, tokens, dim, L, text_dim=None):
+    x = torch.randn(1, tokens, dim, generator=g, device=dev).to(torch.bfloat16)
+    e = torch.randn(1, 6, dim, generator=g, device=dev).to(torch.bfloat16)
+    text = torch.randn(1, L, text_dim or dim, generator=g, device=dev).to(torch.bfloat16)
+    return x, e, text
+
+
+def _linear_flops(rows, dim, ffn, L):
+    """FLOPs of one block's linears: self q/k/v/o and cross q/o on the block's rows, cross k/v on
+    the text, FFN up/down."""
+    return 2.0 * rows * dim * dim * 6 + 2.0 * L * dim * dim * 2 + 2.0 * rows * dim * ffn * 2
+
+
+def time_block(pkg, torch, reps):
+    """one 14B block at 720P (x [1, 75600, 5120], grid 21x45x80 padded to 48
+    rows -> 4 x 20160 tokens), a Skiparse token block entered from full order, every linear HiF8
+    with prepacked weights, dense bf16 attention within the 4 strided sub-grids, cross-attention
+    over 512 text tokens.  Times the fused route and the reference-order route."""
+    D = pkg.dit
+    dev = torch.device("cuda:0")
+    dim, ffn, heads, grid, L = 5120, 13824, 40, (21, 45, 80), 512
+    torch.manual_seed(4)
+    blk = D.OSPNextAttentionBlock(dim, ffn, heads, cross_attn_norm=True, sparse_ratio=2,
+                                  skiparse_block_type="token", is_full2skiparse_block=True, quant="hif8",
+                                  device=dev)
+    g = torch.Generator(device=dev).manual_seed(4)
+    D.init_block_weights(blk, 0.02, g)
+    for m in blk.modules():
+        if isinstance(m, pkg.HIF8Linear):
+            m.prepack()
+    T, H, W = grid
+    x, e, text = _dit_inputs(torch, dev, g, T * H * W, dim, L)
+    rope = D.SkiparseRopeWrapper(D.rope_freqs(dim // heads).to(dev))
+    tm, _ = D.skiparse_masks(1, grid, 2, dev)
+    rows = int(tm.numel())
+
+    def run(fused):
+        with torch.no_grad():
+            return blk(x, tm, tm, e, grid, grid, rope, text, fused=fused)
+
+    out = {"what": "one 14B DiT block at 720P (token block from full order), all linears HiF8, "
+                   "prepacked weights, bf16 SDPA within the 2x2 strided sub-grids",
+           "tokens": T * H * W, "rows_padded": rows}
+    for fused in (True, False):
+        run(fused)
+        torch.cuda.synchronize()
+        ea, eb = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        ea.record()
+        for _ in range(reps):
+            run(fused)
+        eb.record()
+        torch.cuda.synchronize()
+        out["fused_ms" if fused else "reference_order_ms"] = round(ea.elapsed_time(eb) / reps, 3)
+    lf = _linear_flops(rows, dim, ffn, L)
+    n = rows // 4
+    valid = [int(tm[i].sum()) for i in range(4)]
+    af = sum(4.0 * n * v * dim for v in valid) + 4.0 * rows * L * dim
+    out["linear_TFLOP"] = round(lf / 1e12, 3)
+    out["attention_TFLOP"] = round(af / 1e12, 3)
+    out["TFLOPs_fused"] = round((lf + af) / (out["fused_ms"] * 1e-3) / 1e12, 1)
+    del blk, x, e, text
+    torch.cuda.empty_cache()
+    return out
+
+
+def time_step(pkg, torch, reps):
+    """the 40-block loop of a 14B OSP-Next denoising step at 768P native
+    (grid 21x48x84 = 84672 tokens, no padding), dual-end schedule with 8 full blocks, every
+    block linear HiF8 with prepacked weights, text 512 x 4096 through the (bf16) text embedding.
+    The patch/time embeddings and the head are not included (under 0.1 % of the FLOPs)."""
+    D = pkg.dit
+    dev = torch.device("cuda:0")
+    dim, ffn, heads, grid, L, text_dim = 5120, 13824, 40, (21, 48, 84), 512, 4096
+    torch.manual_seed(5)
+    stack = D.OSPNextBlocks(dim, ffn, heads, num_layers=40, num_full_blocks=8, quant="hif8", device=dev)
+    g = torch.Generator(device=dev).manual_seed(5)
+    D.init_block_weights(stack, 0.02, g)
+    for m in stack.modules():
+        if isinstance(m, pkg.HIF8Linear):
+            m.prepack(drop_weight=True)
+    torch.cuda.empty_cache()
+    text_embedding = torch.nn.Sequential(torch.nn.Linear(text_dim, dim), torch.nn.GELU(approximate="tanh"),
+                                         torch.nn.Linear(dim, dim)).to(dev, torch.bfloat16)
+    D.init_block_weights(text_embedding, 0.02, g)
+    T, H, W = grid
+    x, e, text_in = _dit_inputs(torch, dev, g, T * H * W, dim, L, text_dim)
+
+    def run():
+        with torch.no_grad():
+            return stack(x, e, text_embedding(text_in), grid)
+
+    run()
+    torch.cuda.synchronize()
+    ea, eb = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    ea.record()
+    for _ in range(reps):
+        run()
+    eb.record()
+    torch.cuda.synchronize()
+    ms = ea.elapsed_time(eb) / reps
+    rows = T * H * W
+    lf = 40 * _linear_flops(rows, dim, ffn, L)
+    out = {"what": "40-block loop of one 14B denoising step at 768P (dual-end, 8 full blocks), all block "
+                   "linears HiF8, prepacked weights", "tokens": rows, "ms_per_step": round(ms, 1),
+           "linear_TFLOP": round(lf / 1e12, 1), "linear_TFLOPs_over_step": round(lf / (ms * 1e-3) / 1e12, 1)}
+    del stack, x, e, text_in
+    torch.cuda.empty_cache()
+    return out
+
+
 def median(v):
     s = sorted(v)
     return s[len(s) // 2]
@@ -307,8 +417,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--a-format", default="bf16", choices=["tiled", "bf16", "codes"])
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--shapes", default="up,modln,qkv",
-                    help="comma list of up,down,qkvo,ffn,modln,qkv to time in addition")
+    ap.add_argument("--shapes", default="up,modln,qkv,block",
+                    help="comma list of up,down,qkvo,ffn,modln,qkv,block (config 4),step (config 5) "
+                         "to time in addition")
     ap.add_argument("--pmc-calibration", action="store_true",
                     help="also run one plain copy of x (774,144,000 B read + written): the reference "
                          "kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE")
@@ -391,7 +502,20 @@ def main():
     if "qkv" in args.shapes.split(","):
         log("[bench] timing the grouped q/k/v projections")
         extra_shapes["qkv"] = time_qkv(pkg, torch, x, max(3, args.steps // 4))
-    for name in [s for s in args.shapes.split(",") if s and s not in ("up", "ffn", "modln", "qkv")]:
+    if "block" in args.shapes.split(","):
+        log("[bench] timing one 14B DiT block at 720P (config 4)")
+        try:
+            extra_shapes["block"] = time_block(pkg, torch, 3)
+        except Exception as ex:  # the harness around the path (attention backend) may be missing
+            extra_shapes["block"] = {"error": repr(ex)}
+    if "step" in args.shapes.split(","):
+        log("[bench] timing the 40-block denoising step at 768P (config 5)")
+        try:
+            extra_shapes["step"] = time_step(pkg, torch, 2)
+        except Exception as ex:
+            extra_shapes["step"] = {"error": repr(ex)}
+    for name in [s for s in args.shapes.split(",")
+                 if s and s not in ("up", "ffn", "modln", "qkv", "block", "step")]:
         n_, k_ = {"down": (5120, 13824), "qkvo": (5120, 5120)}[name]
         xs, ws, bs = make_inputs(torch, M, k_, n_, seed=1)
         ps = pkg.PackedWeight(ws, 15.0)

@@ -10,6 +10,7 @@ Public surface, mirroring the reference:
   hif8_attention_with_mask, _HIF8QKVQuantFunction   (ospnext/modules/hif8_attention.py)
   QLinear, replace_linear                           (quant_cy_npu/layers/QLinear.py, utils/utils.py)
   WanLayerNorm                                      (ospnext/modules/want2v.py)
+  OSPNextAttentionBlock, OSPNextBlocks (dit)        (ospnext/modules/osp_next.py, the call sites)
 plus the tensor-level HIP ops (absmax_scale, encode, fake_quant, decode,
 linear_fwd), QuantState and PackedWeight.
 """
@@ -43,6 +44,8 @@ from .hif8_linear import (  # noqa: F401
     linear_fwd_grouped,
 )
 from .ffn import HIF8FFN  # noqa: F401
+from . import dit  # noqa: F401
+from .dit import OSPNextAttentionBlock, OSPNextBlocks  # noqa: F401
 from .norm import WanLayerNorm, grouped_weight, modulate, modulated_norm_quant, qkv_from_modulated_norm  # noqa: F401
 from .hif8_attention import (  # noqa: F401
     _HIF8QKVQuantFunction,
@@ -71,4 +74,5 @@ __all__ = [
     "save_packed", "load_packed", "pack_state_dict", "packed_from_codes", "fused_shape_ok", "linear_any",
     "linear_fwd_gelu_amax", "HIF8FFN", "WanLayerNorm", "modulate", "modulated_norm_quant",
     "qkv_from_modulated_norm", "GroupedWeight", "grouped_ok", "linear_fwd_grouped", "grouped_weight",
+    "dit", "OSPNextAttentionBlock", "OSPNextBlocks",
 ]

@@ -43,12 +43,25 @@ class HIF8FFN(nn.Sequential):
     def forward(self, x: Tensor) -> Tensor:
         if not self.fused_ok(x):
             return super().forward(x)
-        up, down = self[0], self[2]
         K = x.shape[-1]
-        x2 = x.reshape(-1, K).contiguous()
-        a, a_fmt, _ = quantize_activation(x2, up.scale_max_forward, "bf16")
-        y_st = QuantState(x2.device)
+        a, _, _ = quantize_activation(x.reshape(-1, K).contiguous(), self[0].scale_max_forward, "bf16")
+        return self._fused_from_xq(a).view(*x.shape[:-1], -1)
+
+    def forward_quantized(self, x_q: Tensor) -> Tensor:
+        """The FFN of an input already quantised with the up-projection's ``scale_max_forward``
+        (``x_q = _quant(x)[0]``, e.g. from ``modulated_norm_quant``): equals ``forward(x)``.
+        Inference only."""
+        if not self.fused_ok(x_q):
+            if torch.is_grad_enabled() and (x_q.requires_grad or any(p.requires_grad for p in self.parameters())):
+                raise RuntimeError("forward_quantized has no autograd; call forward(x) when gradients are needed")
+            return self[2](self[1](self[0].forward_quantized(x_q)))
+        K = x_q.shape[-1]
+        return self._fused_from_xq(x_q.reshape(-1, K).contiguous()).view(*x_q.shape[:-1], -1)
+
+    def _fused_from_xq(self, a: Tensor) -> Tensor:
+        """up with the GELU + amax epilogue, fake quant of its output with that state, down."""
+        up, down = self[0], self[2]
+        y_st = QuantState(a.device)
         y = linear_fwd_gelu_amax(a, up._packed_weight(), up.bias, y_st, down.scale_max_forward)
         yq = fake_quant(y, y_st)
-        out = linear_any(yq, _lib.A_BF16, None, down._packed_weight(), down.bias)
-        return out.view(*x.shape[:-1], out.shape[-1])
+        return linear_any(yq, _lib.A_BF16, None, down._packed_weight(), down.bias)
