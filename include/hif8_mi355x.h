@@ -47,7 +47,13 @@ enum {
     HIF8_ERR_HIP = -4,       /* a HIP runtime call or kernel launch failed */
 };
 
-enum { HIF8_DTYPE_BF16 = 0, HIF8_DTYPE_F32 = 1 };
+enum { HIF8_DTYPE_BF16 = 0, HIF8_DTYPE_F32 = 1, HIF8_DTYPE_BF16_AS_F32 = 2 };
+/* HIF8_DTYPE_BF16_AS_F32: a bf16 tensor quantised as the fp32 tensor x.float() holds it --
+ * fp32 amax, scale and arithmetic, an fp32 state.  This is the self-attention o input of the
+ * reference, whose fp32 values are the bf16 attention output cast up
+ * (ospnext/modules/attention.py:473,518 and osp_next.py:644): quantising the bf16 tensor
+ * directly gives the same x_q without materialising the fp32 copy.  Taken by
+ * hif8_absmax_scale, hif8_encode, hif8_fake_quant (y fp32) and hif8_fake_quant_to_bf16. */
 enum { HIF8_SEM_NPU = 0, HIF8_SEM_TORCH = 1 };
 enum { HIF8_A_BF16 = 0, HIF8_A_CODES = 1 };
 
@@ -71,7 +77,7 @@ int hif8_state_read(const void *state, uint32_t *amax_bits, float *scale, hif8_s
  *   x_max = x.abs().amax().clamp(min=1e-8);  scale = scale_max / x_max
  * with torch's rounding: scale = rnd(rnd(1/x_max) * scale_max), rnd = the input
  * dtype.  One pass over x; the last workgroup also fills the decode tables.
- * dtype: HIF8_DTYPE_BF16 or HIF8_DTYPE_F32.  n >= 1.
+ * dtype: HIF8_DTYPE_BF16, HIF8_DTYPE_F32 or HIF8_DTYPE_BF16_AS_F32 (an fp32 state).  n >= 1.
  */
 int hif8_absmax_scale(const void *x, int dtype, int64_t n, float scale_max, void *state,
                       hif8_stream_t stream);
@@ -88,9 +94,18 @@ int hif8_encode(const void *x, int dtype, int64_t n, const void *state, uint8_t 
                 hif8_stream_t stream);
 
 /* Fake quant: y = quant_dequant_float(x * scale, QType('hif8'), force_fp32=True) / scale
- * (hif8_linear.py:47-48).  y has the dtype of x.  semantics: HIF8_SEM_*. */
+ * (hif8_linear.py:47-48).  y has the dtype of x (fp32 for HIF8_DTYPE_BF16_AS_F32).
+ * semantics: HIF8_SEM_*. */
 int hif8_fake_quant(const void *x, int dtype, int64_t n, const void *state, void *y,
                     int semantics, hif8_stream_t stream);
+
+/* Fake quant into the bf16 GEMM operand: y = bf16(x_q), the rounding torch.autocast(bf16)
+ * applies to x_q when F.linear(x_q, w_q, bias) runs (hif8_linear.py:86 under the pipeline's
+ * autocast, ospnext/schedulers/flow_matching.py:108).  For a bf16 x this is hif8_fake_quant;
+ * for an fp32 x (or HIF8_DTYPE_BF16_AS_F32) it quantises in fp32 and writes 2 bytes per
+ * element, so the fp32 x_q is never stored.  y: n bf16. */
+int hif8_fake_quant_to_bf16(const void *x, int dtype, int64_t n, const void *state, uint16_t *y,
+                            int semantics, hif8_stream_t stream);
 
 /* Decode codes to x_q = decode(code) / scale in out_dtype (bf16 x_q of a bf16
  * tensor, or fp32 x_q of an fp32 tensor). */

@@ -27,6 +27,7 @@ from .hif8_linear import (  # noqa: F401
     encode,
     fake_quant,
     fake_quant_tiled,
+    fake_quant_to_bf16,
     linear_fwd,
     linear_fwd_tiled,
     make_linear,
@@ -67,7 +68,7 @@ from .qlinear import (  # noqa: F401
 __all__ = [
     "QType", "quant_dequant_float", "quant_func", "hif8_quant", "hif8_quant_bf16",
     "HIF8Linear", "PackedWeight", "QuantState", "_quant", "absmax_scale", "decode", "encode",
-    "fake_quant", "linear_fwd", "make_linear", "quantize_activation", "fake_quant_tiled",
+    "fake_quant", "fake_quant_to_bf16", "linear_fwd", "make_linear", "quantize_activation", "fake_quant_tiled",
     "tile_weight_codes", "tiled_rows", "linear_fwd_tiled", "transpose_codes", "linear_dgrad", "dgrad_fused_ok",
     "_HIF8QKVQuantFunction", "attention_with_mask", "hif8_attention_with_mask",
     "scaled_dot_product_attention_with_mask", "LinearForward", "LinearForwardFast", "QLinear", "replace_linear",

@@ -15,7 +15,7 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libhif8_mi355x.so")
 
 HIF8_OK = 0
-DTYPE_BF16, DTYPE_F32 = 0, 1
+DTYPE_BF16, DTYPE_F32, DTYPE_BF16_AS_F32 = 0, 1, 2
 SEM_NPU, SEM_TORCH = 0, 1
 A_BF16, A_CODES = 0, 1
 
@@ -30,6 +30,7 @@ SIGNATURES = {
     "hif8_set_scale": (_i, [_p, _i, _f, _p]),
     "hif8_encode": (_i, [_p, _i, _i64, _p, _p, _p]),
     "hif8_fake_quant": (_i, [_p, _i, _i64, _p, _p, _i, _p]),
+    "hif8_fake_quant_to_bf16": (_i, [_p, _i, _i64, _p, _p, _i, _p]),
     "hif8_decode": (_i, [_p, _i64, _p, _i, _p, _p]),
     "hif8_quant_f32": (_i, [_p, _p, _i64, _i, _p]),
     "hif8_quant_bf16": (_i, [_p, _p, _i64, _i, _p]),

@@ -77,7 +77,7 @@ __global__ __launch_bounds__(kTPB) void k_absmax(const void *__restrict__ xv, in
     const int tid = threadIdx.x;
     uint32_t m = 0;
     const int64_t stride = int64_t(gridDim.x) * kTPB;
-    if (DT == kBF16) {
+    if (DT != kF32) {
         const uint16_t *x = (const uint16_t *)xv;
         const int64_t nvec = n >> 3;                       // uint4 = 8 bf16
         const u32x4 *xq = (const u32x4 *)x;
@@ -140,10 +140,32 @@ __global__ __launch_bounds__(kTPB) void k_absmax(const void *__restrict__ xv, in
     if ((tid & 63) == 0) red[tid >> 6] = m;
     __syncthreads();
     m = max(max(red[0], red[1]), max(red[2], red[3]));
-    fold_amax(st, m, gridDim.x, DT, smax, red + kTPB / 64);
+    // bf16 held as fp32: the fp32 magnitude bits of the same value (NaN stays above Inf)
+    if (DT == kBF16F32) fold_amax(st, m << 16, gridDim.x, kF32, smax, red + kTPB / 64);
+    else fold_amax(st, m, gridDim.x, DT, smax, red + kTPB / 64);
 }
 
-// MODE 0: codes, MODE 1: qdq in the input dtype, MODE 2: decode codes -> x_q.
+// Element j of k_quant through the scalar reference route.
+template <int DT, int MODE>
+__device__ __forceinline__ void scalar_elem(const void *xv, void *outv, int64_t j, float s, int sem)
+{
+    uint32_t xb, yb, code;
+    if (DT == kBF16) {
+        xb = ((const uint16_t *)xv)[j];
+        slow_elem<kBF16>(xb, s, sem, yb, code);
+    } else {
+        xb = DT == kF32 ? ((const uint32_t *)xv)[j] : uint32_t(((const uint16_t *)xv)[j]) << 16;
+        slow_elem<kF32>(xb, s, sem, yb, code);
+        if (MODE == 3) yb = f2bf(u2f(yb));
+    }
+    if (MODE == 0) ((uint8_t *)outv)[j] = uint8_t(code);
+    else if (DT == kBF16 || MODE == 3) ((uint16_t *)outv)[j] = uint16_t(yb);
+    else ((uint32_t *)outv)[j] = yb;
+}
+
+// MODE 0: codes, MODE 1: qdq in the arithmetic dtype (bf16 for kBF16, fp32 otherwise),
+// MODE 2: decode codes -> x_q, MODE 3: qdq rounded to the bf16 GEMM operand.
+// DT kBF16F32 loads bf16 and computes as kF32 on the exact fp32 values.
 template <int DT, int MODE>
 __global__ __launch_bounds__(kTPB) void k_quant(const void *__restrict__ xv, int64_t n,
                                                  const State *__restrict__ st, void *__restrict__ outv,
@@ -213,13 +235,15 @@ __global__ __launch_bounds__(kTPB) void k_quant(const void *__restrict__ xv, int
         return;
     }
 
+    constexpr int kVec = DT == kF32 ? 4 : 2;      // 16-byte loads per 16 elements
+    const bool out16 = DT == kBF16 || MODE == 3;  // bf16 output (MODE 1/3)
     if (fast) {
         // the next group's input is loaded one iteration ahead (two groups in flight)
         u32x4 pre[4] = {};
         if (g < ngrp) {
             const u32x4 *xq = (const u32x4 *)xv;
 #pragma unroll
-            for (int j = 0; j < (DT == kBF16 ? 2 : 4); ++j) pre[j] = ld_stream(&xq[(DT == kBF16 ? 2 : 4) * g + j]);
+            for (int j = 0; j < kVec; ++j) pre[j] = ld_stream(&xq[kVec * g + j]);
         }
         for (; g < ngrp; g += stride) {
             uint32_t codes[4];
@@ -229,8 +253,14 @@ __global__ __launch_bounds__(kTPB) void k_quant(const void *__restrict__ xv, int
             if (g + stride < ngrp) {
                 const u32x4 *xq = (const u32x4 *)xv;
 #pragma unroll
-                for (int j = 0; j < (DT == kBF16 ? 2 : 4); ++j)
-                    pre[j] = ld_stream(&xq[(DT == kBF16 ? 2 : 4) * (g + stride) + j]);
+                for (int j = 0; j < kVec; ++j) pre[j] = ld_stream(&xq[kVec * (g + stride) + j]);
+            }
+            if (DT == kBF16F32) {
+                // the 16 bf16 values as the fp32 words x.float() holds
+                const uint32_t p[8] = {cur[0].x, cur[0].y, cur[0].z, cur[0].w, cur[1].x, cur[1].y, cur[1].z, cur[1].w};
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    cur[j] = u32x4{p[2 * j] << 16, p[2 * j] & 0xFFFF0000u, p[2 * j + 1] << 16, p[2 * j + 1] & 0xFFFF0000u};
             }
             if (DT == kBF16) {
                 u32x4 a = cur[0];
@@ -292,7 +322,7 @@ __global__ __launch_bounds__(kTPB) void k_quant(const void *__restrict__ xv, int
 #pragma unroll
                 for (int t = 0; t < 4; ++t) {
                     uint32_t c = (d >> (8 * t)) & 0xFF;
-                    y[4 * j + t] = DT == kBF16 ? uint32_t(lut16[c]) : f2u(lut32[c]);
+                    y[4 * j + t] = out16 ? uint32_t(lut16[c]) : f2u(lut32[c]);
                 }
             }
             if (sem == kSemTorch) {
@@ -305,11 +335,12 @@ __global__ __launch_bounds__(kTPB) void k_quant(const void *__restrict__ xv, int
                         float xs = DT == kBF16 ? bf2f(xs_full[t]) : u2f(xs_full[t]);
                         float q = qdq_torch(xs);
                         if (DT == kBF16) y[t] = f2bf(bf2f(f2bf(q)) / s);
+                        else if (MODE == 3) y[t] = f2bf(q / s);
                         else y[t] = f2u(q / s);
                     }
                 }
             }
-            if (DT == kBF16) {
+            if (out16) {
                 u32x4 *out = (u32x4 *)outv;
                 out[2 * g] = u32x4{y[0] | (y[1] << 16), y[2] | (y[3] << 16), y[4] | (y[5] << 16), y[6] | (y[7] << 16)};
                 out[2 * g + 1] = u32x4{y[8] | (y[9] << 16), y[10] | (y[11] << 16), y[12] | (y[13] << 16), y[14] | (y[15] << 16)};
@@ -321,24 +352,11 @@ __global__ __launch_bounds__(kTPB) void k_quant(const void *__restrict__ xv, int
         }
     } else {
         // degenerate scale (amax Inf/NaN, scale 0/Inf/NaN): element-wise reference route
-        for (int64_t j = g; j < (ngrp << 4); j += stride) {
-            uint32_t xb = DT == kBF16 ? ((const uint16_t *)xv)[j] : ((const uint32_t *)xv)[j];
-            uint32_t yb, code;
-            slow_elem<DT>(xb, s, sem, yb, code);
-            if (MODE == 0) ((uint8_t *)outv)[j] = uint8_t(code);
-            else if (DT == kBF16) ((uint16_t *)outv)[j] = uint16_t(yb);
-            else ((uint32_t *)outv)[j] = yb;
-        }
+        for (int64_t j = g; j < (ngrp << 4); j += stride) scalar_elem<DT, MODE>(xv, outv, j, s, sem);
     }
     // tail (n % 16) through the scalar route
-    for (int64_t j = (ngrp << 4) + int64_t(blockIdx.x) * kTPB + tid; j < n; j += stride) {
-        uint32_t xb = DT == kBF16 ? ((const uint16_t *)xv)[j] : ((const uint32_t *)xv)[j];
-        uint32_t yb, code;
-        slow_elem<DT>(xb, s, sem, yb, code);
-        if (MODE == 0) ((uint8_t *)outv)[j] = uint8_t(code);
-        else if (DT == kBF16) ((uint16_t *)outv)[j] = uint16_t(yb);
-        else ((uint32_t *)outv)[j] = yb;
-    }
+    for (int64_t j = (ngrp << 4) + int64_t(blockIdx.x) * kTPB + tid; j < n; j += stride)
+        scalar_elem<DT, MODE>(xv, outv, j, s, sem);
 }
 
 // ------------------------------------------------ GEMM operand layouts
@@ -612,12 +630,16 @@ int hif8_state_read(const void *state, uint32_t *amax_bits, float *scale, hif8_s
 int hif8_absmax_scale(const void *x, int dtype, int64_t n, float scale_max, void *state,
                       hif8_stream_t stream)
 {
-    if (!x || !state || n <= 0 || (dtype != HIF8_DTYPE_BF16 && dtype != HIF8_DTYPE_F32)) return HIF8_ERR_ARG;
+    if (!x || !state || n <= 0 || (dtype != HIF8_DTYPE_BF16 && dtype != HIF8_DTYPE_F32 && dtype != kBF16F32))
+        return HIF8_ERR_ARG;
     if (!aligned16(x)) return HIF8_ERR_ALIGN;
-    const int per_thread_vec = dtype == HIF8_DTYPE_BF16 ? 8 : 4;
+    const int per_thread_vec = dtype == HIF8_DTYPE_F32 ? 4 : 8;
     int grid = grid_for((n + per_thread_vec * 8 - 1) / (per_thread_vec * 8), cu_count() * kAmaxWgPerCu);
     if (dtype == HIF8_DTYPE_BF16)
         hipLaunchKernelGGL(k_absmax<kBF16>, dim3(grid), dim3(kTPB), 0, (hipStream_t)stream, x, n, (State *)state, scale_max);
+    else if (dtype == kBF16F32)
+        hipLaunchKernelGGL(k_absmax<kBF16F32>, dim3(grid), dim3(kTPB), 0, (hipStream_t)stream, x, n, (State *)state,
+                           scale_max);
     else
         hipLaunchKernelGGL(k_absmax<kF32>, dim3(grid), dim3(kTPB), 0, (hipStream_t)stream, x, n, (State *)state, scale_max);
     return last_launch();
@@ -634,7 +656,7 @@ static int launch_quant(const void *x, int dtype, int64_t n, const void *state, 
                         int sem, int use_state, hif8_stream_t stream)
 {
     if (!x || !out || n <= 0 || (use_state && !state)) return HIF8_ERR_ARG;
-    if (dtype != HIF8_DTYPE_BF16 && dtype != HIF8_DTYPE_F32) return HIF8_ERR_ARG;
+    if (dtype != HIF8_DTYPE_BF16 && dtype != HIF8_DTYPE_F32 && !(dtype == kBF16F32 && mode != 2)) return HIF8_ERR_ARG;
     if (sem != HIF8_SEM_NPU && sem != HIF8_SEM_TORCH) return HIF8_ERR_ARG;
     if (!aligned16(x) || !aligned16(out)) return HIF8_ERR_ALIGN;
     int grid = grid_for((n + 15) / 16, cu_count() * (mode == 0 ? kEncodeWgPerCu : kQdqWgPerCu));
@@ -644,12 +666,17 @@ static int launch_quant(const void *x, int dtype, int64_t n, const void *state, 
     hipLaunchKernelGGL((k_quant<DT, MODE>), dim3(grid), dim3(kTPB), 0, s, x, n, st, out, sem, use_state)
     if (dtype == HIF8_DTYPE_BF16) {
         if (mode == 0) HIF8_LAUNCH(kBF16, 0);
-        else if (mode == 1) HIF8_LAUNCH(kBF16, 1);
+        else if (mode == 1 || mode == 3) HIF8_LAUNCH(kBF16, 1);
         else HIF8_LAUNCH(kBF16, 2);
-    } else {
+    } else if (dtype == HIF8_DTYPE_F32) {
         if (mode == 0) HIF8_LAUNCH(kF32, 0);
         else if (mode == 1) HIF8_LAUNCH(kF32, 1);
-        else HIF8_LAUNCH(kF32, 2);
+        else if (mode == 2) HIF8_LAUNCH(kF32, 2);
+        else HIF8_LAUNCH(kF32, 3);
+    } else {
+        if (mode == 0) HIF8_LAUNCH(kBF16F32, 0);
+        else if (mode == 1) HIF8_LAUNCH(kBF16F32, 1);
+        else HIF8_LAUNCH(kBF16F32, 3);
     }
 #undef HIF8_LAUNCH
     return last_launch();
@@ -664,6 +691,12 @@ int hif8_fake_quant(const void *x, int dtype, int64_t n, const void *state, void
                     hif8_stream_t stream)
 {
     return launch_quant(x, dtype, n, state, y, 1, semantics, 1, stream);
+}
+
+int hif8_fake_quant_to_bf16(const void *x, int dtype, int64_t n, const void *state, uint16_t *y, int semantics,
+                            hif8_stream_t stream)
+{
+    return launch_quant(x, dtype, n, state, y, 3, semantics, 1, stream);
 }
 
 int hif8_decode(const uint8_t *codes, int64_t n, const void *state, int out_dtype, void *y, hif8_stream_t stream)

@@ -9,6 +9,7 @@ namespace hif8 {
 
 constexpr int kBF16 = HIF8_DTYPE_BF16;
 constexpr int kF32 = HIF8_DTYPE_F32;
+constexpr int kBF16F32 = HIF8_DTYPE_BF16_AS_F32;   // bf16 storage, fp32 arithmetic and state
 constexpr int kSemNpu = HIF8_SEM_NPU;
 constexpr int kSemTorch = HIF8_SEM_TORCH;
 

@@ -300,13 +300,13 @@ def _sdpa(q: Tensor, k: Tensor, v: Tensor) -> Tensor:
 
 
 def attention_key_masked(q: Tensor, k: Tensor, v: Tensor, key_mask: Optional[Tensor] = None,
-                         dtype: torch.dtype = torch.bfloat16) -> Tensor:
+                         dtype: torch.dtype = torch.bfloat16, out_dtype: Optional[torch.dtype] = None) -> Tensor:
     """``attention_with_mask(q, k, v, attn_mask_kv=key_mask)`` of the SDPA branch
-    (attention.py:460-518): computed in ``dtype``, returned in q's dtype.  Keys where
-    ``key_mask`` is False take no weight; each sequence attends to its unmasked keys directly,
-    which is that masked softmax without materialising an [N, N] mask (every query row,
-    padding queries included, gets its output)."""
-    out_dtype = q.dtype
+    (attention.py:460-518): computed in ``dtype``, returned in q's dtype (or ``out_dtype``).
+    Keys where ``key_mask`` is False take no weight; each sequence attends to its unmasked keys
+    directly, which is that masked softmax without materialising an [N, N] mask (every query
+    row, padding queries included, gets its output)."""
+    out_dtype = out_dtype or q.dtype
     q, k, v = q.to(dtype), k.to(dtype), v.to(dtype)
     if key_mask is None:
         return _sdpa(q, k, v).to(out_dtype)
@@ -373,14 +373,17 @@ class OSPNextSelfAttention(nn.Module):
         else:
             self.rearrange_rope = SkiparseRearrange(1, RearrangeType.Identity)
 
-    def _attend(self, q: Tensor, k: Tensor, v: Tensor, key_mask: Optional[Tensor]) -> Tensor:
+    def _attend(self, q: Tensor, k: Tensor, v: Tensor, key_mask: Optional[Tensor],
+                out_dtype: Optional[torch.dtype] = None) -> Tensor:
         if self.quant_attn == "hif8":   # hif8_attention.py:93-126
             q, k, v = _HIF8QKVQuantFunction.apply(q, k, v, self.scale_max_forward, self.scale_max_backward)
-        return attention_key_masked(q, k, v, key_mask)
+        return attention_key_masked(q, k, v, key_mask, out_dtype=out_dtype)
 
     def forward(self, x: Optional[Tensor], attn_mask: Optional[Tensor], grid_sizes_for_rope,
                 rope_wrapper: SkiparseRopeWrapper, qkv: Optional[Sequence[Tensor]] = None) -> Tensor:
-        """``qkv`` = the three projections of x computed by the caller (the fused route)."""
+        """``qkv`` = the three projections of x computed by the caller (the fused route, which
+        also hands the bf16 attention output to ``o`` without its fp32 copy)."""
+        qkv_given = qkv is not None
         if qkv is None:
             qkv = (self.q(x), self.k(x), self.v(x))
         ql, kl, vl = qkv
@@ -391,6 +394,10 @@ class OSPNextSelfAttention(nn.Module):
         v = vl.view(B, N, H, D)
         q = rope_wrapper.apply_rope(q, grid_sizes_for_rope, self.rearrange_rope)
         k = rope_wrapper.apply_rope(k, grid_sizes_for_rope, self.rearrange_rope)
+        if qkv_given and isinstance(self.o, HIF8Linear) and q.dtype == torch.float32:
+            # the attention output is bf16 values returned as fp32: quantise them as such
+            x = self._attend(q, k, v, attn_mask, out_dtype=torch.bfloat16)
+            return self.o.forward_f32_of_bf16(x.flatten(2))
         x = self._attend(q, k, v, attn_mask)
         return self.o(x.flatten(2))
 

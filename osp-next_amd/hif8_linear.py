@@ -66,27 +66,50 @@ def _aligned(t: Tensor) -> Tensor:
     return t if t.data_ptr() % 16 == 0 else t.clone()
 
 
-def absmax_scale(x: Tensor, scale_max: float, state: QuantState) -> QuantState:
-    """hif8_linear.py:45-46 into ``state`` (amax, scale and decode tables)."""
+def _dtype_arg(x: Tensor, as_f32: bool) -> int:
+    """The library's dtype code for x; ``as_f32`` quantises a bf16 x as x.float() would be."""
+    if as_f32:
+        if x.dtype != torch.bfloat16:
+            raise TypeError("as_f32 applies to a bfloat16 tensor")
+        return _lib.DTYPE_BF16_AS_F32
+    return _lib.dtype_code(x.dtype)
+
+
+def absmax_scale(x: Tensor, scale_max: float, state: QuantState, as_f32: bool = False) -> QuantState:
+    """hif8_linear.py:45-46 into ``state`` (amax, scale and decode tables).  ``as_f32``: the
+    fp32 rule for a bf16 x, as ``_quant(x.float())`` computes it."""
     _lib.require_gpu_tensor(x, "x")
     x = _aligned(x)
     if x.numel() == 0:
         raise ValueError("amax of an empty tensor")
-    _lib.check(_lib.load().hif8_absmax_scale(x.data_ptr(), _lib.dtype_code(x.dtype), x.numel(),
+    _lib.check(_lib.load().hif8_absmax_scale(x.data_ptr(), _dtype_arg(x, as_f32), x.numel(),
                                              float(scale_max), state.ptr, _lib.stream_ptr(x.device)),
                "hif8_absmax_scale")
     return state
 
 
-def encode(x: Tensor, state: QuantState) -> Tensor:
+def encode(x: Tensor, state: QuantState, as_f32: bool = False) -> Tensor:
     """HiF8 codes of qdq(x * scale) (NPU semantics), one byte per element."""
     _lib.require_gpu_tensor(x, "x")
     x = _aligned(x)
     codes = torch.empty(x.shape, dtype=torch.uint8, device=x.device)
     if x.numel():
-        _lib.check(_lib.load().hif8_encode(x.data_ptr(), _lib.dtype_code(x.dtype), x.numel(), state.ptr,
+        _lib.check(_lib.load().hif8_encode(x.data_ptr(), _dtype_arg(x, as_f32), x.numel(), state.ptr,
                                            codes.data_ptr(), _lib.stream_ptr(x.device)), "hif8_encode")
     return codes
+
+
+def fake_quant_to_bf16(x: Tensor, state: QuantState, semantics: int = _lib.SEM_NPU, as_f32: bool = False) -> Tensor:
+    """bf16(x_q): the GEMM operand F.linear's bf16 autocast makes of ``_quant(x)[0]``
+    (hif8_linear.py:86); for an fp32 x (or ``as_f32``) the fp32 x_q is never stored."""
+    _lib.require_gpu_tensor(x, "x")
+    x = _aligned(x)
+    y = torch.empty(x.shape, dtype=torch.bfloat16, device=x.device)
+    if x.numel():
+        _lib.check(_lib.load().hif8_fake_quant_to_bf16(x.data_ptr(), _dtype_arg(x, as_f32), x.numel(), state.ptr,
+                                                       y.data_ptr(), semantics, _lib.stream_ptr(x.device)),
+                   "hif8_fake_quant_to_bf16")
+    return y
 
 
 def fake_quant(x: Tensor, state: QuantState, semantics: int = _lib.SEM_NPU) -> Tensor:
@@ -335,12 +358,16 @@ def linear_fwd_tiled(xt: Tensor, M: int, w: PackedWeight, bias: Optional[Tensor]
     return y
 
 
-def quantize_activation(x2: Tensor, scale_max: float, a_format: str):
-    """Quantise a [M,K] activation for the fused GEMM: returns (a, a_fmt, state)."""
-    st = absmax_scale(x2, scale_max, QuantState(x2.device))
-    if a_format == "codes" or x2.dtype != torch.bfloat16:
-        return encode(x2, st), _lib.A_CODES, st
-    return fake_quant(x2, st), _lib.A_BF16, st
+def quantize_activation(x2: Tensor, scale_max: float, a_format: str, as_f32: bool = False):
+    """Quantise a [M,K] activation for the fused GEMM: returns (a, a_fmt, state).  An fp32
+    activation (or a bf16 one with ``as_f32``) is quantised in fp32 and handed over as its
+    bf16 autocast rounding; ``a_format="codes"`` gives the 8-bit codes instead."""
+    st = absmax_scale(x2, scale_max, QuantState(x2.device), as_f32)
+    if a_format == "codes":
+        return encode(x2, st, as_f32), _lib.A_CODES, st
+    if x2.dtype == torch.bfloat16 and not as_f32:
+        return fake_quant(x2, st), _lib.A_BF16, st
+    return fake_quant_to_bf16(x2, st, as_f32=as_f32), _lib.A_BF16, st
 
 
 # --------------------------------------------------------------- autograd
@@ -380,6 +407,9 @@ class _HIF8LinearFunction(torch.autograd.Function):
         a, a_fmt, a_st = quantize_activation(x2, scale_max_forward, "codes" if a_format == "codes" else "bf16")
         y = linear_any(a, a_fmt, a_st, packed, bias)
         if needs_grad:
+            if x.dtype != torch.bfloat16 and a_fmt == _lib.A_BF16:
+                # the backward's x_q is the fp32 one (hif8_linear.py:78-82): keep its codes
+                a, a_fmt = encode(x2, a_st), _lib.A_CODES
             ctx.a, ctx.a_fmt, ctx.a_st, ctx.packed = a, a_fmt, a_st, packed
             ctx.x_dtype, ctx.w_dtype = x.dtype, weight.dtype
             ctx.x_shape = x.shape
@@ -479,6 +509,22 @@ class HIF8Linear(nn.Linear):
         x2 = x_q.reshape(-1, K).contiguous()
         y = linear_any(x2, _lib.A_BF16, None, self._packed_weight(), self.bias)
         return y.view(*x_q.shape[:-1], y.shape[-1])
+
+    def forward_f32_of_bf16(self, x: Tensor) -> Tensor:
+        """``forward(x.float())`` for a bf16 x without the fp32 copy: x quantised with fp32
+        arithmetic as ``_quant`` does for the fp32 tensor, the GEMM on its bf16 autocast
+        rounding.  The self-attention ``o`` input is such a tensor (the bf16 attention output
+        returned as fp32, attention.py:473,518).  Inference only."""
+        if torch.is_grad_enabled() and (x.requires_grad or self.weight.requires_grad
+                                        or (self.bias is not None and self.bias.requires_grad)):
+            raise RuntimeError("forward_f32_of_bf16 has no autograd; call forward(x.float())")
+        if x.dtype != torch.bfloat16:
+            raise TypeError(f"forward_f32_of_bf16 takes a bfloat16 tensor, got {x.dtype}")
+        K = x.shape[-1]
+        x2 = x.reshape(-1, K).contiguous()
+        a, a_fmt, a_st = quantize_activation(x2, self.scale_max_forward, "bf16", as_f32=True)
+        y = linear_any(a, a_fmt, a_st, self._packed_weight(), self.bias)
+        return y.view(*x.shape[:-1], y.shape[-1])
 
     def extra_repr(self) -> str:
         return (f"in_features={self.in_features}, out_features={self.out_features}, "
