@@ -357,6 +357,48 @@ def time_step(pkg, torch, reps):
     return out
 
 
+def time_data_dependence(pkg, torch, x, w, reps):
+    """The fused GEMM on the FFN-up shape with constant instead of random operands (x, W, both):
+    a kernel at the board's power limit runs faster when its operands do not toggle.  Not the
+    benchmark workload; reported beside it."""
+    dev = x.device
+    M, K = x.shape
+    N = w.shape[0]
+    L = pkg._lib.load()
+    stream = pkg._lib.stream_ptr(dev)
+    y = torch.empty(M, N, dtype=torch.bfloat16, device=dev)
+
+    def operands(xx, ww):
+        st = pkg.absmax_scale(xx, 15.0, pkg.QuantState(dev))
+        return pkg.fake_quant(xx, st), pkg.PackedWeight(ww, 15.0)
+
+    def gemm_ms(xq, pw):
+        def run():
+            pkg._lib.check(L.hif8_linear_fwd(xq.data_ptr(), pkg._lib.A_BF16, None, pw.codes.data_ptr(), pw.state.ptr,
+                                             None, y.data_ptr(), M, N, K, stream), "linear")
+        run()
+        torch.cuda.synchronize()
+        ea, eb = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        ea.record()
+        for _ in range(reps):
+            run()
+        eb.record()
+        torch.cuda.synchronize()
+        return round(ea.elapsed_time(eb) / reps, 3)
+
+    xc = torch.full_like(x, 0.5)
+    wc = torch.full_like(w, 0.01)
+    out = {"what": "k_linear_dtl ms at the FFN-up shape by operand data (x / W)"}
+    xr_q, wr_p = operands(x, w)
+    xc_q, wc_p = operands(xc, wc)
+    out["random/random"] = gemm_ms(xr_q, wr_p)
+    out["random/const"] = gemm_ms(xr_q, wc_p)
+    out["const/random"] = gemm_ms(xc_q, wr_p)
+    out["const/const"] = gemm_ms(xc_q, wc_p)
+    del xc, wc, xr_q, wr_p, xc_q, wc_p, y
+    return out
+
+
 def median(v):
     s = sorted(v)
     return s[len(s) // 2]
@@ -373,12 +415,14 @@ def _cpu_model() -> str:
     return platform.machine()
 
 
-def cpu_baseline(torch, M, K, N, sample_rows=1024):
-    """The reference CPU path (torch ops: _quant + quant_hif8 + F.linear in bf16) on a
-    row slice; the per-call weight quantisation is timed once and the activation
-    part scaled linearly in M."""
+def cpu_baseline(torch, M, K, N, sample_rows=4096, target_s=10.0):
+    """The reference CPU path (torch ops: _quant + quant_hif8 + F.linear in bf16) on a bounded
+    sample of the same workload: a [sample_rows, K] slice of x (quantise + GEMM against the
+    quantised W) repeated until about ``target_s`` seconds of CPU work, and the per-call weight
+    quantisation twice; the full step is the weight part plus the slice time scaled to M."""
     sys.path.insert(0, ROOT)
     from oracle import hif8_ref as R
+    import torch.nn.functional as F
 
     threads = min(os.cpu_count() or 1, 16)
     torch.set_num_threads(threads)
@@ -387,25 +431,32 @@ def cpu_baseline(torch, M, K, N, sample_rows=1024):
     x[:, torch.randperm(K, generator=g)[:16]] *= 20
     x = x.to(torch.bfloat16)
     w = (torch.randn(N, K, generator=g) * 0.02).to(torch.bfloat16)
-    import torch.nn.functional as F
     R.quant_torch_cpu(x[:64], 15.0)  # warm
-    t0 = time.perf_counter()
-    wq, _ = R.quant_torch_cpu(w, 15.0)
-    t_w = time.perf_counter() - t0
-    t0 = time.perf_counter()
-    xq, _ = R.quant_torch_cpu(x, 15.0)
-    t_x = time.perf_counter() - t0
-    F.linear(xq[:64], wq)  # warm
-    t0 = time.perf_counter()
-    F.linear(xq, wq)
-    t_g = time.perf_counter() - t0
-    t_full = t_w + (M / sample_rows) * (t_x + t_g)
+    t_start = time.perf_counter()
+    t_w = []
+    for _ in range(2):
+        t0 = time.perf_counter()
+        wq, _ = R.quant_torch_cpu(w, 15.0)
+        t_w.append(time.perf_counter() - t0)
+    F.linear(x[:64], wq)  # warm
+    t_slice = []
+    while True:
+        t0 = time.perf_counter()
+        xq, _ = R.quant_torch_cpu(x, 15.0)
+        F.linear(xq, wq)
+        t_slice.append(time.perf_counter() - t0)
+        if time.perf_counter() - t_start >= target_s or len(t_slice) >= 200:
+            break
+    total = time.perf_counter() - t_start
+    tw, ts = median(t_w), median(t_slice)
+    t_full = tw + (M / sample_rows) * ts
     value = 2.0 * M * N * K / t_full / 1e12
     return {
         "value": round(value, 4), "unit": "TFLOP/s", "cores": threads, "kind": "port",
-        "sample": (f"reference CPU path (torch ops, bf16 F.linear) on x[{sample_rows},{K}] x W[{N},{K}]: "
-                   f"W qdq {t_w:.2f}s, x qdq {t_x:.3f}s, GEMM {t_g:.3f}s; full-M time extrapolated "
-                   f"linearly to M={M}: {t_full:.1f}s"),
+        "sample": (f"reference CPU path (torch ops, bf16 F.linear) on the FFN-up shape: W[{N},{K}] qdq x2 "
+                   f"(median {tw:.2f}s) and {len(t_slice)} reps of an x[{sample_rows},{K}] slice, qdq + GEMM "
+                   f"(median {ts:.3f}s), {total:.1f}s of CPU work; one step at M={M} = W qdq + "
+                   f"{M / sample_rows:.2f} slices = {t_full:.2f}s"),
         "cpu_model": _cpu_model(),
     }
 
@@ -418,8 +469,8 @@ def main():
     ap.add_argument("--a-format", default="bf16", choices=["tiled", "bf16", "codes"])
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--shapes", default="up,modln,qkv,block",
-                    help="comma list of up,down,qkvo,ffn,modln,qkv,block (config 4),step (config 5) "
-                         "to time in addition")
+                    help="comma list of up,down,qkvo,ffn,modln,qkv,block (config 4),step (config 5),"
+                         "data (the GEMM with constant operands) to time in addition")
     ap.add_argument("--pmc-calibration", action="store_true",
                     help="also run one plain copy of x (774,144,000 B read + written): the reference "
                          "kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE")
@@ -502,6 +553,9 @@ def main():
     if "qkv" in args.shapes.split(","):
         log("[bench] timing the grouped q/k/v projections")
         extra_shapes["qkv"] = time_qkv(pkg, torch, x, max(3, args.steps // 4))
+    if "data" in args.shapes.split(","):
+        log("[bench] timing the fused GEMM with constant operands")
+        extra_shapes["data"] = time_data_dependence(pkg, torch, x, w, max(3, args.steps // 2))
     if "block" in args.shapes.split(","):
         log("[bench] timing one 14B DiT block at 720P (config 4)")
         try:
@@ -515,7 +569,7 @@ def main():
         except Exception as ex:
             extra_shapes["step"] = {"error": repr(ex)}
     for name in [s for s in args.shapes.split(",")
-                 if s and s not in ("up", "ffn", "modln", "qkv", "block", "step")]:
+                 if s and s not in ("up", "ffn", "modln", "qkv", "block", "step", "data")]:
         n_, k_ = {"down": (5120, 13824), "qkvo": (5120, 5120)}[name]
         xs, ws, bs = make_inputs(torch, M, k_, n_, seed=1)
         ps = pkg.PackedWeight(ws, 15.0)

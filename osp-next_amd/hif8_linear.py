@@ -391,6 +391,18 @@ def hif8_linear_inference(x: Tensor, packed: PackedWeight, bias: Optional[Tensor
     return y.view(*x.shape[:-1], y.shape[-1])
 
 
+def _forward_no_grad(x: Tensor, packed: PackedWeight, bias: Optional[Tensor], scale_max_forward: float,
+                     a_format: str = "bf16") -> Tensor:
+    """_HIF8LinearFunction.forward without autograd bookkeeping (nothing kept for a backward)."""
+    if x.dtype not in (torch.bfloat16, torch.float32):
+        raise TypeError(f"HIF8Linear takes bfloat16 or float32 input, got {x.dtype}")
+    K = x.shape[-1]
+    a, a_fmt, a_st = quantize_activation(x.reshape(-1, K).contiguous(), scale_max_forward,
+                                         "codes" if a_format == "codes" else "bf16")
+    y = linear_any(a, a_fmt, a_st, packed, bias)
+    return y.view(*x.shape[:-1], y.shape[-1])
+
+
 class _HIF8LinearFunction(torch.autograd.Function):
     """hif8_linear.py:56-111 with the fused HIP forward."""
 
@@ -491,8 +503,10 @@ class HIF8Linear(nn.Linear):
         packed = self._packed_weight()
         grad = torch.is_grad_enabled() and (x.requires_grad or self.weight.requires_grad
                                             or (self.bias is not None and self.bias.requires_grad))
-        if not grad and self.a_format == "tiled":
-            return hif8_linear_inference(x, packed, self.bias, self.scale_max_forward)
+        if not grad:
+            if self.a_format == "tiled":
+                return hif8_linear_inference(x, packed, self.bias, self.scale_max_forward)
+            return _forward_no_grad(x, packed, self.bias, self.scale_max_forward, self.a_format)
         return _HIF8LinearFunction.apply(x, self.weight, self.bias, self.scale_max_forward,
                                          self.scale_max_backward, packed, self.a_format)
 
