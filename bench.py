@@ -542,6 +542,21 @@ def main():
     }
     encode["frac"] = round(encode["achieved_GBps"] / PEAK_HBM_GBPS, 4)
     encode["traffic"] = measured_traffic("k_absmax+k_quant_encode")
+    # streaming references with torch's own elementwise kernels on the same x (context only):
+    # a copy (2 B read + 2 B written per element) and a cast to uint8 (2 B read + 1 B written,
+    # the encode kernel's traffic shape)
+    refs = {}
+    for name, dst, nbytes in (("copy", torch.empty_like(x), 4 * n), ("cast_u8", codes, 3 * n)):
+        dst.copy_(x)
+        torch.cuda.synchronize()
+        ea, eb = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        ea.record()
+        for _ in range(5):
+            dst.copy_(x)
+        eb.record()
+        torch.cuda.synchronize()
+        refs[name + "_GBps"] = round(nbytes / (ea.elapsed_time(eb) / 5 * 1e-3) / 1e9, 1)
+    encode["torch_streaming_refs"] = refs
     del codes
 
     extra_shapes = {}
