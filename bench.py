@@ -3,14 +3,17 @@
 Workload (Wan-14B 720P): one HIF8Linear forward of the FFN-up
 projection, x [75600, 5120] bf16 (N(0,1), 16 outlier channels x20) against
 W [13824, 5120] held as packed 8-bit HiF8 codes (N(0,0.02), prepacked once,
-outside the timed region).  A step = amax+scale of x, fake-quant of x, fused
-dequant-GEMM + bias -> y [75600, 13824] bf16: the reference's
+outside the timed region).  A step = amax+scale of x, fake-quant of x, the GEMM of
+x_q and the dequantised weight + bias -> y [75600, 13824] bf16: the reference's
 _HIF8LinearFunction.forward (ospnext/modules/hif8_linear.py:68-86).
 
-value = 2*M*N*K / step time (TFLOP/s).  The per-kernel times come from HIP
+value = 2*M*N*K / step time (TFLOP/s).  At this M the step takes HIF8Linear's decode-once
+route (the weight codes decoded to bf16 once per call, then the decode-free GEMM); the fused
+dequant-GEMM route is timed beside it (other_route).  The per-kernel times come from HIP
 events on the stream the kernels run on (torch's current stream).
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--a-format bf16|codes]
+                    [--route auto|fused|decode_once] [--shapes ...]
 """
 from __future__ import annotations
 
@@ -42,12 +45,14 @@ def make_inputs(torch, M, K, N, seed=0, dev="cuda:0"):
     return x, w, b
 
 
-def time_linear(pkg, torch, x, packed, b, steps, warmup, a_format):
-    """Times steps of [amax+scale, quantise, fused GEMM]; returns per-phase ms lists.
+def time_linear(pkg, torch, x, packed, b, steps, warmup, a_format, route="fused"):
+    """Times steps of [amax+scale, quantise, GEMM]; returns per-phase ms lists.
 
-    a_format "tiled": x_q written in the GEMM operand layout + tiled fused GEMM
-    (the HIF8Linear inference path); "bf16"/"codes": row-major x_q / codes and
-    the row-major fused GEMM."""
+    a_format "tiled": x_q written in the GEMM operand layout + tiled fused GEMM; "bf16"/"codes":
+    row-major x_q / codes and the row-major fused GEMM.  route "decode_once" (bf16 only): the GEMM
+    phase is hif8_decode of the weight codes into a bf16 buffer, then the decode-free GEMM
+    hif8_linear_fwd_wq (the HIF8Linear route from DECODE_ONCE_MIN_ROWS rows up); its two parts
+    are timed separately as well."""
     st = pkg.QuantState(x.device)
     L = pkg._lib.load()
     stream = pkg._lib.stream_ptr(x.device)
@@ -58,6 +63,7 @@ def time_linear(pkg, torch, x, packed, b, steps, warmup, a_format):
         a = torch.empty(pkg.tiled_rows(M) * K, dtype=torch.bfloat16, device=x.device)
     else:
         a = torch.empty((M, K), dtype=torch.uint8 if a_format == "codes" else torch.bfloat16, device=x.device)
+    wq = torch.empty((N, K), dtype=torch.bfloat16, device=x.device) if route == "decode_once" else None
 
     def amax():
         pkg._lib.check(L.hif8_absmax_scale(x.data_ptr(), 0, x.numel(), 15.0, st.ptr, stream), "amax")
@@ -70,8 +76,15 @@ def time_linear(pkg, torch, x, packed, b, steps, warmup, a_format):
         else:
             pkg._lib.check(L.hif8_fake_quant(x.data_ptr(), 0, x.numel(), st.ptr, a.data_ptr(), 0, stream), "qdq")
 
+    def wdecode():
+        pkg._lib.check(L.hif8_decode(packed.codes.data_ptr(), N * K, packed.state.ptr, 0, wq.data_ptr(), stream),
+                       "decode")
+
     def gemm():
-        if a_format == "tiled":
+        if route == "decode_once":
+            pkg._lib.check(L.hif8_linear_fwd_wq(a.data_ptr(), wq.data_ptr(), b.data_ptr(), y.data_ptr(), M, N, K,
+                                                stream), "linear_wq")
+        elif a_format == "tiled":
             pkg._lib.check(L.hif8_linear_fwd_tiled(a.data_ptr(), packed.wt.data_ptr(), packed.state.ptr,
                                                    b.data_ptr(), y.data_ptr(), M, N, K, stream), "linear")
         else:
@@ -79,10 +92,14 @@ def time_linear(pkg, torch, x, packed, b, steps, warmup, a_format):
             pkg._lib.check(L.hif8_linear_fwd(a.data_ptr(), fmt, st.ptr, packed.codes.data_ptr(), packed.state.ptr,
                                              b.data_ptr(), y.data_ptr(), M, N, K, stream), "linear")
 
+    def wdec_maybe():
+        if route == "decode_once":
+            wdecode()
+
     for _ in range(warmup):
-        amax(); quant(); gemm()
+        amax(); quant(); wdec_maybe(); gemm()
     torch.cuda.synchronize()
-    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(steps)]
+    ev = [[torch.cuda.Event(enable_timing=True) for _ in range(5)] for _ in range(steps)]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(steps):
@@ -92,12 +109,15 @@ def time_linear(pkg, torch, x, packed, b, steps, warmup, a_format):
         e[1].record()
         quant()
         e[2].record()
-        gemm()
+        wdec_maybe()
         e[3].record()
+        gemm()
+        e[4].record()
     torch.cuda.synchronize()
     wall = (time.perf_counter() - t0) * 1e3
     return {"wall_ms": wall, "amax": [e[0].elapsed_time(e[1]) for e in ev],
-            "quant": [e[1].elapsed_time(e[2]) for e in ev], "gemm": [e[2].elapsed_time(e[3]) for e in ev], "y": y}
+            "quant": [e[1].elapsed_time(e[2]) for e in ev], "wdecode": [e[2].elapsed_time(e[3]) for e in ev],
+            "gemm": [e[3].elapsed_time(e[4]) for e in ev], "y": y}
 
 
 TRAFFIC_DOC = os.path.join(ROOT, "profiles", "hif8_kernels_14b_720p_hbm_traffic.md")
@@ -467,6 +487,8 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--a-format", default="bf16", choices=["tiled", "bf16", "codes"])
+    ap.add_argument("--route", default="auto", choices=["auto", "fused", "decode_once"],
+                    help="GEMM route for bf16 activations (auto: HIF8Linear's rule, decode_once at this M)")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--shapes", default="up,modln,qkv,block",
                     help="comma list of up,down,qkvo,ffn,modln,qkv,block (config 4),step (config 5),"
@@ -496,16 +518,33 @@ def main():
         torch.cuda.synchronize()
         del xc
     torch.cuda.synchronize()
-    log("[bench] timing FFN-up step")
-    r = time_linear(pkg, torch, x, packed, b, args.steps, args.warmup, args.a_format)
-    step_ms = [a + q + g for a, q, g in zip(r["amax"], r["quant"], r["gemm"])]
+    route = args.route
+    if route == "auto":   # HIF8Linear's own choice for bf16 activations (hif8_linear.decode_once)
+        route = "decode_once" if (args.a_format == "bf16" and M >= pkg.hif8_linear.DECODE_ONCE_MIN_ROWS) else "fused"
+    if route == "decode_once" and args.a_format != "bf16":
+        raise SystemExit("--route decode_once takes --a-format bf16")
+    log(f"[bench] timing FFN-up step ({route})")
+    r = time_linear(pkg, torch, x, packed, b, args.steps, args.warmup, args.a_format, route)
+    step_ms = [a + q + d + g for a, q, d, g in zip(r["amax"], r["quant"], r["wdecode"], r["gemm"])]
     ms_step = r["wall_ms"] / args.steps
     flops = 2.0 * M * N * K
     value = flops / (ms_step * 1e-3) / 1e12
     gemm_ms = sum(r["gemm"]) / len(r["gemm"])
     amax_ms = sum(r["amax"]) / len(r["amax"])
     quant_ms = sum(r["quant"]) / len(r["quant"])
+    wdec_ms = sum(r["wdecode"]) / len(r["wdecode"])
     gemm_tflops = flops / (gemm_ms * 1e-3) / 1e12
+    # the other route on the same operands, for comparison
+    other = "fused" if route == "decode_once" else ("decode_once" if args.a_format == "bf16" else None)
+    other_route = None
+    if other:
+        ro = time_linear(pkg, torch, x, packed, b, max(3, args.steps // 2), 1, args.a_format, other)
+        og = sum(ro["gemm"]) / len(ro["gemm"])
+        od = sum(ro["wdecode"]) / len(ro["wdecode"])
+        other_route = {"route": other, "gemm_ms": round(og, 4), "wdecode_ms": round(od, 4),
+                       "gemm_TFLOPs": round(flops / (og * 1e-3) / 1e12, 1),
+                       "kernel": "k_linear_w16" if other == "decode_once" else "k_linear_dtl"}
+        del ro
     n = M * K
     enc_bytes = 5 * n if args.a_format == "codes" else 6 * n   # amax read + quantise read/write
     enc_gbps = enc_bytes / ((amax_ms + quant_ms) * 1e-3) / 1e9
@@ -588,7 +627,7 @@ def main():
         n_, k_ = {"down": (5120, 13824), "qkvo": (5120, 5120)}[name]
         xs, ws, bs = make_inputs(torch, M, k_, n_, seed=1)
         ps = pkg.PackedWeight(ws, 15.0)
-        rr = time_linear(pkg, torch, xs, ps, bs, max(3, args.steps // 2), 2, args.a_format)
+        rr = time_linear(pkg, torch, xs, ps, bs, max(3, args.steps // 2), 2, args.a_format, route)
         gm = sum(rr["gemm"]) / len(rr["gemm"])
         extra_shapes[name] = {"M": M, "N": n_, "K": k_, "gemm_ms": round(gm, 4),
                               "gemm_TFLOPs": round(2.0 * M * n_ * k_ / (gm * 1e-3) / 1e12, 1),
@@ -625,6 +664,10 @@ def main():
             cpu = {"error": str(ex)}
 
     kernel_name = {"tiled": "k_linear_tiled", "codes": "k_linear", "bf16": "k_linear_dtl"}[args.a_format]
+    if route == "decode_once":
+        kernel_name = "k_linear_w16"
+    gemm_desc = ("weight codes decoded once to bf16 (hif8_decode) -> decode-free HiF8 GEMM (k_linear_w16)"
+                 if route == "decode_once" else "fused HiF8 dequant-GEMM")
     out = {
         "metric": METRIC,
         "value": round(value, 2),
@@ -640,9 +683,9 @@ def main():
         "data": "synthetic",
         "config": {
             "workload": ("Wan-14B 720P FFN-up HIF8Linear forward: x[75600,5120] bf16 -> amax+scale -> "
-                         f"{'encode' if args.a_format == 'codes' else 'fake-quant'} ({args.a_format}) -> fused HiF8 dequant-GEMM "
-                         "(W[13824,5120] packed 8-bit HiF8, bias) -> y bf16"),
-            "M": M, "K": K, "N": N, "a_format": args.a_format, "scale_max": 15.0,
+                         f"{'encode' if args.a_format == 'codes' else 'fake-quant'} ({args.a_format}) -> {gemm_desc} "
+                         "(W[13824,5120] held as packed 8-bit HiF8, bias) -> y bf16"),
+            "M": M, "K": K, "N": N, "a_format": args.a_format, "route": route, "scale_max": 15.0,
         },
         "roofline": {
             "kernel": kernel_name,
@@ -655,8 +698,9 @@ def main():
             "traffic_source": "profiles/hif8_kernels_14b_720p_hbm_traffic.md (rocprofv3 FETCH_SIZE x2 + WRITE_SIZE)",
             "gemm_ms": round(gemm_ms, 4),
         },
-        "phases_ms": {"amax": round(amax_ms, 4), "quant": round(quant_ms, 4), "gemm": round(gemm_ms, 4),
-                      "events_sum": round(median(step_ms), 4)},
+        "phases_ms": {"amax": round(amax_ms, 4), "quant": round(quant_ms, 4), "weight_decode": round(wdec_ms, 4),
+                      "gemm": round(gemm_ms, 4), "events_sum": round(median(step_ms), 4)},
+        "other_route": other_route,
         "act_quant_GBps": round(enc_gbps, 1),
         "encode": encode,
         "shapes": extra_shapes,

@@ -167,6 +167,24 @@ int hif8_linear_fwd_gelu_amax(const void *a, const uint8_t *w_codes, const void 
                               hif8_stream_t stream);
 
 /* ---------------------------------------------------------------------------
+ * Decode-once route of hif8_linear_fwd for many rows: the same linear
+ *   y[M,N] = x_q[M,K] @ w_q[N,K]^T + bias
+ * (hif8_linear.py:86) with w_q given already dequantised, bf16 [N, K] -- hif8_decode of the
+ * packed codes with the weight's state, into a caller buffer, once per call.  The fused kernel
+ * decodes each weight element once per 256-row tile of x (M/256 times); this route decodes it
+ * once and streams bf16 W.  Same MFMA products in the same k order: the outputs equal
+ * hif8_linear_fwd's bit for bit.  Shapes, alignment and the GELU + amax and grouped variants
+ * as for hif8_linear_fwd / _gelu_amax / _grouped (w_q concatenated along N for groups).
+ * No counterpart of its own in the reference: it is F.linear on the dequantised operands. */
+int hif8_linear_fwd_wq(const uint16_t *a, const uint16_t *w_q, const uint16_t *bias, uint16_t *y, int64_t M,
+                       int64_t N, int64_t K, hif8_stream_t stream);
+int hif8_linear_fwd_wq_gelu_amax(const uint16_t *a, const uint16_t *w_q, const uint16_t *bias, uint16_t *y,
+                                 int64_t M, int64_t N, int64_t K, float scale_max, void *y_state,
+                                 hif8_stream_t stream);
+int hif8_linear_fwd_wq_grouped(const uint16_t *a, const uint16_t *w_q, const uint16_t *bias, uint16_t *const *ys,
+                               const int64_t *ns, int groups, int64_t M, int64_t K, hif8_stream_t stream);
+
+/* ---------------------------------------------------------------------------
  * GEMM-native operand layouts and the tiled fused linear (the fast path of
  * hif8_linear.py:68-86).
  *

@@ -43,6 +43,7 @@ from .hif8_linear import (  # noqa: F401
     GroupedWeight,
     grouped_ok,
     linear_fwd_grouped,
+    linear_fwd_wq,
 )
 from .ffn import HIF8FFN  # noqa: F401
 from . import dit  # noqa: F401
@@ -75,5 +76,5 @@ __all__ = [
     "save_packed", "load_packed", "pack_state_dict", "packed_from_codes", "fused_shape_ok", "linear_any",
     "linear_fwd_gelu_amax", "HIF8FFN", "WanLayerNorm", "modulate", "modulated_norm_quant",
     "qkv_from_modulated_norm", "GroupedWeight", "grouped_ok", "linear_fwd_grouped", "grouped_weight",
-    "dit", "OSPNextAttentionBlock", "OSPNextBlocks",
+    "dit", "OSPNextAttentionBlock", "OSPNextBlocks", "linear_fwd_wq",
 ]

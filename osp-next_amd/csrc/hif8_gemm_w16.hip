@@ -1,0 +1,436 @@
+// Decode-free twin of the fused HiF8 GEMM for MI355X (gfx950):
+//   Y[M,N] = X_q[M,K] . W_q[N,K]^T + bias[N]
+// with W_q already dequantised to bf16 (hif8_decode of the packed codes, once per call).  The
+// fused kernel (hif8_gemm_dtl.hip) decodes every weight element once per 256-row tile of X:
+// at M = 75600 that is 296 decodes per element, about a tenth of its cycles and of its energy
+// at the board's power limit.  Decoding W once into a workspace and streaming bf16 W costs one
+// pass over the codes and twice the weight bytes through L2; for a few thousand rows and more
+// it is the faster route.  The products are the same bf16 x fp32-accumulate MFMAs on the same
+// operand values, in the same k order, so the two kernels agree bit for bit.
+//
+// Design (shared with k_linear_dtl except for W):
+//   - One workgroup per 256 x 256 output tile, 4 waves; wave w owns output features
+//     n0 + 64w .. +63 for all 256 rows: 2 x 8 tiles of v_mfma_f32_32x32x16_bf16.
+//   - X and W (bf16, 32 KB each per 64-k step) go global -> LDS with buffer_load ... lds, two
+//     stages each, both in the same swizzled row layout; fragments are ds_read_b128.
+//   - The main loop is the fixed schedule in hif8_gemm_schedule_w16.inc (gen_gemm_schedule.py).
+//   - Epilogue: bias, RNE to bf16, staged through LDS into whole 512-byte row stores; the GELU +
+//     amax variant and grouped outputs as in k_linear_dtl.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "hif8_internal.h"
+#include "hif8_state_dev.h"
+
+namespace hif8 {
+namespace w16 {
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kTile = 256;
+constexpr int kBK = 64;
+constexpr int kThreads = 256;
+constexpr int kGroupM = 16;  // m-tiles per group in the tile order
+
+// LDS map (bytes): X stage s at s * 32K, W stage s at 64K + s * 32K, each 256 rows x 128 B with
+// the 16-B chunks of row m XOR-swizzled by f(m); the epilogue reuses everything.
+constexpr uint32_t kX0 = 0;
+constexpr uint32_t kW0 = 65536;
+constexpr uint32_t kOutRow = 528;  // epilogue: padded LDS row of the 256-wide output tile
+constexpr uint32_t kLds = 256 * kOutRow;
+static_assert(kLds >= 131072, "LDS holds the four operand stages");
+
+#define ASMV asm volatile
+
+template <int OFF> __device__ __forceinline__ void ldsb128(u32x4 &d, uint32_t a)
+{
+    ASMV("ds_read_b128 %0, %1 offset:%2" : "=v"(d) : "v"(a), "i"(OFF));
+}
+__device__ __forceinline__ void mfma(f32x16 &c, const u32x4 &a, const u32x4 &b)
+{
+    ASMV("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+a"(c) : "v"(a), "v"(b));
+}
+template <int N> __device__ __forceinline__ void wait_lgkm() { ASMV("s_waitcnt lgkmcnt(%0)" ::"i"(N)); }
+template <int N> __device__ __forceinline__ void wait_vm() { ASMV("s_waitcnt vmcnt(%0)" ::"i"(N)); }
+__device__ __forceinline__ void barrier() { ASMV("s_barrier" ::: "memory"); }
+// 64 lanes x 16 B from the buffer (voffset per lane) into LDS at m0v + lane*16
+__device__ __forceinline__ void dtl_load(uint32_t m0v, uint32_t voff, const u32x4 &rs)
+{
+    ASMV("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(m0v), "v"(voff), "s"(rs) : "memory", "m0");
+}
+__device__ __forceinline__ void tie(u32x4 &a) { ASMV("" : "+v"(a)); }
+
+// GELU with the tanh approximation, as k_linear_dtl's epilogue evaluates it.
+__device__ __forceinline__ float gelu_tanh(float x)
+{
+    const float u = 0.7978845608028654f * (x + 0.044715f * (x * x * x));
+    const float e = __builtin_amdgcn_exp2f(__builtin_fabsf(u) * 2.8853900817779268f);  // e^(2|u|)
+    const float d = 2.0f * __builtin_amdgcn_rcpf(1.0f + e);
+    const float th = __builtin_copysignf(1.0f - d, u);
+    return 0.5f * x * (1.0f + th);
+}
+
+__device__ __forceinline__ uint32_t f2bf_pk(float lo, float hi)
+{
+    typedef float f32x2 __attribute__((ext_vector_type(2)));
+    typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+    f32x2 v = {lo, hi};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
+}
+
+// Per-wave loop state.  Fragment sets alternate between phases: set 0 is consumed in phase 0
+// and filled in phase 1, set 1 the other way round.
+struct Ctx {
+    u32x4 B[2][16];   // [set][q*8 + j]  X fragments (m-tile j, k-half q)
+    u32x4 A[2][4];    // [set][q*2 + i]  W fragments (n-tile i, k-half q)
+    uint32_t xb[2][2];  // X fragment read base [k-half p][q]
+    uint32_t wb[2][2];  // W fragment read base [p][q]
+    f32x16 acc[2][8];
+    u32x4 rx, rw, ex, ew;  // buffer resources: X, W, and the effective ones (size 0 past the end)
+    int nk_eff;
+    uint32_t xoff[8], woff[8];  // DTL source offsets of the next k-step to load
+    uint32_t wave;
+};
+
+template <int I> __device__ __forceinline__ void adv(Ctx &c)
+{
+    if (I < 8) ASMV("v_add_u32 %0, 0x80, %0" : "+v"(c.xoff[I]));
+    else ASMV("v_add_u32 %0, 0x80, %0" : "+v"(c.woff[I - 8]));
+}
+__device__ __forceinline__ void advance_all(Ctx &c)
+{
+    adv<0>(c); adv<1>(c); adv<2>(c); adv<3>(c); adv<4>(c); adv<5>(c); adv<6>(c); adv<7>(c);
+    adv<8>(c); adv<9>(c); adv<10>(c); adv<11>(c); adv<12>(c); adv<13>(c); adv<14>(c); adv<15>(c);
+}
+
+// DTL item i of a k-step into stage S: items 0..7 are X, 8..15 W (8 x 1 KB per wave each)
+template <int S> __device__ __forceinline__ void issue_dtl(Ctx &c, int i)
+{
+    if (i < 8) {
+        const uint32_t m0v = __builtin_amdgcn_readfirstlane(kX0 + S * 32768u + (c.wave * 8u + i) * 1024u);
+        dtl_load(m0v, c.xoff[i], c.ex);
+    } else {
+        const uint32_t m0v = __builtin_amdgcn_readfirstlane(kW0 + S * 32768u + (c.wave * 8u + (i - 8)) * 1024u);
+        dtl_load(m0v, c.woff[i - 8], c.ew);
+    }
+}
+
+template <int NS, int NP, int NXT, int J, int Q> __device__ __forceinline__ void rd_x(Ctx &c)
+{
+    ldsb128<NS * 32768 + J * 4096>(c.B[NXT][Q * 8 + J], c.xb[NP][Q]);
+}
+template <int NS, int NP, int NXT, int I, int Q> __device__ __forceinline__ void rd_w(Ctx &c)
+{
+    ldsb128<NS * 32768 + I * 4096>(c.A[NXT][Q * 2 + I], c.wb[NP][Q]);
+}
+template <int CUR, int MI> __device__ __forceinline__ void mm(Ctx &c)
+{
+    constexpr int q = MI / 16, i = (MI / 8) % 2, j = MI % 8;
+    mfma(c.acc[i][j], c.A[CUR][q * 2 + i], c.B[CUR][q * 8 + j]);
+}
+// after the wait covering the k-half Q fragments of set SET
+template <int SET, int Q> __device__ __forceinline__ void tie_q(Ctx &c)
+{
+#pragma unroll
+    for (int j = 0; j < 8; ++j) tie(c.B[SET][Q * 8 + j]);
+    tie(c.A[SET][Q * 2]);
+    tie(c.A[SET][Q * 2 + 1]);
+}
+
+#include "hif8_gemm_schedule_w16.inc"
+
+// EPI 0: y = rnd(acc + bias).  EPI 1: y = rnd(gelu(rnd(acc + bias))) with amax|y| folded into
+// y_st (scale for y_smax).  The output features are G.n groups, each with its output buffer.
+template <int EPI>
+__global__ __launch_bounds__(kThreads, 1) void k_linear_w16(const uint16_t *__restrict__ X, const uint16_t *__restrict__ Wq,
+                                                            const Groups G, const uint16_t *__restrict__ bias,
+                                                            int M, int N, int K, int tiles_m, int tiles_n,
+                                                            State *__restrict__ y_st, float y_smax)
+{
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[kLds];
+    ASMV("; lds base %0" ::"v"(uint32_t(uintptr_t(smem))) : "memory");
+    Ctx c;
+    const uint32_t tid = threadIdx.x, lane = tid & 63u;
+    c.wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t r = lane & 31u, h = lane >> 5;
+
+    // tile order: groups of kGroupM m-tiles, n-tiles outer within a group (as k_linear_dtl)
+    const int t = blockIdx.x;
+    const int group = t / (kGroupM * tiles_n);
+    const int first_m = group * kGroupM;
+    const int gm = (tiles_m - first_m) < kGroupM ? (tiles_m - first_m) : kGroupM;
+    const int within = t - group * kGroupM * tiles_n;
+    const int m0 = (first_m + within % gm) * kTile;
+    const int n0 = (within / gm) * kTile;
+    int gi = 0;
+    while (gi + 1 < G.n && n0 / kTile >= G.tile_end[gi]) ++gi;
+    uint16_t *__restrict__ Y = G.y[gi];
+    const int col0 = gi == 0 ? 0 : G.tile_end[gi - 1] * kTile;
+    const int ycols = G.cols[gi];
+
+    {
+        const uint64_t xa = uint64_t(X) + uint64_t(m0) * uint64_t(K) * 2u;
+        const uint32_t xrows = uint32_t(M - m0 < kTile ? M - m0 : kTile);
+        c.rx = u32x4{uint32_t(xa), uint32_t(xa >> 32), xrows * uint32_t(K) * 2u, 0x00020000u};
+        const uint64_t wa = uint64_t(Wq) + uint64_t(n0) * uint64_t(K) * 2u;
+        const uint32_t wrows = uint32_t(N - n0 < kTile ? N - n0 : kTile);
+        c.rw = u32x4{uint32_t(wa), uint32_t(wa >> 32), wrows * uint32_t(K) * 2u, 0x00020000u};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            c.rx[i] = __builtin_amdgcn_readfirstlane(c.rx[i]);
+            c.rw[i] = __builtin_amdgcn_readfirstlane(c.rw[i]);
+        }
+    }
+    // DTL source offsets of k-step 0.  LDS 16-B slot s of a stage is written by lane s%64 of
+    // load s/64; its source chunk is the slot's chunk un-swizzled (the XOR is an involution).
+    // X and W rows share the layout.
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const uint32_t row = (c.wave * 8u + i) * 8u + (lane >> 3);
+        const uint32_t ch = (lane & 7u) ^ (lane >> 3) ^ uint32_t(i & 1);
+        c.xoff[i] = row * uint32_t(K) * 2u + ch * 16u;
+        c.woff[i] = c.xoff[i];
+    }
+    // Fragment read bases.  Row m, 16-B chunk k/8 sits at m*128 + ((chunk ^ f(m)) << 4),
+    // f(m) = (m & 7) ^ ((m >> 3) & 1): the 32 rows of a fragment read hit distinct banks.
+    // MFMA k-slot (half h, e) of k-half q in phase p is k = 32p + 16h + 8q + e for both
+    // operands (the order k_linear_dtl uses).
+    const uint32_t fr = (r & 7u) ^ ((r >> 3) & 1u);
+#pragma unroll
+    for (int p = 0; p < 2; ++p)
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+            const uint32_t ch = ((4u * p + 2u * h + q) ^ fr) << 4;
+            c.xb[p][q] = kX0 + r * 128u + ch;
+            c.wb[p][q] = kW0 + (c.wave * 64u + r) * 128u + ch;
+        }
+
+    const int nk = K / kBK;
+    const int odd = nk & 1;  // an odd k-step count gets a zero k-step in front
+    c.nk_eff = nk + odd;
+    c.ex = c.rx;
+    c.ew = c.rw;
+    if (odd) {
+#pragma unroll
+        for (int it = 0; it < 8; ++it) {
+            *(u32x4 *)(smem + kX0 + (uint32_t(it) * 256u + tid) * 16u) = u32x4{0, 0, 0, 0};
+            *(u32x4 *)(smem + kW0 + (uint32_t(it) * 256u + tid) * 16u) = u32x4{0, 0, 0, 0};
+        }
+    }
+    wait_lgkm<0>();
+    if (!odd) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) issue_dtl<0>(c, i);
+        advance_all(c);
+    }
+    c.ex[2] = c.nk_eff > 1 ? c.rx[2] : 0u;
+    c.ew[2] = c.nk_eff > 1 ? c.rw[2] : 0u;
+    // DTL(1) items 12..15 are issued by the first phase 0, which then advances the offsets
+#pragma unroll
+    for (int i = 0; i < 12; ++i) issue_dtl<1>(c, i);
+    wait_vm<12>();
+    barrier();
+    // reads for phase (0, 0) from stage 0 into set 0
+    rd_x<0, 0, 0, 0, 0>(c); rd_x<0, 0, 0, 1, 0>(c); rd_x<0, 0, 0, 2, 0>(c); rd_x<0, 0, 0, 3, 0>(c);
+    rd_x<0, 0, 0, 4, 0>(c); rd_x<0, 0, 0, 5, 0>(c); rd_x<0, 0, 0, 6, 0>(c); rd_x<0, 0, 0, 7, 0>(c);
+    rd_w<0, 0, 0, 0, 0>(c); rd_w<0, 0, 0, 1, 0>(c);
+    rd_x<0, 0, 0, 0, 1>(c); rd_x<0, 0, 0, 1, 1>(c); rd_x<0, 0, 0, 2, 1>(c); rd_x<0, 0, 0, 3, 1>(c);
+    rd_x<0, 0, 0, 4, 1>(c); rd_x<0, 0, 0, 5, 1>(c); rd_x<0, 0, 0, 6, 1>(c); rd_x<0, 0, 0, 7, 1>(c);
+    rd_w<0, 0, 0, 0, 1>(c); rd_w<0, 0, 0, 1, 1>(c);
+
+#pragma unroll
+    for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) c.acc[i][j] = f32x16{};
+    // Two k-steps per iteration (stage 0 then stage 1).  The loads of k-step kt+2 use the
+    // resources with size 0 past the end: they read nothing and nothing consumes them.
+    for (int kt = 0; kt < c.nk_eff; kt += 2) {
+        phase0<0>(c);
+        c.ex[2] = kt + 2 < c.nk_eff ? c.rx[2] : 0u;
+        c.ew[2] = kt + 2 < c.nk_eff ? c.rw[2] : 0u;
+        phase1<0>(c);
+        phase0<1>(c);
+        c.ex[2] = kt + 3 < c.nk_eff ? c.rx[2] : 0u;
+        c.ew[2] = kt + 3 < c.nk_eff ? c.rw[2] : 0u;
+        phase1<1>(c);
+    }
+    // no load may still target LDS when it is reused or released
+    wait_vm<0>();
+    wait_lgkm<0>();
+    ASMV("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7"
+         : "+a"(c.acc[0][0]), "+a"(c.acc[0][1]), "+a"(c.acc[0][2]), "+a"(c.acc[0][3]), "+a"(c.acc[0][4]),
+           "+a"(c.acc[0][5]), "+a"(c.acc[0][6]), "+a"(c.acc[0][7]), "+a"(c.acc[1][0]), "+a"(c.acc[1][1]),
+           "+a"(c.acc[1][2]), "+a"(c.acc[1][3]), "+a"(c.acc[1][4]), "+a"(c.acc[1][5]), "+a"(c.acc[1][6]),
+           "+a"(c.acc[1][7]));
+
+    // Epilogue.  acc[i][j] lane (r, h), element e: D[n][m] with n = 64w + 32i + 8(e/4) + 4h + e%4,
+    // m = 32j + r.  Rows go to LDS (padded), then each wave stores 2 rows x 512 B per instruction.
+    __syncthreads();
+    uint32_t ymax = 0;  // EPI 1: largest magnitude bits of this lane's in-range outputs
+    {
+        const uint32_t wl = c.wave * 64u;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const uint32_t nl = wl + uint32_t(i * 32 + 8 * g) + 4u * h;
+                const int n = n0 + int(nl);
+                float b0 = 0.f, b1 = 0.f, b2 = 0.f, b3 = 0.f;
+                if (bias && n < N) {
+                    const uint2 bb = *(const uint2 *)(bias + n);
+                    b0 = __builtin_bit_cast(float, bb.x << 16);
+                    b1 = __builtin_bit_cast(float, bb.x & 0xFFFF0000u);
+                    b2 = __builtin_bit_cast(float, bb.y << 16);
+                    b3 = __builtin_bit_cast(float, bb.y & 0xFFFF0000u);
+                }
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    const f32x16 &a = c.acc[i][j];
+                    uint2 v;
+                    if (EPI == 0) {
+                        v.x = f2bf_pk(a[4 * g] + b0, a[4 * g + 1] + b1);
+                        v.y = f2bf_pk(a[4 * g + 2] + b2, a[4 * g + 3] + b3);
+                    } else {
+                        const uint32_t p01 = f2bf_pk(a[4 * g] + b0, a[4 * g + 1] + b1);
+                        const uint32_t p23 = f2bf_pk(a[4 * g + 2] + b2, a[4 * g + 3] + b3);
+                        v.x = f2bf_pk(gelu_tanh(bf2f(p01 & 0xFFFFu)), gelu_tanh(bf2f(p01 >> 16)));
+                        v.y = f2bf_pk(gelu_tanh(bf2f(p23 & 0xFFFFu)), gelu_tanh(bf2f(p23 >> 16)));
+                        const int m = m0 + j * 32 + int(r);
+                        if (n < N && m < M) {
+                            typedef uint16_t u16x2 __attribute__((ext_vector_type(2)));
+                            const u16x2 mg = __builtin_elementwise_max(__builtin_bit_cast(u16x2, v.x & 0x7FFF7FFFu),
+                                                                       __builtin_bit_cast(u16x2, v.y & 0x7FFF7FFFu));
+                            ymax = max(ymax, uint32_t(max(mg.x, mg.y)));
+                        }
+                    }
+                    *(uint2 *)(smem + (uint32_t(j * 32) + r) * kOutRow + nl * 2u) = v;
+                }
+            }
+        }
+    }
+    __syncthreads();
+    {
+        const uint32_t colb = (lane & 31u) * 16u;
+        const int n = n0 + int(colb / 2u);
+#pragma unroll
+        for (int blk = 0; blk < 4; ++blk) {
+            u32x4 v[8];
+#pragma unroll
+            for (int it = 0; it < 8; ++it) {
+                const uint32_t row = c.wave * 64u + uint32_t(blk * 8 + it) * 2u + h;
+                v[it] = *(const u32x4 *)(smem + row * kOutRow + colb);
+            }
+#pragma unroll
+            for (int it = 0; it < 8; ++it) {
+                const int m = m0 + int(c.wave * 64u + uint32_t(blk * 8 + it) * 2u + h);
+                if (m < M && n - col0 < ycols) *(u32x4 *)(Y + size_t(m) * size_t(ycols) + (n - col0)) = v[it];
+            }
+        }
+    }
+    if (EPI == 1) {
+        for (int o = 32; o > 0; o >>= 1) ymax = max(ymax, (uint32_t)__shfl_xor((int)ymax, o, 64));
+        uint32_t *red = (uint32_t *)smem;  // the staging rows are read: reuse after the barrier
+        __syncthreads();
+        if (lane == 0) red[c.wave] = ymax;
+        __syncthreads();
+        ymax = max(max(red[0], red[1]), max(red[2], red[3]));
+        fold_amax(y_st, ymax, gridDim.x, kBF16, y_smax, red + 4);
+    }
+}
+
+}  // namespace w16
+
+// Shapes: K % 64 == 0, N % 8 == 0, 16-byte aligned X, W_q and Y, 8-byte aligned bias (checked
+// by the caller).  M, N < 2^31, K < 2^22.  y_st != NULL selects the GELU + amax epilogue.
+static int launch_w16(const uint16_t *x, const uint16_t *w_q, const Groups &g, const uint16_t *bias, int64_t M,
+                      int64_t N, int64_t K, hif8_stream_t stream, State *y_st, float y_smax)
+{
+    hipStream_t s = (hipStream_t)stream;
+    if (K >= (int64_t(1) << 22)) return HIF8_ERR_SHAPE;
+    const int tiles_m = int((M + w16::kTile - 1) / w16::kTile);
+    const int tiles_n = int((N + w16::kTile - 1) / w16::kTile);
+    const int64_t tiles = int64_t(tiles_m) * tiles_n;
+    if (tiles >= (int64_t(1) << 31)) return HIF8_ERR_SHAPE;
+    if (y_st)
+        hipLaunchKernelGGL(w16::k_linear_w16<1>, dim3(unsigned(tiles)), dim3(w16::kThreads), 0, s, x, w_q, g, bias,
+                           int(M), int(N), int(K), tiles_m, tiles_n, y_st, y_smax);
+    else
+        hipLaunchKernelGGL(w16::k_linear_w16<0>, dim3(unsigned(tiles)), dim3(w16::kThreads), 0, s, x, w_q, g, bias,
+                           int(M), int(N), int(K), tiles_m, tiles_n, (State *)nullptr, 0.0f);
+    return hipGetLastError() == hipSuccess ? HIF8_OK : HIF8_ERR_HIP;
+}
+
+int launch_linear_w16(const uint16_t *x, const uint16_t *w_q, const uint16_t *bias, uint16_t *y, int64_t M,
+                      int64_t N, int64_t K, hif8_stream_t stream, State *y_st, float y_smax)
+{
+    Groups g{};
+    g.n = 1;
+    g.tile_end[0] = int((N + w16::kTile - 1) / w16::kTile);
+    g.cols[0] = int(N);
+    g.y[0] = y;
+    return launch_w16(x, w_q, g, bias, M, N, K, stream, y_st, y_smax);
+}
+
+int launch_linear_w16_groups(const uint16_t *x, const uint16_t *w_q, const Groups &g, const uint16_t *bias,
+                             int64_t M, int64_t N, int64_t K, hif8_stream_t stream)
+{
+    return launch_w16(x, w_q, g, bias, M, N, K, stream, nullptr, 0.0f);
+}
+
+}  // namespace hif8
+
+using namespace hif8;
+
+static int check_w16(const void *a, const void *w_q, const uint16_t *bias, const void *y, int64_t M, int64_t N,
+                     int64_t K)
+{
+    if (!a || !w_q || !y) return HIF8_ERR_ARG;
+    if (M <= 0 || N <= 0 || K <= 0) return HIF8_ERR_ARG;
+    if (M >= (int64_t(1) << 31) || N >= (int64_t(1) << 31) || K >= (int64_t(1) << 22)) return HIF8_ERR_SHAPE;
+    if (K % w16::kBK != 0 || N % 8 != 0) return HIF8_ERR_SHAPE;
+    if (((uintptr_t)a | (uintptr_t)w_q | (uintptr_t)y) & 15u) return HIF8_ERR_ALIGN;
+    if (bias && ((uintptr_t)bias & 7u)) return HIF8_ERR_ALIGN;
+    const int64_t tiles = ((M + w16::kTile - 1) / w16::kTile) * ((N + w16::kTile - 1) / w16::kTile);
+    if (tiles >= (int64_t(1) << 31)) return HIF8_ERR_SHAPE;
+    return HIF8_OK;
+}
+
+extern "C" int hif8_linear_fwd_wq(const uint16_t *a, const uint16_t *w_q, const uint16_t *bias, uint16_t *y,
+                                  int64_t M, int64_t N, int64_t K, hif8_stream_t stream)
+{
+    const int rc = check_w16(a, w_q, bias, y, M, N, K);
+    return rc != HIF8_OK ? rc : launch_linear_w16(a, w_q, bias, y, M, N, K, stream, nullptr, 0.0f);
+}
+
+extern "C" int hif8_linear_fwd_wq_gelu_amax(const uint16_t *a, const uint16_t *w_q, const uint16_t *bias,
+                                            uint16_t *y, int64_t M, int64_t N, int64_t K, float scale_max,
+                                            void *y_state, hif8_stream_t stream)
+{
+    if (!y_state) return HIF8_ERR_ARG;
+    const int rc = check_w16(a, w_q, bias, y, M, N, K);
+    return rc != HIF8_OK ? rc : launch_linear_w16(a, w_q, bias, y, M, N, K, stream, (State *)y_state, scale_max);
+}
+
+extern "C" int hif8_linear_fwd_wq_grouped(const uint16_t *a, const uint16_t *w_q, const uint16_t *bias,
+                                          uint16_t *const *ys, const int64_t *ns, int groups, int64_t M, int64_t K,
+                                          hif8_stream_t stream)
+{
+    if (!ys || !ns || groups < 1) return HIF8_ERR_ARG;
+    if (groups > kMaxGroups) return HIF8_ERR_SHAPE;
+    Groups g{};
+    g.n = groups;
+    int64_t N = 0;
+    for (int i = 0; i < groups; ++i) {
+        if (!ys[i] || ns[i] <= 0) return HIF8_ERR_ARG;
+        if (ns[i] % 8 != 0 || (i + 1 < groups && ns[i] % w16::kTile != 0)) return HIF8_ERR_SHAPE;
+        if ((uintptr_t)ys[i] & 15u) return HIF8_ERR_ALIGN;
+        N += ns[i];
+        if (N >= (int64_t(1) << 31)) return HIF8_ERR_SHAPE;
+        g.tile_end[i] = int((N + w16::kTile - 1) / w16::kTile);
+        g.cols[i] = int(ns[i]);
+        g.y[i] = ys[i];
+    }
+    const int rc = check_w16(a, w_q, bias, ys[0], M, N, K);
+    return rc != HIF8_OK ? rc : launch_linear_w16_groups(a, w_q, g, bias, M, N, K, stream);
+}

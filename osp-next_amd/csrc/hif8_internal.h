@@ -46,6 +46,11 @@ struct Groups {
 int launch_linear_dtl(const uint16_t *x, const uint8_t *w_codes, const State *w_st, const uint16_t *bias,
                       uint16_t *y, int64_t M, int64_t N, int64_t K, hif8_stream_t stream, State *y_st = nullptr,
                       float y_smax = 0.0f);
+// The decode-free twin (hif8_gemm_w16.hip): W given as dequantised bf16 [N, K].
+int launch_linear_w16(const uint16_t *x, const uint16_t *w_q, const uint16_t *bias, uint16_t *y, int64_t M,
+                      int64_t N, int64_t K, hif8_stream_t stream, State *y_st, float y_smax);
+int launch_linear_w16_groups(const uint16_t *x, const uint16_t *w_q, const Groups &g, const uint16_t *bias,
+                             int64_t M, int64_t N, int64_t K, hif8_stream_t stream);
 // The grouped form: N is the total of the groups' features.
 int launch_linear_dtl_groups(const uint16_t *x, const uint8_t *w_codes, const Groups &g, const uint16_t *bias,
                              int64_t M, int64_t N, int64_t K, hif8_stream_t stream);

@@ -124,11 +124,16 @@ def fake_quant(x: Tensor, state: QuantState, semantics: int = _lib.SEM_NPU) -> T
     return y
 
 
-def decode(codes: Tensor, state: QuantState, dtype: torch.dtype = torch.bfloat16) -> Tensor:
-    """x_q = decode(code) / scale in ``dtype``."""
+def decode(codes: Tensor, state: QuantState, dtype: torch.dtype = torch.bfloat16, out: Optional[Tensor] = None) -> Tensor:
+    """x_q = decode(code) / scale in ``dtype`` (into ``out`` when given: contiguous, 16-byte aligned)."""
     _lib.require_gpu_tensor(codes, "codes")
     codes = _aligned(codes)
-    y = torch.empty(codes.shape, dtype=dtype, device=codes.device)
+    if out is None:
+        y = torch.empty(codes.shape, dtype=dtype, device=codes.device)
+    else:
+        if out.dtype != dtype or out.numel() != codes.numel() or not out.is_contiguous() or out.data_ptr() % 16:
+            raise ValueError("decode: out must be a contiguous, 16-byte aligned tensor of the codes' size and dtype")
+        y = out
     if codes.numel():
         _lib.check(_lib.load().hif8_decode(codes.data_ptr(), codes.numel(), state.ptr, _lib.dtype_code(dtype),
                                            y.data_ptr(), _lib.stream_ptr(codes.device)), "hif8_decode")
@@ -232,6 +237,44 @@ def linear_dgrad(grad_q2: Tensor, w: "PackedWeight") -> Tensor:
     return y
 
 
+# GEMM route for bf16 activations: "fused" decodes the packed weight inside the GEMM (each
+# element once per 256-row tile of x), "decode_once" decodes it into a bf16 buffer per call and
+# runs the decode-free twin (hif8_linear_fwd_wq), "auto" takes decode_once from
+# DECODE_ONCE_MIN_ROWS rows up.  Both give the same bits.
+GEMM_ROUTE = "auto"
+DECODE_ONCE_MIN_ROWS = 8192   # measured: the routes tie near 8192 rows (14B FFN-up), decode_once wins above
+
+
+def decode_once(M: int) -> bool:
+    if GEMM_ROUTE not in ("auto", "fused", "decode_once"):
+        raise ValueError(f"GEMM_ROUTE must be auto, fused or decode_once, not {GEMM_ROUTE!r}")
+    return GEMM_ROUTE == "decode_once" or (GEMM_ROUTE == "auto" and M >= DECODE_ONCE_MIN_ROWS)
+
+
+def linear_fwd_wq(a: Tensor, w_q: Tensor, bias: Optional[Tensor], y_state: Optional[QuantState] = None,
+                  scale_max: float = 15.0) -> Tensor:
+    """hif8_linear_fwd_wq[_gelu_amax]: y = x_q @ w_q^T + bias with w_q the dequantised bf16 weight
+    [N, K] (``PackedWeight.dequantize()``); with ``y_state`` the GELU + amax epilogue."""
+    M, K = a.shape
+    N = w_q.shape[0]
+    if w_q.shape[1] != K or w_q.dtype != torch.bfloat16 or a.dtype != torch.bfloat16:
+        raise ValueError("linear_fwd_wq takes bf16 x_q [M, K] and bf16 w_q [N, K]")
+    y = torch.empty((M, N), dtype=torch.bfloat16, device=a.device)
+    b_ptr = None
+    if bias is not None:
+        bias = bias.detach().to(torch.bfloat16).contiguous()
+        b_ptr = bias.data_ptr()
+    L = _lib.load()
+    s = _lib.stream_ptr(a.device)
+    if y_state is None:
+        _lib.check(L.hif8_linear_fwd_wq(a.data_ptr(), w_q.data_ptr(), b_ptr, y.data_ptr(), M, N, K, s),
+                   "hif8_linear_fwd_wq")
+    else:
+        _lib.check(L.hif8_linear_fwd_wq_gelu_amax(a.data_ptr(), w_q.data_ptr(), b_ptr, y.data_ptr(), M, N, K,
+                                                  float(scale_max), y_state.ptr, s), "hif8_linear_fwd_wq_gelu_amax")
+    return y
+
+
 def fused_shape_ok(N: int, K: int) -> bool:
     """Shapes hif8_linear_fwd takes: in_features K % 64 == 0, out_features N % 8 == 0."""
     return K % 64 == 0 and N % 8 == 0 and K < (1 << 22)
@@ -251,11 +294,14 @@ def linear_any(a: Tensor, a_fmt: int, a_state: Optional[QuantState], w: PackedWe
 
 def linear_fwd(a: Tensor, a_fmt: int, a_state: Optional[QuantState], w: PackedWeight,
                bias: Optional[Tensor]) -> Tensor:
-    """hif8_linear_fwd: y[M,N] = x_q[M,K] @ w_q[N,K]^T + bias, bf16 out."""
+    """hif8_linear_fwd: y[M,N] = x_q[M,K] @ w_q[N,K]^T + bias, bf16 out (bf16 activations from
+    DECODE_ONCE_MIN_ROWS rows up: the weight decoded once, then hif8_linear_fwd_wq)."""
     M, K = a.shape
     N = w.shape[0]
     if w.shape[1] != K:
         raise ValueError(f"in_features mismatch: x has {K}, weight has {w.shape[1]}")
+    if a_fmt == _lib.A_BF16 and decode_once(M):
+        return linear_fwd_wq(a, w.dequantize(torch.bfloat16), bias)
     y = torch.empty((M, N), dtype=torch.bfloat16, device=a.device)
     b_ptr = 0
     if bias is not None:
@@ -313,11 +359,20 @@ def linear_fwd_grouped(a: Tensor, gw: GroupedWeight) -> "List[Tensor]":
         raise TypeError("the grouped GEMM takes the bf16 x_q")
     ys = [torch.empty((M, n), dtype=torch.bfloat16, device=a.device) for n in gw.ns]
     g = len(ys)
-    states = (ctypes.c_void_p * g)(*[p.state.ptr for p in gw.packs])
     outs = (ctypes.c_void_p * g)(*[y.data_ptr() for y in ys])
     ns = (ctypes.c_int64 * g)(*gw.ns)
-    _lib.check(_lib.load().hif8_linear_fwd_grouped(a.data_ptr(), gw.codes.data_ptr(), states,
-                                                   gw.bias.data_ptr() if gw.bias is not None else None, outs, ns,
+    b_ptr = gw.bias.data_ptr() if gw.bias is not None else None
+    if decode_once(M):
+        w_q = torch.empty((sum(gw.ns), K), dtype=torch.bfloat16, device=a.device)
+        row = 0
+        for p, n in zip(gw.packs, gw.ns):
+            decode(p.codes, p.state, torch.bfloat16, out=w_q[row:row + n])
+            row += n
+        _lib.check(_lib.load().hif8_linear_fwd_wq_grouped(a.data_ptr(), w_q.data_ptr(), b_ptr, outs, ns, g, M, K,
+                                                          _lib.stream_ptr(a.device)), "hif8_linear_fwd_wq_grouped")
+        return ys
+    states = (ctypes.c_void_p * g)(*[p.state.ptr for p in gw.packs])
+    _lib.check(_lib.load().hif8_linear_fwd_grouped(a.data_ptr(), gw.codes.data_ptr(), states, b_ptr, outs, ns,
                                                    g, M, K, _lib.stream_ptr(a.device)), "hif8_linear_fwd_grouped")
     return ys
 
@@ -332,6 +387,8 @@ def linear_fwd_gelu_amax(a: Tensor, w: PackedWeight, bias: Optional[Tensor], y_s
         raise ValueError(f"in_features mismatch: x has {K}, weight has {w.shape[1]}")
     if a.dtype != torch.bfloat16:
         raise TypeError("the GELU + amax epilogue takes bf16 activations")
+    if decode_once(M):
+        return linear_fwd_wq(a, w.dequantize(torch.bfloat16), bias, y_state, scale_max)
     y = torch.empty((M, N), dtype=torch.bfloat16, device=a.device)
     b_ptr = None
     if bias is not None:

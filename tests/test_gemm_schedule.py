@@ -24,6 +24,8 @@ def test_schedule_include_is_generated():
     spec.loader.exec_module(gen)
     with open(os.path.join(CSRC, "hif8_gemm_schedule.inc")) as f:
         assert f.read() == gen.generate()
+    with open(os.path.join(CSRC, "hif8_gemm_schedule_w16.inc")) as f:
+        assert f.read() == gen.generate_w16()
 
 
 @pytest.fixture(scope="module")
@@ -87,3 +89,39 @@ def test_checker_catches_planted_mistakes():
         "v_mfma_f32_32x32x16_bf16 a[0:15], v[4:7], v[12:15], a[0:15]",
     ])
     assert not isa_check.check_body(ok)
+
+
+@pytest.fixture(scope="module")
+def w16_asm(tmp_path_factory):
+    if not os.path.exists(HIPCC):
+        pytest.skip("hipcc not available")
+    out = tmp_path_factory.mktemp("isa16") / "w16.s"
+    cmd = [HIPCC, "-O3", "-std=c++17", "--offload-arch=gfx950", "-Xclang", "-target-feature", "-Xclang",
+           "-packed-fp32-ops", "--cuda-device-only", "-S", os.path.join(CSRC, "hif8_gemm_w16.hip"), "-o", str(out),
+           "-Rpass-analysis=kernel-resource-usage"]
+    r = subprocess.run(cmd, capture_output=True, text=True, timeout=600)
+    assert r.returncode == 0, r.stderr[-2000:]
+    return out.read_text(), r.stderr
+
+
+def test_w16_resources(w16_asm):
+    """The decode-free twin: both instantiations, no spills, the 132 KB LDS array."""
+    _, remarks = w16_asm
+    spills = re.findall(r"(?:VGPRs|SGPRs) Spill: (\d+)", remarks)
+    lds = re.findall(r"LDS Size \[bytes/block\]: (\d+)", remarks)
+    scratch = re.findall(r"ScratchSize \[bytes/lane\]: (\d+)", remarks)
+    assert len(lds) == 2 and set(lds) == {"135168"}, lds
+    assert spills and set(spills) == {"0"}, spills
+    assert scratch and set(scratch) == {"0"}, scratch
+
+
+def test_w16_main_loop_hazards(w16_asm):
+    """Per 2 k-steps: 128 MFMAs, 80 fragment reads (20 per phase), 32 global->LDS loads."""
+    import isa_check
+    loops = isa_check.mfma_loops(w16_asm[0])
+    assert len(loops) == 2
+    for body in loops:
+        kinds = isa_check.census(body)
+        assert kinds.get("mfma") == 128 and kinds.get("lds_load") == 80 and kinds.get("lds_dma") == 32, kinds
+        errors = isa_check.check_body(body)
+        assert not errors, "\n".join(errors[:20])
