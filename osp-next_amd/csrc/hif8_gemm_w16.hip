@@ -8,11 +8,19 @@
 // it is the faster route.  The products are the same bf16 x fp32-accumulate MFMAs on the same
 // operand values, in the same k order, so the two kernels agree bit for bit.
 //
-// Design (shared with k_linear_dtl except for W):
-//   - One workgroup per 256 x 256 output tile, 4 waves; wave w owns output features
-//     n0 + 64w .. +63 for all 256 rows: 2 x 8 tiles of v_mfma_f32_32x32x16_bf16.
-//   - X and W (bf16, 32 KB each per 64-k step) go global -> LDS with buffer_load ... lds, two
-//     stages each, both in the same swizzled row layout; fragments are ds_read_b128.
+// Design (shared with k_linear_dtl except for W, the wave quadrants and the LDS ring):
+//   - One workgroup per 256 x 256 output tile, 4 waves; wave w owns the 128 x 128 quadrant of
+//     rows 128 (w & 1) .. +127 and output features 128 (w >> 1) .. +127: 4 x 4 tiles of
+//     v_mfma_f32_32x32x16_bf16.  (k_linear_dtl gives each wave 64 features for all 256 rows
+//     because a wave decodes the W rows it uses; with W already bf16 the quadrants read a fifth
+//     less from LDS per k-step.)
+//   - X and W (bf16) go global -> LDS with buffer_load ... lds.  LDS is a ring of five 32 KB
+//     operand stages (one operand, 256 rows x 64 k each; 160 KB): k-step j's X and W take
+//     stages 2j and 2j + 1.  Each k-step has one barrier (in its second phase); the X loads of
+//     k-step j + 2 are issued in the first phase of k-step j and the W loads right after the
+//     barrier, so they have three and two phases to land.  With two 64 KB stages (128 KB) the
+//     last loads of a k-step had less than one phase, and the loop waited for the misses of
+//     every panel that L2 does not hold.
 //   - The main loop is the fixed schedule in hif8_gemm_schedule_w16.inc (gen_gemm_schedule.py).
 //   - Epilogue: bias, RNE to bf16, staged through LDS into whole 512-byte row stores; the GELU +
 //     amax variant and grouped outputs as in k_linear_dtl.
@@ -33,13 +41,14 @@ constexpr int kBK = 64;
 constexpr int kThreads = 256;
 constexpr int kGroupM = 16;  // m-tiles per group in the tile order
 
-// LDS map (bytes): X stage s at s * 32K, W stage s at 64K + s * 32K, each 256 rows x 128 B with
-// the 16-B chunks of row m XOR-swizzled by f(m); the epilogue reuses everything.
-constexpr uint32_t kX0 = 0;
-constexpr uint32_t kW0 = 65536;
+// LDS map (bytes): operand stage s (0..4) at s * 32K, 256 rows x 128 B (64 k) with the 16-B
+// chunks of row m XOR-swizzled by f(m) = (m & 7) ^ ((m >> 3) & 1): the 32 rows of a fragment
+// read hit distinct banks.  The epilogue reuses the first 132 KB.
+constexpr uint32_t kSlot = 32768;
+constexpr uint32_t kSlots = 5;
 constexpr uint32_t kOutRow = 528;  // epilogue: padded LDS row of the 256-wide output tile
-constexpr uint32_t kLds = 256 * kOutRow;
-static_assert(kLds >= 131072, "LDS holds the four operand stages");
+constexpr uint32_t kLds = kSlots * kSlot;
+static_assert(kLds >= 256 * kOutRow, "the epilogue staging fits in the ring");
 
 #define ASMV asm volatile
 
@@ -79,63 +88,73 @@ __device__ __forceinline__ uint32_t f2bf_pk(float lo, float hi)
     return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
 }
 
-// Per-wave loop state.  Fragment sets alternate between phases: set 0 is consumed in phase 0
-// and filled in phase 1, set 1 the other way round.
+// Per-wave loop state.  Fragment sets alternate between phases: set 0 is consumed in the even
+// phase (first 32 k of a k-step) and filled in the odd one, set 1 the other way round.
 struct Ctx {
-    u32x4 B[2][16];   // [set][q*8 + j]  X fragments (m-tile j, k-half q)
-    u32x4 A[2][4];    // [set][q*2 + i]  W fragments (n-tile i, k-half q)
-    uint32_t xb[2][2];  // X fragment read base [k-half p][q]
-    uint32_t wb[2][2];  // W fragment read base [p][q]
-    f32x16 acc[2][8];
+    u32x4 B[2][8];    // [set][q*4 + j]  X fragments (m-tile j, k-half q)
+    u32x4 A[2][8];    // [set][q*4 + i]  W fragments (n-tile i, k-half q)
+    uint32_t xb[2][2], wb[2][2];  // fragment read bases in stage 0 [phase p][q]
+    uint32_t xr[2], wr[2];        // the same in the stages read this phase [q]
+    f32x16 acc[4][4];
     u32x4 rx, rw, ex, ew;  // buffer resources: X, W, and the effective ones (size 0 past the end)
-    int nk_eff;
-    uint32_t xoff[8], woff[8];  // DTL source offsets of the next k-step to load
+    uint32_t xoff[8], woff[8];  // DTL source offsets of the next X and W stage to load
+    uint32_t xs, ws, ls;  // LDS offsets of the X and W stages read and of the stage loaded this phase
     uint32_t wave;
 };
 
+__device__ __forceinline__ uint32_t ring(uint32_t off, uint32_t n) { return off + n * kSlot >= kLds ? off + n * kSlot - kLds : off + n * kSlot; }
+// before the reads of phase P: the even phase reads the second half of its own k-step, the odd
+// phase the first half of the next one, whose stages are two further along the ring
+template <int P> __device__ __forceinline__ void read_bases(Ctx &c)
+{
+    if (P == 1) {
+        c.xs = ring(c.xs, 2);
+        c.ws = ring(c.ws, 2);
+    }
+    constexpr int p = 1 - P;
+    c.xr[0] = c.xb[p][0] + c.xs;
+    c.xr[1] = c.xb[p][1] + c.xs;
+    c.wr[0] = c.wb[p][0] + c.ws;
+    c.wr[1] = c.wb[p][1] + c.ws;
+}
+__device__ __forceinline__ void rotate(Ctx &c) { c.ls = ring(c.ls, 1); }
 template <int I> __device__ __forceinline__ void adv(Ctx &c)
 {
     if (I < 8) ASMV("v_add_u32 %0, 0x80, %0" : "+v"(c.xoff[I]));
     else ASMV("v_add_u32 %0, 0x80, %0" : "+v"(c.woff[I - 8]));
 }
-__device__ __forceinline__ void advance_all(Ctx &c)
-{
-    adv<0>(c); adv<1>(c); adv<2>(c); adv<3>(c); adv<4>(c); adv<5>(c); adv<6>(c); adv<7>(c);
-    adv<8>(c); adv<9>(c); adv<10>(c); adv<11>(c); adv<12>(c); adv<13>(c); adv<14>(c); adv<15>(c);
-}
 
-// DTL item i of a k-step into stage S: items 0..7 are X, 8..15 W (8 x 1 KB per wave each)
-template <int S> __device__ __forceinline__ void issue_dtl(Ctx &c, int i)
+// DTL item i (8 rows x 128 B, rows (8 wave + i) * 8 ..) of the X (OP 0) or W (OP 1) stage at
+// the current source offsets, into the stage at `stage`.
+template <int OP> __device__ __forceinline__ void issue_dtl(Ctx &c, uint32_t stage, int i)
 {
-    if (i < 8) {
-        const uint32_t m0v = __builtin_amdgcn_readfirstlane(kX0 + S * 32768u + (c.wave * 8u + i) * 1024u);
-        dtl_load(m0v, c.xoff[i], c.ex);
-    } else {
-        const uint32_t m0v = __builtin_amdgcn_readfirstlane(kW0 + S * 32768u + (c.wave * 8u + (i - 8)) * 1024u);
-        dtl_load(m0v, c.woff[i - 8], c.ew);
-    }
+    const uint32_t m0v = __builtin_amdgcn_readfirstlane(stage + (c.wave * 8u + uint32_t(i)) * 1024u);
+    if (OP == 0) dtl_load(m0v, c.xoff[i], c.ex);
+    else dtl_load(m0v, c.woff[i], c.ew);
 }
+template <int OP> __device__ __forceinline__ void issue_dtl(Ctx &c, int i) { issue_dtl<OP>(c, c.ls, i); }
 
-template <int NS, int NP, int NXT, int J, int Q> __device__ __forceinline__ void rd_x(Ctx &c)
+template <int NXT, int J, int Q> __device__ __forceinline__ void rd_x(Ctx &c)
 {
-    ldsb128<NS * 32768 + J * 4096>(c.B[NXT][Q * 8 + J], c.xb[NP][Q]);
+    ldsb128<J * 4096>(c.B[NXT][Q * 4 + J], c.xr[Q]);
 }
-template <int NS, int NP, int NXT, int I, int Q> __device__ __forceinline__ void rd_w(Ctx &c)
+template <int NXT, int I, int Q> __device__ __forceinline__ void rd_w(Ctx &c)
 {
-    ldsb128<NS * 32768 + I * 4096>(c.A[NXT][Q * 2 + I], c.wb[NP][Q]);
+    ldsb128<I * 4096>(c.A[NXT][Q * 4 + I], c.wr[Q]);
 }
 template <int CUR, int MI> __device__ __forceinline__ void mm(Ctx &c)
 {
-    constexpr int q = MI / 16, i = (MI / 8) % 2, j = MI % 8;
-    mfma(c.acc[i][j], c.A[CUR][q * 2 + i], c.B[CUR][q * 8 + j]);
+    constexpr int q = MI / 16, i = (MI / 4) % 4, j = MI % 4;
+    mfma(c.acc[i][j], c.A[CUR][q * 4 + i], c.B[CUR][q * 4 + j]);
 }
 // after the wait covering the k-half Q fragments of set SET
 template <int SET, int Q> __device__ __forceinline__ void tie_q(Ctx &c)
 {
 #pragma unroll
-    for (int j = 0; j < 8; ++j) tie(c.B[SET][Q * 8 + j]);
-    tie(c.A[SET][Q * 2]);
-    tie(c.A[SET][Q * 2 + 1]);
+    for (int j = 0; j < 4; ++j) {
+        tie(c.B[SET][Q * 4 + j]);
+        tie(c.A[SET][Q * 4 + j]);
+    }
 }
 
 #include "hif8_gemm_schedule_w16.inc"
@@ -192,86 +211,82 @@ __global__ __launch_bounds__(kThreads, 1) void k_linear_w16(const uint16_t *__re
         c.xoff[i] = row * uint32_t(K) * 2u + ch * 16u;
         c.woff[i] = c.xoff[i];
     }
-    // Fragment read bases.  Row m, 16-B chunk k/8 sits at m*128 + ((chunk ^ f(m)) << 4),
-    // f(m) = (m & 7) ^ ((m >> 3) & 1): the 32 rows of a fragment read hit distinct banks.
-    // MFMA k-slot (half h, e) of k-half q in phase p is k = 32p + 16h + 8q + e for both
-    // operands (the order k_linear_dtl uses).
+    // Fragment read bases.  MFMA k-slot (half h, e) of k-half q in phase p is k = 32p + 16h +
+    // 8q + e for both operands (the order k_linear_dtl uses): chunk 4p + 2h + q of rows
+    // wm + 32j + r (X) and wn + 32i + r (W); f(row) = f(r).
     const uint32_t fr = (r & 7u) ^ ((r >> 3) & 1u);
+    const uint32_t wm = (c.wave & 1u) * 128u, wn = (c.wave >> 1) * 128u;
 #pragma unroll
     for (int p = 0; p < 2; ++p)
 #pragma unroll
         for (int q = 0; q < 2; ++q) {
             const uint32_t ch = ((4u * p + 2u * h + q) ^ fr) << 4;
-            c.xb[p][q] = kX0 + r * 128u + ch;
-            c.wb[p][q] = kW0 + (c.wave * 64u + r) * 128u + ch;
+            c.xb[p][q] = (wm + r) * 128u + ch;
+            c.wb[p][q] = (wn + r) * 128u + ch;
         }
 
     const int nk = K / kBK;
-    const int odd = nk & 1;  // an odd k-step count gets a zero k-step in front
-    c.nk_eff = nk + odd;
+    // Prologue: X and W of k-steps 0 and 1 into stages 0..3; wait for k-step 0.
     c.ex = c.rx;
     c.ew = c.rw;
-    if (odd) {
 #pragma unroll
-        for (int it = 0; it < 8; ++it) {
-            *(u32x4 *)(smem + kX0 + (uint32_t(it) * 256u + tid) * 16u) = u32x4{0, 0, 0, 0};
-            *(u32x4 *)(smem + kW0 + (uint32_t(it) * 256u + tid) * 16u) = u32x4{0, 0, 0, 0};
-        }
-    }
-    wait_lgkm<0>();
-    if (!odd) {
+    for (int i = 0; i < 8; ++i) issue_dtl<0>(c, 0u, i);
 #pragma unroll
-        for (int i = 0; i < 16; ++i) issue_dtl<0>(c, i);
-        advance_all(c);
-    }
-    c.ex[2] = c.nk_eff > 1 ? c.rx[2] : 0u;
-    c.ew[2] = c.nk_eff > 1 ? c.rw[2] : 0u;
-    // DTL(1) items 12..15 are issued by the first phase 0, which then advances the offsets
+    for (int i = 0; i < 8; ++i) issue_dtl<1>(c, kSlot, i);
+    c.ex[2] = nk > 1 ? c.rx[2] : 0u;
+    c.ew[2] = nk > 1 ? c.rw[2] : 0u;
+    adv<0>(c); adv<1>(c); adv<2>(c); adv<3>(c); adv<4>(c); adv<5>(c); adv<6>(c); adv<7>(c);
+    adv<8>(c); adv<9>(c); adv<10>(c); adv<11>(c); adv<12>(c); adv<13>(c); adv<14>(c); adv<15>(c);
 #pragma unroll
-    for (int i = 0; i < 12; ++i) issue_dtl<1>(c, i);
-    wait_vm<12>();
+    for (int i = 0; i < 8; ++i) issue_dtl<0>(c, 2u * kSlot, i);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) issue_dtl<1>(c, 3u * kSlot, i);
+    adv<0>(c); adv<1>(c); adv<2>(c); adv<3>(c); adv<4>(c); adv<5>(c); adv<6>(c); adv<7>(c);
+    adv<8>(c); adv<9>(c); adv<10>(c); adv<11>(c); adv<12>(c); adv<13>(c); adv<14>(c); adv<15>(c);
+    wait_vm<16>();
     barrier();
-    // reads for phase (0, 0) from stage 0 into set 0
-    rd_x<0, 0, 0, 0, 0>(c); rd_x<0, 0, 0, 1, 0>(c); rd_x<0, 0, 0, 2, 0>(c); rd_x<0, 0, 0, 3, 0>(c);
-    rd_x<0, 0, 0, 4, 0>(c); rd_x<0, 0, 0, 5, 0>(c); rd_x<0, 0, 0, 6, 0>(c); rd_x<0, 0, 0, 7, 0>(c);
-    rd_w<0, 0, 0, 0, 0>(c); rd_w<0, 0, 0, 1, 0>(c);
-    rd_x<0, 0, 0, 0, 1>(c); rd_x<0, 0, 0, 1, 1>(c); rd_x<0, 0, 0, 2, 1>(c); rd_x<0, 0, 0, 3, 1>(c);
-    rd_x<0, 0, 0, 4, 1>(c); rd_x<0, 0, 0, 5, 1>(c); rd_x<0, 0, 0, 6, 1>(c); rd_x<0, 0, 0, 7, 1>(c);
-    rd_w<0, 0, 0, 0, 1>(c); rd_w<0, 0, 0, 1, 1>(c);
+    // reads for the first phase (k-step 0, first half) into set 0: the q0 set, then the q1 set
+    c.xs = 0;
+    c.ws = kSlot;
+    c.xr[0] = c.xb[0][0]; c.xr[1] = c.xb[0][1];
+    c.wr[0] = c.wb[0][0] + kSlot; c.wr[1] = c.wb[0][1] + kSlot;
+    rd_w<0, 0, 0>(c); rd_x<0, 0, 0>(c); rd_w<0, 1, 0>(c); rd_x<0, 1, 0>(c);
+    rd_w<0, 2, 0>(c); rd_x<0, 2, 0>(c); rd_w<0, 3, 0>(c); rd_x<0, 3, 0>(c);
+    rd_w<0, 0, 1>(c); rd_x<0, 0, 1>(c); rd_w<0, 1, 1>(c); rd_x<0, 1, 1>(c);
+    rd_w<0, 2, 1>(c); rd_x<0, 2, 1>(c); rd_w<0, 3, 1>(c); rd_x<0, 3, 1>(c);
+    c.ls = 4u * kSlot;  // the first phase loads X of k-step 2
+    read_bases<0>(c);
 
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < 8; ++j) c.acc[i][j] = f32x16{};
-    // Two k-steps per iteration (stage 0 then stage 1).  The loads of k-step kt+2 use the
-    // resources with size 0 past the end: they read nothing and nothing consumes them.
-    for (int kt = 0; kt < c.nk_eff; kt += 2) {
-        phase0<0>(c);
-        c.ex[2] = kt + 2 < c.nk_eff ? c.rx[2] : 0u;
-        c.ew[2] = kt + 2 < c.nk_eff ? c.rw[2] : 0u;
-        phase1<0>(c);
-        phase0<1>(c);
-        c.ex[2] = kt + 3 < c.nk_eff ? c.rx[2] : 0u;
-        c.ew[2] = kt + 3 < c.nk_eff ? c.rw[2] : 0u;
-        phase1<1>(c);
+        for (int j = 0; j < 4; ++j) c.acc[i][j] = f32x16{};
+    // One k-step per iteration.  The loads of k-step kk + 2 use the resources with size 0 past
+    // the end: they read nothing and nothing consumes them.
+    for (int kk = 0; kk < nk; ++kk) {
+        c.ex[2] = kk + 2 < nk ? c.rx[2] : 0u;
+        c.ew[2] = kk + 2 < nk ? c.rw[2] : 0u;
+        phase0(c);
+        phase1(c);
     }
     // no load may still target LDS when it is reused or released
     wait_vm<0>();
     wait_lgkm<0>();
     ASMV("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7"
-         : "+a"(c.acc[0][0]), "+a"(c.acc[0][1]), "+a"(c.acc[0][2]), "+a"(c.acc[0][3]), "+a"(c.acc[0][4]),
-           "+a"(c.acc[0][5]), "+a"(c.acc[0][6]), "+a"(c.acc[0][7]), "+a"(c.acc[1][0]), "+a"(c.acc[1][1]),
-           "+a"(c.acc[1][2]), "+a"(c.acc[1][3]), "+a"(c.acc[1][4]), "+a"(c.acc[1][5]), "+a"(c.acc[1][6]),
-           "+a"(c.acc[1][7]));
+         : "+a"(c.acc[0][0]), "+a"(c.acc[0][1]), "+a"(c.acc[0][2]), "+a"(c.acc[0][3]), "+a"(c.acc[1][0]),
+           "+a"(c.acc[1][1]), "+a"(c.acc[1][2]), "+a"(c.acc[1][3]), "+a"(c.acc[2][0]), "+a"(c.acc[2][1]),
+           "+a"(c.acc[2][2]), "+a"(c.acc[2][3]), "+a"(c.acc[3][0]), "+a"(c.acc[3][1]), "+a"(c.acc[3][2]),
+           "+a"(c.acc[3][3]));
 
-    // Epilogue.  acc[i][j] lane (r, h), element e: D[n][m] with n = 64w + 32i + 8(e/4) + 4h + e%4,
-    // m = 32j + r.  Rows go to LDS (padded), then each wave stores 2 rows x 512 B per instruction.
+    // Epilogue.  acc[i][j] lane (r, h), element e: D[n][m] with n = wn + 32i + 8(e/4) + 4h + e%4,
+    // m = wm + 32j + r.  Rows go to LDS (padded), then each wave stores 2 rows x 512 B per
+    // instruction.
     __syncthreads();
     uint32_t ymax = 0;  // EPI 1: largest magnitude bits of this lane's in-range outputs
     {
-        const uint32_t wl = c.wave * 64u;
+        const uint32_t wl = wn;
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
+        for (int i = 0; i < 4; ++i) {
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
                 const uint32_t nl = wl + uint32_t(i * 32 + 8 * g) + 4u * h;
@@ -285,7 +300,7 @@ __global__ __launch_bounds__(kThreads, 1) void k_linear_w16(const uint16_t *__re
                     b3 = __builtin_bit_cast(float, bb.y & 0xFFFF0000u);
                 }
 #pragma unroll
-                for (int j = 0; j < 8; ++j) {
+                for (int j = 0; j < 4; ++j) {
                     const f32x16 &a = c.acc[i][j];
                     uint2 v;
                     if (EPI == 0) {
@@ -296,7 +311,7 @@ __global__ __launch_bounds__(kThreads, 1) void k_linear_w16(const uint16_t *__re
                         const uint32_t p23 = f2bf_pk(a[4 * g + 2] + b2, a[4 * g + 3] + b3);
                         v.x = f2bf_pk(gelu_tanh(bf2f(p01 & 0xFFFFu)), gelu_tanh(bf2f(p01 >> 16)));
                         v.y = f2bf_pk(gelu_tanh(bf2f(p23 & 0xFFFFu)), gelu_tanh(bf2f(p23 >> 16)));
-                        const int m = m0 + j * 32 + int(r);
+                        const int m = m0 + int(wm) + j * 32 + int(r);
                         if (n < N && m < M) {
                             typedef uint16_t u16x2 __attribute__((ext_vector_type(2)));
                             const u16x2 mg = __builtin_elementwise_max(__builtin_bit_cast(u16x2, v.x & 0x7FFF7FFFu),
@@ -304,7 +319,7 @@ __global__ __launch_bounds__(kThreads, 1) void k_linear_w16(const uint16_t *__re
                             ymax = max(ymax, uint32_t(max(mg.x, mg.y)));
                         }
                     }
-                    *(uint2 *)(smem + (uint32_t(j * 32) + r) * kOutRow + nl * 2u) = v;
+                    *(uint2 *)(smem + (wm + uint32_t(j * 32) + r) * kOutRow + nl * 2u) = v;
                 }
             }
         }

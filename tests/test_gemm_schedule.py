@@ -105,23 +105,23 @@ def w16_asm(tmp_path_factory):
 
 
 def test_w16_resources(w16_asm):
-    """The decode-free twin: both instantiations, no spills, the 132 KB LDS array."""
+    """The decode-free twin: both instantiations, no spills, the 160 KB LDS ring."""
     _, remarks = w16_asm
     spills = re.findall(r"(?:VGPRs|SGPRs) Spill: (\d+)", remarks)
     lds = re.findall(r"LDS Size \[bytes/block\]: (\d+)", remarks)
     scratch = re.findall(r"ScratchSize \[bytes/lane\]: (\d+)", remarks)
-    assert len(lds) == 2 and set(lds) == {"135168"}, lds
+    assert len(lds) == 2 and set(lds) == {"163840"}, lds
     assert spills and set(spills) == {"0"}, spills
     assert scratch and set(scratch) == {"0"}, scratch
 
 
 def test_w16_main_loop_hazards(w16_asm):
-    """Per 2 k-steps: 128 MFMAs, 80 fragment reads (20 per phase), 32 global->LDS loads."""
+    """Per k-step: 64 MFMAs, 32 fragment reads (16 per phase), 16 global->LDS loads."""
     import isa_check
     loops = isa_check.mfma_loops(w16_asm[0])
     assert len(loops) == 2
     for body in loops:
         kinds = isa_check.census(body)
-        assert kinds.get("mfma") == 128 and kinds.get("lds_load") == 80 and kinds.get("lds_dma") == 32, kinds
+        assert kinds.get("mfma") == 64 and kinds.get("lds_load") == 32 and kinds.get("lds_dma") == 16, kinds
         errors = isa_check.check_body(body)
         assert not errors, "\n".join(errors[:20])
