@@ -5,15 +5,18 @@
 // at M = 75600 that is 296 decodes per element, about a tenth of its cycles and of its energy
 // at the board's power limit.  Decoding W once into a workspace and streaming bf16 W costs one
 // pass over the codes and twice the weight bytes through L2; for a few thousand rows and more
-// it is the faster route.  The products are the same bf16 x fp32-accumulate MFMAs on the same
-// operand values, in the same k order, so the two kernels agree bit for bit.
+// it is the faster route.  The products are bf16 x bf16 with fp32 accumulation on the same
+// operand values as the fused kernel, in 16x16x32 instead of 32x32x16 MFMAs, so an output can
+// differ from the fused kernel's by one bf16 rounding step.
 //
-// Design (shared with k_linear_dtl except for W, the wave quadrants and the LDS ring):
+// Design (shared with k_linear_dtl except for W, the MFMA shape, the wave quadrants and the
+// LDS ring):
 //   - One workgroup per 256 x 256 output tile, 4 waves; wave w owns the 128 x 128 quadrant of
-//     rows 128 (w & 1) .. +127 and output features 128 (w >> 1) .. +127: 4 x 4 tiles of
-//     v_mfma_f32_32x32x16_bf16.  (k_linear_dtl gives each wave 64 features for all 256 rows
-//     because a wave decodes the W rows it uses; with W already bf16 the quadrants read a fifth
-//     less from LDS per k-step.)
+//     rows 128 (w & 1) .. +127 and output features 128 (w >> 1) .. +127: 8 x 8 tiles of
+//     v_mfma_f32_16x16x32_bf16.  At the board's power limit the 16x16x32 form sustains about
+//     13 % more bf16 throughput than 32x32x16 on the same operand data (it moves fewer
+//     accumulator bytes per flop).  (k_linear_dtl gives each wave 64 features for all 256
+//     rows because a wave decodes the W rows it uses.)
 //   - X and W (bf16) go global -> LDS with buffer_load ... lds.  LDS is a ring of five 32 KB
 //     operand stages (one operand, 256 rows x 64 k each; 160 KB): k-step j's X and W take
 //     stages 2j and 2j + 1.  Each k-step has one barrier (in its second phase); the X loads of
@@ -33,7 +36,7 @@
 namespace hif8 {
 namespace w16 {
 
-typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kTile = 256;
@@ -56,9 +59,9 @@ template <int OFF> __device__ __forceinline__ void ldsb128(u32x4 &d, uint32_t a)
 {
     ASMV("ds_read_b128 %0, %1 offset:%2" : "=v"(d) : "v"(a), "i"(OFF));
 }
-__device__ __forceinline__ void mfma(f32x16 &c, const u32x4 &a, const u32x4 &b)
+__device__ __forceinline__ void mfma(f32x4 &c, const u32x4 &a, const u32x4 &b)
 {
-    ASMV("v_mfma_f32_32x32x16_bf16 %0, %1, %2, %0" : "+a"(c) : "v"(a), "v"(b));
+    ASMV("v_mfma_f32_16x16x32_bf16 %0, %1, %2, %0" : "+a"(c) : "v"(a), "v"(b));
 }
 template <int N> __device__ __forceinline__ void wait_lgkm() { ASMV("s_waitcnt lgkmcnt(%0)" ::"i"(N)); }
 template <int N> __device__ __forceinline__ void wait_vm() { ASMV("s_waitcnt vmcnt(%0)" ::"i"(N)); }
@@ -91,11 +94,11 @@ __device__ __forceinline__ uint32_t f2bf_pk(float lo, float hi)
 // Per-wave loop state.  Fragment sets alternate between phases: set 0 is consumed in the even
 // phase (first 32 k of a k-step) and filled in the odd one, set 1 the other way round.
 struct Ctx {
-    u32x4 B[2][8];    // [set][q*4 + j]  X fragments (m-tile j, k-half q)
-    u32x4 A[2][8];    // [set][q*4 + i]  W fragments (n-tile i, k-half q)
-    uint32_t xb[2][2], wb[2][2];  // fragment read bases in stage 0 [phase p][q]
-    uint32_t xr[2], wr[2];        // the same in the stages read this phase [q]
-    f32x16 acc[4][4];
+    u32x4 B[2][8];    // [set][j]  X fragments (m-tile j)
+    u32x4 A[2][8];    // [set][i]  W fragments (n-tile i)
+    uint32_t xb[2], wb[2];  // fragment read bases in stage 0 [phase p]
+    uint32_t xr, wr;        // the same in the stages read this phase
+    f32x4 acc[8][8];
     u32x4 rx, rw, ex, ew;  // buffer resources: X, W, and the effective ones (size 0 past the end)
     uint32_t xoff[8], woff[8];  // DTL source offsets of the next X and W stage to load
     uint32_t xs, ws, ls;  // LDS offsets of the X and W stages read and of the stage loaded this phase
@@ -112,10 +115,8 @@ template <int P> __device__ __forceinline__ void read_bases(Ctx &c)
         c.ws = ring(c.ws, 2);
     }
     constexpr int p = 1 - P;
-    c.xr[0] = c.xb[p][0] + c.xs;
-    c.xr[1] = c.xb[p][1] + c.xs;
-    c.wr[0] = c.wb[p][0] + c.ws;
-    c.wr[1] = c.wb[p][1] + c.ws;
+    c.xr = c.xb[p] + c.xs;
+    c.wr = c.wb[p] + c.ws;
 }
 __device__ __forceinline__ void rotate(Ctx &c) { c.ls = ring(c.ls, 1); }
 template <int I> __device__ __forceinline__ void adv(Ctx &c)
@@ -134,26 +135,21 @@ template <int OP> __device__ __forceinline__ void issue_dtl(Ctx &c, uint32_t sta
 }
 template <int OP> __device__ __forceinline__ void issue_dtl(Ctx &c, int i) { issue_dtl<OP>(c, c.ls, i); }
 
-template <int NXT, int J, int Q> __device__ __forceinline__ void rd_x(Ctx &c)
-{
-    ldsb128<J * 4096>(c.B[NXT][Q * 4 + J], c.xr[Q]);
-}
-template <int NXT, int I, int Q> __device__ __forceinline__ void rd_w(Ctx &c)
-{
-    ldsb128<I * 4096>(c.A[NXT][Q * 4 + I], c.wr[Q]);
-}
+// fragment reads: 16 rows x 128 B per m- or n-tile
+template <int NXT, int J> __device__ __forceinline__ void rd_x(Ctx &c) { ldsb128<J * 2048>(c.B[NXT][J], c.xr); }
+template <int NXT, int I> __device__ __forceinline__ void rd_w(Ctx &c) { ldsb128<I * 2048>(c.A[NXT][I], c.wr); }
 template <int CUR, int MI> __device__ __forceinline__ void mm(Ctx &c)
 {
-    constexpr int q = MI / 16, i = (MI / 4) % 4, j = MI % 4;
-    mfma(c.acc[i][j], c.A[CUR][q * 4 + i], c.B[CUR][q * 4 + j]);
+    constexpr int i = MI / 8, j = MI % 8;
+    mfma(c.acc[i][j], c.A[CUR][i], c.B[CUR][j]);
 }
-// after the wait covering the k-half Q fragments of set SET
-template <int SET, int Q> __device__ __forceinline__ void tie_q(Ctx &c)
+// after the wait covering the fragments of set SET
+template <int SET> __device__ __forceinline__ void tie_set(Ctx &c)
 {
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-        tie(c.B[SET][Q * 4 + j]);
-        tie(c.A[SET][Q * 4 + j]);
+    for (int j = 0; j < 8; ++j) {
+        tie(c.B[SET][j]);
+        tie(c.A[SET][j]);
     }
 }
 
@@ -172,7 +168,7 @@ __global__ __launch_bounds__(kThreads, 1) void k_linear_w16(const uint16_t *__re
     Ctx c;
     const uint32_t tid = threadIdx.x, lane = tid & 63u;
     c.wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const uint32_t r = lane & 31u, h = lane >> 5;
+    const uint32_t r = lane & 15u, g = lane >> 4;
 
     // tile order: groups of kGroupM m-tiles, n-tiles outer within a group (as k_linear_dtl)
     const int t = blockIdx.x;
@@ -211,19 +207,17 @@ __global__ __launch_bounds__(kThreads, 1) void k_linear_w16(const uint16_t *__re
         c.xoff[i] = row * uint32_t(K) * 2u + ch * 16u;
         c.woff[i] = c.xoff[i];
     }
-    // Fragment read bases.  MFMA k-slot (half h, e) of k-half q in phase p is k = 32p + 16h +
-    // 8q + e for both operands (the order k_linear_dtl uses): chunk 4p + 2h + q of rows
-    // wm + 32j + r (X) and wn + 32i + r (W); f(row) = f(r).
+    // Fragment read bases.  Lane (r, g) = (lane & 15, lane >> 4) holds k = 32p + 8g .. +7 of
+    // phase p for row r of its 16-row tile, for both operands: chunk 4p + g of rows wm + 16j + r
+    // (X) and wn + 16i + r (W); f(row) = f(r).
     const uint32_t fr = (r & 7u) ^ ((r >> 3) & 1u);
     const uint32_t wm = (c.wave & 1u) * 128u, wn = (c.wave >> 1) * 128u;
 #pragma unroll
-    for (int p = 0; p < 2; ++p)
-#pragma unroll
-        for (int q = 0; q < 2; ++q) {
-            const uint32_t ch = ((4u * p + 2u * h + q) ^ fr) << 4;
-            c.xb[p][q] = (wm + r) * 128u + ch;
-            c.wb[p][q] = (wn + r) * 128u + ch;
-        }
+    for (int p = 0; p < 2; ++p) {
+        const uint32_t ch = ((4u * p + g) ^ fr) << 4;
+        c.xb[p] = (wm + r) * 128u + ch;
+        c.wb[p] = (wn + r) * 128u + ch;
+    }
 
     const int nk = K / kBK;
     // Prologue: X and W of k-steps 0 and 1 into stages 0..3; wait for k-step 0.
@@ -245,22 +239,21 @@ __global__ __launch_bounds__(kThreads, 1) void k_linear_w16(const uint16_t *__re
     adv<8>(c); adv<9>(c); adv<10>(c); adv<11>(c); adv<12>(c); adv<13>(c); adv<14>(c); adv<15>(c);
     wait_vm<16>();
     barrier();
-    // reads for the first phase (k-step 0, first half) into set 0: the q0 set, then the q1 set
+    // reads for the first phase (k-step 0, first half) into set 0
     c.xs = 0;
     c.ws = kSlot;
-    c.xr[0] = c.xb[0][0]; c.xr[1] = c.xb[0][1];
-    c.wr[0] = c.wb[0][0] + kSlot; c.wr[1] = c.wb[0][1] + kSlot;
-    rd_w<0, 0, 0>(c); rd_x<0, 0, 0>(c); rd_w<0, 1, 0>(c); rd_x<0, 1, 0>(c);
-    rd_w<0, 2, 0>(c); rd_x<0, 2, 0>(c); rd_w<0, 3, 0>(c); rd_x<0, 3, 0>(c);
-    rd_w<0, 0, 1>(c); rd_x<0, 0, 1>(c); rd_w<0, 1, 1>(c); rd_x<0, 1, 1>(c);
-    rd_w<0, 2, 1>(c); rd_x<0, 2, 1>(c); rd_w<0, 3, 1>(c); rd_x<0, 3, 1>(c);
+    c.xr = c.xb[0];
+    c.wr = c.wb[0] + kSlot;
+    rd_w<0, 0>(c); rd_x<0, 0>(c); rd_x<0, 1>(c); rd_x<0, 2>(c); rd_x<0, 3>(c);
+    rd_x<0, 4>(c); rd_x<0, 5>(c); rd_x<0, 6>(c); rd_x<0, 7>(c);
+    rd_w<0, 1>(c); rd_w<0, 2>(c); rd_w<0, 3>(c); rd_w<0, 4>(c); rd_w<0, 5>(c); rd_w<0, 6>(c); rd_w<0, 7>(c);
     c.ls = 4u * kSlot;  // the first phase loads X of k-step 2
     read_bases<0>(c);
 
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
+    for (int i = 0; i < 8; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) c.acc[i][j] = f32x16{};
+        for (int j = 0; j < 8; ++j) c.acc[i][j] = f32x4{};
     // One k-step per iteration.  The loads of k-step kk + 2 use the resources with size 0 past
     // the end: they read nothing and nothing consumes them.
     for (int kk = 0; kk < nk; ++kk) {
@@ -272,24 +265,23 @@ __global__ __launch_bounds__(kThreads, 1) void k_linear_w16(const uint16_t *__re
     // no load may still target LDS when it is reused or released
     wait_vm<0>();
     wait_lgkm<0>();
-    ASMV("s_nop 7\n\ts_nop 7\n\ts_nop 7\n\ts_nop 7"
-         : "+a"(c.acc[0][0]), "+a"(c.acc[0][1]), "+a"(c.acc[0][2]), "+a"(c.acc[0][3]), "+a"(c.acc[1][0]),
-           "+a"(c.acc[1][1]), "+a"(c.acc[1][2]), "+a"(c.acc[1][3]), "+a"(c.acc[2][0]), "+a"(c.acc[2][1]),
-           "+a"(c.acc[2][2]), "+a"(c.acc[2][3]), "+a"(c.acc[3][0]), "+a"(c.acc[3][1]), "+a"(c.acc[3][2]),
-           "+a"(c.acc[3][3]));
+    // the last MFMAs' results must be complete before the accumulators are read
+    ASMV("s_nop 7\n\ts_nop 7\n\ts_nop 7" ::: "memory");
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) ASMV("" : "+a"(c.acc[i][j]));
 
-    // Epilogue.  acc[i][j] lane (r, h), element e: D[n][m] with n = wn + 32i + 8(e/4) + 4h + e%4,
-    // m = wm + 32j + r.  Rows go to LDS (padded), then each wave stores 2 rows x 512 B per
+    // Epilogue.  acc[i][j] lane (r, g), element e: D[n][m] with n = wn + 16i + 4g + e,
+    // m = wm + 16j + r.  Rows go to LDS (padded), then each wave stores 2 rows x 512 B per
     // instruction.
     __syncthreads();
     uint32_t ymax = 0;  // EPI 1: largest magnitude bits of this lane's in-range outputs
     {
-        const uint32_t wl = wn;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-#pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                const uint32_t nl = wl + uint32_t(i * 32 + 8 * g) + 4u * h;
+        for (int i = 0; i < 8; ++i) {
+            {
+                const uint32_t nl = wn + uint32_t(i * 16) + 4u * g;
                 const int n = n0 + int(nl);
                 float b0 = 0.f, b1 = 0.f, b2 = 0.f, b3 = 0.f;
                 if (bias && n < N) {
@@ -300,18 +292,18 @@ __global__ __launch_bounds__(kThreads, 1) void k_linear_w16(const uint16_t *__re
                     b3 = __builtin_bit_cast(float, bb.y & 0xFFFF0000u);
                 }
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const f32x16 &a = c.acc[i][j];
+                for (int j = 0; j < 8; ++j) {
+                    const f32x4 &a = c.acc[i][j];
                     uint2 v;
                     if (EPI == 0) {
-                        v.x = f2bf_pk(a[4 * g] + b0, a[4 * g + 1] + b1);
-                        v.y = f2bf_pk(a[4 * g + 2] + b2, a[4 * g + 3] + b3);
+                        v.x = f2bf_pk(a[0] + b0, a[1] + b1);
+                        v.y = f2bf_pk(a[2] + b2, a[3] + b3);
                     } else {
-                        const uint32_t p01 = f2bf_pk(a[4 * g] + b0, a[4 * g + 1] + b1);
-                        const uint32_t p23 = f2bf_pk(a[4 * g + 2] + b2, a[4 * g + 3] + b3);
+                        const uint32_t p01 = f2bf_pk(a[0] + b0, a[1] + b1);
+                        const uint32_t p23 = f2bf_pk(a[2] + b2, a[3] + b3);
                         v.x = f2bf_pk(gelu_tanh(bf2f(p01 & 0xFFFFu)), gelu_tanh(bf2f(p01 >> 16)));
                         v.y = f2bf_pk(gelu_tanh(bf2f(p23 & 0xFFFFu)), gelu_tanh(bf2f(p23 >> 16)));
-                        const int m = m0 + int(wm) + j * 32 + int(r);
+                        const int m = m0 + int(wm) + j * 16 + int(r);
                         if (n < N && m < M) {
                             typedef uint16_t u16x2 __attribute__((ext_vector_type(2)));
                             const u16x2 mg = __builtin_elementwise_max(__builtin_bit_cast(u16x2, v.x & 0x7FFF7FFFu),
@@ -319,14 +311,14 @@ __global__ __launch_bounds__(kThreads, 1) void k_linear_w16(const uint16_t *__re
                             ymax = max(ymax, uint32_t(max(mg.x, mg.y)));
                         }
                     }
-                    *(uint2 *)(smem + (wm + uint32_t(j * 32) + r) * kOutRow + nl * 2u) = v;
+                    *(uint2 *)(smem + (wm + uint32_t(j * 16) + r) * kOutRow + nl * 2u) = v;
                 }
             }
         }
     }
     __syncthreads();
     {
-        const uint32_t colb = (lane & 31u) * 16u;
+        const uint32_t colb = (lane & 31u) * 16u, h = lane >> 5;
         const int n = n0 + int(colb / 2u);
 #pragma unroll
         for (int blk = 0; blk < 4; ++blk) {

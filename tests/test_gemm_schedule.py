@@ -116,12 +116,12 @@ def test_w16_resources(w16_asm):
 
 
 def test_w16_main_loop_hazards(w16_asm):
-    """Per k-step: 64 MFMAs, 32 fragment reads (16 per phase), 16 global->LDS loads."""
+    """Per k-step: 128 MFMAs (16x16x32), 32 fragment reads (16 per phase), 16 global->LDS loads."""
     import isa_check
     loops = isa_check.mfma_loops(w16_asm[0])
     assert len(loops) == 2
     for body in loops:
         kinds = isa_check.census(body)
-        assert kinds.get("mfma") == 64 and kinds.get("lds_load") == 32 and kinds.get("lds_dma") == 16, kinds
+        assert kinds.get("mfma") == 128 and kinds.get("lds_load") == 32 and kinds.get("lds_dma") == 16, kinds
         errors = isa_check.check_body(body)
         assert not errors, "\n".join(errors[:20])

@@ -1,9 +1,15 @@
 """GPU parity of the decode-once route (hif8_gemm_w16.hip): the weight decoded once to bf16
 (hif8_decode) and the decode-free GEMM (hif8_linear_fwd_wq and its GELU + amax and grouped
-forms) against the fused GEMM, which decodes the packed codes inside.  Both issue the same MFMA
-products on the same operand values in the same k order, so the outputs are compared bit for
-bit (the fused GEMM itself is checked against the oracle in test_gpu_linear.py).  Shapes cover
-ragged M and N, an odd k-step count and a single k-step."""
+forms) against the fused GEMM, which decodes the packed codes inside.
+
+Both multiply the same bf16 operand values with fp32 accumulation.  The fused kernel uses
+32x32x16 MFMAs and the decode-free one 16x16x32, whose products are summed in a different order,
+so an output may differ by a bf16 rounding step.  The check is therefore against the fp64
+product of the same operands: every output of both kernels within one bf16 ulp (2^-7 |ref|)
+plus 2^-16 of sum |x_q||w_q| (fp32 accumulation), and the two kernels within twice that.  A
+wrong row, column or k index gives errors of the order of the output itself.  The fused GEMM is
+also checked against the oracle in test_gpu_linear.py.  Shapes cover ragged M and N, an odd
+k-step count and a single k-step."""
 from __future__ import annotations
 
 import ctypes
@@ -29,6 +35,20 @@ def operands(pkg, M, K, N, seed, bias=True):
     return a, fmt, st, pkg.PackedWeight(w, 15.0), b
 
 
+def bound(a, w_q, b, *ys):
+    """Asserts every y within one bf16 ulp + 2^-16 sum|x||w| of the fp64 product, and the ys
+    within twice that of each other."""
+    ref = a.double() @ w_q.double().t()
+    if b is not None:
+        ref = ref + b.double()
+    tol = ref.abs() * 2.0 ** -7 + (a.double().abs() @ w_q.double().abs().t()) * 2.0 ** -16
+    for y in ys:
+        err = (y.double() - ref).abs()
+        assert bool((err <= tol).all()), float((err / tol).max())
+    for y in ys[1:]:
+        assert bool(((y.double() - ys[0].double()).abs() <= 2 * tol).all())
+
+
 def fused(pkg, a, fmt, st, packed, b):
     old = pkg.hif8_linear.GEMM_ROUTE
     pkg.hif8_linear.GEMM_ROUTE = "fused"
@@ -40,17 +60,22 @@ def fused(pkg, a, fmt, st, packed, b):
 
 @pytest.mark.parametrize("M,K,N", SHAPES)
 @pytest.mark.parametrize("bias", [True, False])
-def test_wq_equals_fused(pkg, M, K, N, bias):
+def test_wq_matches_fused(pkg, M, K, N, bias):
     print(f"[w16] M={M} K={K} N={N} bias={bias}", flush=True)
     a, fmt, st, packed, b = operands(pkg, M, K, N, M + K + N, bias)
     want = fused(pkg, a, fmt, st, packed, b)
-    got = pkg.linear_fwd_wq(a, packed.dequantize(torch.bfloat16), b)
+    w_q = packed.dequantize(torch.bfloat16)
+    got = pkg.linear_fwd_wq(a, w_q, b)
     torch.cuda.synchronize()
-    assert torch.equal(got.view(torch.int16), want.view(torch.int16))
+    bound(a, w_q, b, want, got)
+
+
+def _amax_bits(y):
+    return int((y.view(torch.int16).int() & 0x7FFF).max())
 
 
 @pytest.mark.parametrize("M,K,N", [(300, 256, 264), (2048, 1536, 8960)])
-def test_wq_gelu_amax_equals_fused(pkg, M, K, N):
+def test_wq_gelu_amax_matches_fused(pkg, M, K, N):
     a, fmt, st, packed, b = operands(pkg, M, K, N, 7 * M + N)
     s_f, s_w = pkg.QuantState(DEV), pkg.QuantState(DEV)
     old = pkg.hif8_linear.GEMM_ROUTE
@@ -61,8 +86,13 @@ def test_wq_gelu_amax_equals_fused(pkg, M, K, N):
         got = pkg.linear_fwd_gelu_amax(a, packed, b, s_w, 15.0)
     finally:
         pkg.hif8_linear.GEMM_ROUTE = old
-    assert torch.equal(got.view(torch.int16), want.view(torch.int16))
-    assert s_f.read() == s_w.read()
+    # gelu is 1.13-Lipschitz and rounds once more: a bf16 step of the input moves the output by
+    # at most about two
+    diff = (got.double() - want.double()).abs()
+    assert bool((diff <= want.double().abs() * 2.0 ** -6 + 1e-3).all()), float(diff.max())
+    # each state holds the amax of its own output
+    assert s_f.read()[0] == _amax_bits(want)
+    assert s_w.read()[0] == _amax_bits(got)
 
 
 def test_wq_grouped_equals_single(pkg):
@@ -82,13 +112,16 @@ def test_wq_grouped_equals_single(pkg):
         ys = pkg.linear_fwd_grouped(a, gw)
         pkg.hif8_linear.GEMM_ROUTE = "fused"
         for y, p, b in zip(ys, packs, biases):
-            assert torch.equal(y.view(torch.int16), pkg.linear_fwd(a, fmt, st, p, b).view(torch.int16))
+            w_q = p.dequantize(torch.bfloat16)
+            # a group's output equals the single-weight launch of the same kernel bit for bit
+            assert torch.equal(y.view(torch.int16), pkg.linear_fwd_wq(a, w_q, b).view(torch.int16))
+            bound(a, w_q, b, pkg.linear_fwd(a, fmt, st, p, b), y)
     finally:
         pkg.hif8_linear.GEMM_ROUTE = old
 
 
 def test_module_routes_agree(pkg):
-    """HIF8Linear gives the same bits on either route (bf16 and fp32 input)."""
+    """HIF8Linear gives the same result on either route (bf16 and fp32 input), to one rounding."""
     lin = pkg.HIF8Linear(512, 768, device=DEV, dtype=torch.bfloat16)
     x = torch.randn(3000, 512, device=DEV).to(torch.bfloat16)
     outs = {}
@@ -101,7 +134,9 @@ def test_module_routes_agree(pkg):
     finally:
         pkg.hif8_linear.GEMM_ROUTE = old
     for u, v in zip(outs["fused"], outs["decode_once"]):
-        assert torch.equal(u.view(torch.int16), v.view(torch.int16))
+        diff = (u.double() - v.double()).abs()
+        assert bool((diff <= u.double().abs() * 2.0 ** -6 + 1e-4).all()), float(diff.max())
+        assert float((u != v).float().mean()) < 0.01
 
 
 def test_wq_rejects_bad_shapes(pkg):
