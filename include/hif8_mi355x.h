@@ -172,9 +172,8 @@ int hif8_linear_fwd_gelu_amax(const void *a, const uint8_t *w_codes, const void 
  * (hif8_linear.py:86) with w_q given already dequantised, bf16 [N, K] -- hif8_decode of the
  * packed codes with the weight's state, into a caller buffer, once per call.  The fused kernel
  * decodes each weight element once per 256-row tile of x (M/256 times); this route decodes it
- * once and streams bf16 W.  The same products with fp32 accumulation, summed by 16x16x32
- * MFMAs (hif8_linear_fwd: 32x32x16), so an output can differ from hif8_linear_fwd's by one bf16
- * rounding step.  Shapes, alignment and the GELU + amax and grouped variants
+ * once and streams bf16 W.  The same 16x16x32 MFMA products in the same k order: the outputs
+ * equal hif8_linear_fwd's bit for bit.  Shapes, alignment and the GELU + amax and grouped variants
  * as for hif8_linear_fwd / _gelu_amax / _grouped (w_q concatenated along N for groups).
  * No counterpart of its own in the reference: it is F.linear on the dequantised operands. */
 int hif8_linear_fwd_wq(const uint16_t *a, const uint16_t *w_q, const uint16_t *bias, uint16_t *y, int64_t M,

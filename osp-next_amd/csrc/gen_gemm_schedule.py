@@ -1,15 +1,12 @@
-"""Generate hif8_gemm_schedule.inc: the two phase bodies of the fused GEMM's main loop.
+"""Generate hif8_gemm_schedule.inc and hif8_gemm_schedule_w16.inc: the phase bodies of the
+main loops of the fused GEMM (hif8_gemm_dtl.hip) and of its decode-free twin
+(hif8_gemm_w16.hip).
 
-A k-step (64 k) is two phases of 32 k.  A phase issues the wave's 32 MFMAs
-(2 n-tiles x 8 m-tiles x 2 k-halves) and, in the gaps between them, everything
-the NEXT phase needs: W code reads, X fragment reads, the decode-table lookups
-and their address computations, the packing of looked-up values into MFMA
-operands, and (phase 1) the global->LDS loads of the k-step after next.
-
-Gap g holds the ops issued right after MFMA g; ("pre", n) holds ops issued
-right before MFMA n.  The wait counts below follow the issue order: LDS
-operations complete in order, so lgkmcnt(n) means "all but the n most recent
-LDS operations are done".
+A k-step (64 k) is two phases of 32 k.  A phase issues the wave's 64 MFMAs
+(v_mfma_f32_16x16x32_bf16, 16 cycles each) and, in the gaps between them, what the NEXT phase
+needs.  Gap g holds the ops issued right after MFMA g; ("pre", n) holds ops issued right before
+MFMA n.  Between two 16-cycle MFMAs a wave has three more issue slots.  LDS operations complete
+in order, so lgkmcnt(n) means "all but the n most recent LDS operations are done".
 
     python3 gen_gemm_schedule.py [out.inc [out_w16.inc]]
         (defaults: hif8_gemm_schedule.inc, hif8_gemm_schedule_w16.inc)
@@ -17,67 +14,116 @@ LDS operations are done".
 import os
 import sys
 
-# DTL (direct global->LDS loads) of the k-step after next: 12 per wave, 7 right after the
-# barrier of phase 1 (into the stage phase 1 just finished reading), 5 in the following
-# phase 0 (same k-step, same stage); the source offsets advance after the last one.
-DTL_PHASE1_GAPS = (1, 4, 7, 10, 13, 16, 19)
-DTL_PHASE0_GAPS = (0, 3, 6, 9, 12)
+# ---------------------------------------------------------------------------------------------
+# The fused GEMM (hif8_gemm_dtl.hip).  Wave w owns output features 64w .. +63 for all 256 rows:
+# MFMA m of a phase is n-tile i = m / 16 (16 features) times m-tile j = m % 16 (16 rows).  For
+# the next phase a phase reads its 16 X fragments (ds_read_b128) and the wave's W codes (one
+# ds_read_b64 of 8 codes per n-tile and lane), looks the 32 codes of each lane up in the
+# per-lane decode table (a v_perm address and a ds_read_u16 each) and packs n-tile 0's
+# looked-up values into its MFMA operand; n-tiles 1..3 are packed in the phase that uses them,
+# before MFMA 16, 32 and 48.  Phase 1 opens with the k-step's barrier and issues 7 of the 12
+# global->LDS loads of the k-step after next; the next phase 0 issues the other 5 and advances
+# the source offsets.
+#
+# The ops are placed greedily, in the order below, each at the first gap from its pacing
+# position on that has a free slot: fragment reads are never in adjacent gaps and loads sit
+# four gaps apart (the spacing the decode-free twin measured best), so the LDS and load traffic
+# is spread over the phase instead of bunched.  Waits are derived from the placement: before an
+# op that consumes an LDS load, lgkmcnt(number of LDS ops issued after that load), unless an
+# earlier wait already covered it (at most 15, the counter's width).
+
+NGAPS = 64
+CAP = 3  # non-MFMA issue slots per gap (a load with its m0 write takes two)
+DTL_GAPS = {1: (1, 5, 9, 13, 17, 21, 25), 0: (1, 5, 9, 13, 17)}
+
+
+class _Op:
+    def __init__(self, text, kind, cost=1, lds=False, deps=(), after=(), earliest=0, latest=NGAPS - 1, ties=()):
+        self.text, self.kind, self.cost, self.lds = text, kind, cost, lds
+        self.deps, self.after, self.earliest, self.latest, self.ties = list(deps), list(after), earliest, latest, ties
+        self.gap = None
 
 
 def schedule(phase):
-    ops = {}
-
-    def at(pos, *items):
-        ops.setdefault(pos, []).extend(items)
-
-    cur, nxt = (0, 1) if phase == 0 else (1, 0)
+    cur, nxt = phase, 1 - phase
     ns = "S" if phase == 0 else "1 - S"     # stage the next phase reads
     npar = 1 if phase == 0 else 0           # k-half (p) of the next phase
-    if phase == 1:
-        # Phase 0's stage reads (its last are the q1 X fragments, 10 LDS ops before the
-        # end of its issue order) are done, and DTL(k+1) has landed: then the barrier.
-        at(("pre", 0), "wait_lgkm<10>();", "wait_vm<0>();", "barrier();")
-    at(("pre", 0), f"rd_code<{ns}, {npar}, 0>(c);", f"rd_code<{ns}, {npar}, 1>(c);")
-    for j in range(8):
-        at(j, f"rd_x<{ns}, {npar}, {nxt}, {j}, 0>(c);")
-    if phase == 1:
-        for n, g in enumerate(DTL_PHASE1_GAPS):
-            at(g, f"issue_dtl<S>(c, {n});")
-    else:
-        for n, g in enumerate(DTL_PHASE0_GAPS):
-            at(g, f"issue_dtl<1 - S>(c, {7 + n});")
-    # The codes were followed by 7 X reads: lgkmcnt(7) covers them and everything the
-    # previous phase issued (q1 X fragments and q1 lookups of the current set).
-    at(("pre", 7), "wait_lgkm<7>();", "tie(c.cd[0]); tie(c.cd[1]);", f"tie_q1<{cur}>(c);")
+    slots = [[] for _ in range(NGAPS)]
+    used = [0] * NGAPS
+    b128 = [False] * NGAPS
+    placed = {}
 
-    # 32 lookups in gaps 8..23, two per gap; each address is computed one gap ahead into
-    # slot (g % 2) * 2 + k so that no read waits on the VALU op right before it.
-    def slot(g, k):
-        return (g % 2) * 2 + k
+    def put(op, g):
+        slots[g].append(op)
+        used[g] += op.cost
+        b128[g] = b128[g] or op.kind == "b128"
+        op.gap = g
+        placed[op.text] = op
 
-    at(7, f"lka<{slot(8, 0)}, 0>(c);", f"lka<{slot(8, 1)}, 1>(c);")
-    for g in range(8, 24):
-        t = g - 8
-        ll = 2 * t
-        q = ll // 16
-        if g < 23:
-            at(g, f"lka<{slot(g + 1, 0)}, {ll + 2}>(c);", f"lka<{slot(g + 1, 1)}, {ll + 3}>(c);")
-        at(g, f"lkr<{nxt}, {q}, {slot(g, 0)}, {ll % 16}>(c);", f"lkr<{nxt}, {q}, {slot(g, 1)}, {ll % 16 + 1}>(c);")
-        if g < 16:
-            # q1 operands of the current set, first used by MFMA 16 and 24
-            at(g, f"pk<{cur}, {2 if t < 4 else 3}, {t % 4}>(c);")
-    for g in range(16, 20):
-        t = g - 16
-        at(g, f"rd_x<{ns}, {npar}, {nxt}, {2 * t}, 1>(c);", f"rd_x<{ns}, {npar}, {nxt}, {2 * t + 1}, 1>(c);")
-        if phase == 0:
-            at(g, f"adv<{3 * t}>(c);", f"adv<{3 * t + 1}>(c);", f"adv<{3 * t + 2}>(c);")
-    # The q0 lookups (gaps 8..15) are followed by 24 LDS ops: lgkmcnt(15) covers them.
-    at(("pre", 24), "wait_lgkm<15>();", f"tie_t0<{nxt}>(c);")
-    for g in range(24, 32):
-        t = g - 24
-        # q0 operands of the next set: fragment 0 by gap 27 (first used by the next
-        # phase's MFMA 0), fragment 1 by gap 31 (first used by its MFMA 8)
-        at(g, f"pk<{nxt}, {0 if t < 4 else 1}, {t % 4}>(c);")
+    def place(op):
+        lo = op.earliest
+        for a, dist in op.after:
+            lo = max(lo, placed[a].gap + dist)
+        for g in range(lo, NGAPS):
+            if used[g] + op.cost > CAP:
+                continue
+            if op.kind == "b128" and any(b128[h] for h in (g - 1, g, g + 1) if 0 <= h < NGAPS):
+                continue
+            if g > op.latest:
+                raise RuntimeError(f"{op.text} misses gap {op.latest}")
+            put(op, g)
+            return
+        raise RuntimeError(f"no room for {op.text}")
+
+    for n, g in enumerate(DTL_GAPS[phase]):
+        if phase == 1:
+            put(_Op(f"issue_dtl<S>(c, {n});", "dtl", cost=2), g)
+        else:
+            put(_Op(f"issue_dtl<1 - S>(c, {len(DTL_GAPS[1]) + n});", "dtl", cost=2), g)
+    for i in (1, 2, 3):
+        for d in range(4):
+            place(_Op(f"pk<{cur}, {i}, {d}>(c);", "valu", earliest=(0, 0, 8, 24)[i] + 2 * d, latest=16 * i - 2))
+    codes = [f"rd_code<{ns}, {npar}, {i}>(c);" for i in range(4)]
+    for t in codes:
+        place(_Op(t, "b64", lds=True))
+    for j in range(16):
+        place(_Op(f"rd_x<{ns}, {npar}, {nxt}, {j}>(c);", "b128", lds=True, earliest=2 + 3 * j))
+    for ll in range(32):
+        r = ll % 4
+        after = [(codes[-1], 6)]
+        if ll >= 4:   # the address slot is free once the lookup 4 before has read it
+            after.append((f"lkr<{nxt}, {r}, {ll - 4}>(c);", 0))
+        place(_Op(f"lka<{r}, {ll}>(c);", "valu", deps=codes, after=after, earliest=10 + (5 * ll) // 4,
+                  ties=("tie_cd(c);",)))
+        place(_Op(f"lkr<{nxt}, {r}, {ll}>(c);", "u16", lds=True, after=[(f"lka<{r}, {ll}>(c);", 1)]))
+    tile0 = [f"lkr<{nxt}, {ll % 4}, {ll}>(c);" for ll in range(8)]
+    for d in range(4):
+        place(_Op(f"pk<{nxt}, 0, {d}>(c);", "valu", deps=tile0, after=[(t, 4) for t in tile0], earliest=52 + d,
+                  latest=NGAPS - 3, ties=(f"tie8(c.T[{nxt}][0]);",)))
+    if phase == 0:
+        for a in range(12):
+            place(_Op(f"adv<{a}>(c);", "valu", earliest=DTL_GAPS[0][-1] + 1 + 2 * a))
+
+    ops = {}
+    pre = ["wait_lgkm<0>();"] if phase == 0 else ["wait_lgkm<0>();", "wait_vm<0>();", "barrier();"]
+    ops[("pre", 0)] = pre + [f"tie_set<{cur}>(c);"]
+    issued, done, index = 0, 0, {}
+    for g in range(NGAPS):
+        lines = []
+        for op in slots[g]:
+            if op.deps:
+                need = max(index[d] for d in op.deps) + 1
+                if need > done:
+                    # lgkmcnt is a 4-bit field: waiting for at most 15 outstanding covers more
+                    n = min(issued - need, 15)
+                    lines.append(f"wait_lgkm<{n}>();")
+                    lines += list(op.ties)
+                    done = issued - n
+            lines.append(op.text)
+            if op.lds:
+                index[op.text] = issued
+                issued += 1
+        ops[g] = lines
     return ops
 
 
@@ -85,7 +131,7 @@ def emit(phase):
     ops = schedule(phase)
     cur = 0 if phase == 0 else 1
     lines = [f"template <int S> __device__ __forceinline__ void phase{phase}(Ctx &c)", "{"]
-    for m in range(32):
+    for m in range(NGAPS):
         lines += ["    " + op for op in ops.get(("pre", m), [])]
         lines.append(f"    mm<{cur}, {m}>(c);")
         lines += ["    " + op for op in ops.get(m, [])]

@@ -5,9 +5,8 @@
 // at M = 75600 that is 296 decodes per element, about a tenth of its cycles and of its energy
 // at the board's power limit.  Decoding W once into a workspace and streaming bf16 W costs one
 // pass over the codes and twice the weight bytes through L2; for a few thousand rows and more
-// it is the faster route.  The products are bf16 x bf16 with fp32 accumulation on the same
-// operand values as the fused kernel, in 16x16x32 instead of 32x32x16 MFMAs, so an output can
-// differ from the fused kernel's by one bf16 rounding step.
+// it is the faster route.  The products are the same v_mfma_f32_16x16x32_bf16 on the same
+// operand values, in the same k order, so the two kernels agree bit for bit.
 //
 // Design (shared with k_linear_dtl except for W, the MFMA shape, the wave quadrants and the
 // LDS ring):

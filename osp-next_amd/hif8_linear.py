@@ -240,8 +240,7 @@ def linear_dgrad(grad_q2: Tensor, w: "PackedWeight") -> Tensor:
 # GEMM route for bf16 activations: "fused" decodes the packed weight inside the GEMM (each
 # element once per 256-row tile of x), "decode_once" decodes it into a bf16 buffer per call and
 # runs the decode-free twin (hif8_linear_fwd_wq), "auto" takes decode_once from
-# DECODE_ONCE_MIN_ROWS rows up.  Both multiply the same operand values with fp32 accumulation;
-# their sums are taken in a different order, so an output can differ by one bf16 rounding step.
+# DECODE_ONCE_MIN_ROWS rows up.  Both issue the same MFMA products in the same order: the same bits.
 GEMM_ROUTE = "auto"
 DECODE_ONCE_MIN_ROWS = 8192   # measured: the routes tie near 8192 rows (14B FFN-up), decode_once wins above
 

@@ -3,7 +3,7 @@
 - hif8_gemm_schedule.inc is what gen_gemm_schedule.py generates;
 - compiled for gfx950, the kernel spills nothing, uses the full 160 KB LDS array, and its
   main loop passes the in-flight-register and VALU->MFMA checks of isa_check.py with the
-  expected instruction census (128 MFMA, 200 LDS loads, 24 global->LDS loads per 2 k-steps).
+  expected instruction census (256 MFMA, 208 LDS loads, 24 global->LDS loads per 2 k-steps).
 """
 import importlib.util
 import os
@@ -38,6 +38,10 @@ def dtl_asm(tmp_path_factory):
            "-Rpass-analysis=kernel-resource-usage"]
     r = subprocess.run(cmd, capture_output=True, text=True, timeout=600)
     assert r.returncode == 0, r.stderr[-2000:]
+    # the assembler checks operand ranges (e.g. lgkmcnt <= 15) that -S does not
+    obj = subprocess.run(cmd[:-5] + ["-c", os.path.join(CSRC, "hif8_gemm_dtl.hip"), "-o", str(out) + ".o"],
+                         capture_output=True, text=True, timeout=600)
+    assert obj.returncode == 0, obj.stderr[-2000:]
     return out.read_text(), r.stderr
 
 
@@ -58,7 +62,7 @@ def test_main_loop_hazards(dtl_asm):
     assert len(loops) == 2
     for body in loops:
         kinds = isa_check.census(body)
-        assert kinds.get("mfma") == 128 and kinds.get("lds_load") == 200 and kinds.get("lds_dma") == 24, kinds
+        assert kinds.get("mfma") == 256 and kinds.get("lds_load") == 208 and kinds.get("lds_dma") == 24, kinds
         errors = isa_check.check_body(body)
         assert not errors, "\n".join(errors[:20])
 
