@@ -33,8 +33,19 @@ import sys
 # earlier wait already covered it (at most 15, the counter's width).
 
 NGAPS = 64
-CAP = 3  # non-MFMA issue slots per gap (a load with its m0 write takes two)
+# Non-MFMA issue slots used per gap (a load with its m0 write takes two).  A gap has room for
+# three, but lab copies timed with s_memtime ran the loop at 2611 cycles per k-step with three
+# and 2474 with two (MFMAs alone: 2089).
+CAP = 2
 DTL_GAPS = {1: (1, 5, 9, 13, 17, 21, 25), 0: (1, 5, 9, 13, 17)}
+# pacing (first gap each op may take): X fragment j at X_START + X_STEP * j; lookup LL at
+# LK_START + LK_NUM * LL // LK_DEN, at least CODE_GAPS after the last code read; the packs of
+# the current set's n-tile i from PK_CUR[i] (two gaps apart), the next set's n-tile 0 from PK_NEXT
+X_START, X_STEP = 2, 3
+LK_START, LK_NUM, LK_DEN = 10, 5, 4
+CODE_GAPS = 6
+PK_CUR = (0, 0, 8, 24)
+PK_NEXT = 52
 
 
 class _Op:
@@ -82,23 +93,23 @@ def schedule(phase):
             put(_Op(f"issue_dtl<1 - S>(c, {len(DTL_GAPS[1]) + n});", "dtl", cost=2), g)
     for i in (1, 2, 3):
         for d in range(4):
-            place(_Op(f"pk<{cur}, {i}, {d}>(c);", "valu", earliest=(0, 0, 8, 24)[i] + 2 * d, latest=16 * i - 2))
+            place(_Op(f"pk<{cur}, {i}, {d}>(c);", "valu", earliest=PK_CUR[i] + 2 * d, latest=16 * i - 2))
     codes = [f"rd_code<{ns}, {npar}, {i}>(c);" for i in range(4)]
     for t in codes:
         place(_Op(t, "b64", lds=True))
     for j in range(16):
-        place(_Op(f"rd_x<{ns}, {npar}, {nxt}, {j}>(c);", "b128", lds=True, earliest=2 + 3 * j))
+        place(_Op(f"rd_x<{ns}, {npar}, {nxt}, {j}>(c);", "b128", lds=True, earliest=X_START + X_STEP * j))
     for ll in range(32):
         r = ll % 4
-        after = [(codes[-1], 6)]
+        after = [(codes[-1], CODE_GAPS)]
         if ll >= 4:   # the address slot is free once the lookup 4 before has read it
             after.append((f"lkr<{nxt}, {r}, {ll - 4}>(c);", 0))
-        place(_Op(f"lka<{r}, {ll}>(c);", "valu", deps=codes, after=after, earliest=10 + (5 * ll) // 4,
+        place(_Op(f"lka<{r}, {ll}>(c);", "valu", deps=codes, after=after, earliest=LK_START + (LK_NUM * ll) // LK_DEN,
                   ties=("tie_cd(c);",)))
         place(_Op(f"lkr<{nxt}, {r}, {ll}>(c);", "u16", lds=True, after=[(f"lka<{r}, {ll}>(c);", 1)]))
     tile0 = [f"lkr<{nxt}, {ll % 4}, {ll}>(c);" for ll in range(8)]
     for d in range(4):
-        place(_Op(f"pk<{nxt}, 0, {d}>(c);", "valu", deps=tile0, after=[(t, 4) for t in tile0], earliest=52 + d,
+        place(_Op(f"pk<{nxt}, 0, {d}>(c);", "valu", deps=tile0, after=[(t, 4) for t in tile0], earliest=PK_NEXT + d,
                   latest=NGAPS - 3, ties=(f"tie8(c.T[{nxt}][0]);",)))
     if phase == 0:
         for a in range(12):
