@@ -185,6 +185,24 @@ int hif8_linear_fwd_wq_grouped(const uint16_t *a, const uint16_t *w_q, const uin
                                const int64_t *ns, int groups, int64_t M, int64_t K, hif8_stream_t stream);
 
 /* ---------------------------------------------------------------------------
+ * The DiT block's q/k normalisation and rotary embedding in one pass (the harness around the
+ * path: the q/k projections' outputs on their way into attention).  x and out are bf16
+ * [rows, dim], weight fp32 [dim]:
+ *   y = rnd_bf16(rnd_f32(rnd_bf16(x * rsqrt(mean(x^2) + eps)) * weight))
+ * is WanRMSNorm with an fp32 weight and a bf16 output (want2v.py:77-93 as osp_next.py:666-667
+ * runs it under the high-precision norm policy).  With cos_t/sin_t (fp32 [cos batches, seq,
+ * head_dim / 2]) each head's pairs (y[2i], y[2i+1]) are then rotated in fp32 by the angle of
+ * the row's token (osp_next.py:596-644; row r is token r % seq of batch r / seq, which uses cos
+ * batch r / seq / rep) and rounded to bf16 as the attention casts them (attention.py:460-518);
+ * with NULL tables out = y (the cross-attention's norms, osp_next.py:794-796).  Shapes:
+ * dim % 512 == 0, dim <= 8192; with rope 512 % head_dim == 0, dim % head_dim == 0 and
+ * rows % seq == 0.  16-byte aligned pointers.  No counterpart of its own in the reference,
+ * which runs these as about fifteen torch ops. */
+int hif8_rms_norm_rope(const uint16_t *x, const float *weight, const float *cos_t, const float *sin_t, uint16_t *out,
+                       int64_t rows, int64_t dim, int64_t head_dim, int64_t seq, int64_t rep, float eps,
+                       hif8_stream_t stream);
+
+/* ---------------------------------------------------------------------------
  * GEMM-native operand layouts and the tiled fused linear (the fast path of
  * hif8_linear.py:68-86).
  *

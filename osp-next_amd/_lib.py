@@ -48,6 +48,7 @@ SIGNATURES = {
     "hif8_linear_fwd_wq": (_i, [_p, _p, _p, _p, _i64, _i64, _i64, _p]),
     "hif8_linear_fwd_wq_gelu_amax": (_i, [_p, _p, _p, _p, _i64, _i64, _i64, _f, _p, _p]),
     "hif8_linear_fwd_wq_grouped": (_i, [_p, _p, _p, ctypes.POINTER(_p), ctypes.POINTER(_i64), _i, _i64, _i64, _p]),
+    "hif8_rms_norm_rope": (_i, [_p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _f, _p]),
 }
 
 _lib = None

@@ -1,0 +1,160 @@
+// q/k normalisation and rotary embedding of the DiT's attention in one pass (MI355X, gfx950).
+//
+// The reference computes, on the bf16 output of the q (or k) projection x [rows, dim]:
+//   WanRMSNorm with an fp32 weight and a bf16 output (want2v.py:77-93 under the model's
+//   high-precision norm policy):
+//     y1 = rnd_bf16(x * rsqrt(mean(x^2) + eps))      _norm(x.float()).type_as(x)
+//     y2 = rnd_bf16(rnd_f32(y1 * w))                  * weight (fp32), .to(bf16)
+//   then, for self-attention, the 3-D RoPE (osp_next.py:596-644) on pairs (2i, 2i+1) of each
+//   head, in fp32, with the token's angles:
+//     o1 = x1 * cos - x2 * sin,  o2 = x1 * sin + x2 * cos
+//   and the attention's cast of the fp32 result to bf16 (attention.py:460-518): out = rnd_bf16(o).
+// As torch ops that is about fifteen passes over fp32 and bf16 copies of the tensor; here it is
+// one read and one write of bf16 per element.  Every rounding point above is kept (products and
+// sums in fp32, -ffp-contract=off for this file); the mean's sum is taken in this kernel's own
+// order, so y1 can differ from torch's by one bf16 step where x * rsqrt lands next to a rounding
+// boundary.
+//
+// One wavefront per row: lane l holds elements c*512 + 8l .. +7 of each 512-element chunk c, as
+// one 16-byte load; with 512 % head_dim == 0 its four rope pairs have the same in-head index in
+// every chunk, so each lane loads its 4 cosines and 4 sines once per row.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "hif8_internal.h"
+
+namespace hif8 {
+namespace dit {
+
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kThreads = 256;
+constexpr int kMaxChunks = 16;  // dim <= 8192
+
+__device__ __forceinline__ float lo(uint32_t v) { return __builtin_bit_cast(float, v << 16); }
+__device__ __forceinline__ float hi(uint32_t v) { return __builtin_bit_cast(float, v & 0xFFFF0000u); }
+__device__ __forceinline__ uint32_t bf(float f)
+{
+    // round to nearest even; NaN stays NaN
+    const uint32_t u = __builtin_bit_cast(uint32_t, f);
+    if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (u >> 16) | 0x40u;
+    return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
+}
+__device__ __forceinline__ uint32_t pack(float a, float b) { return bf(a) | (bf(b) << 16); }
+
+template <int NC, bool ROPE>
+__global__ __launch_bounds__(kThreads) void k_rms_norm_rope(const uint16_t *__restrict__ x, const float *__restrict__ w,
+                                                            const float *__restrict__ cs, const float *__restrict__ sn,
+                                                            uint16_t *__restrict__ out, int64_t rows, int dim,
+                                                            int head_dim, int64_t seq, int64_t rep, float eps)
+{
+    const int lane = threadIdx.x & 63;
+    const int64_t wstride = int64_t(gridDim.x) * (kThreads / 64);
+    const float inv_dim = 1.0f / float(dim);
+    for (int64_t row = int64_t(blockIdx.x) * (kThreads / 64) + (threadIdx.x >> 6); row < rows; row += wstride) {
+        const u32x4 *xr = (const u32x4 *)(x + row * dim);
+        u32x4 v[NC];
+#pragma unroll
+        for (int c = 0; c < NC; ++c) v[c] = __builtin_nontemporal_load(&xr[c * 64 + lane]);
+        float ss = 0.f;
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const float a = lo(v[c][t]), b = hi(v[c][t]);
+                ss += a * a;
+                ss += b * b;
+            }
+        }
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
+        const float r = rsqrtf(ss * inv_dim + eps);
+        f32x4 ca = {}, sa = {};
+        if (ROPE) {
+            const int64_t s = row % seq;
+            const int64_t cr = (row / seq / rep) * seq + s;
+            const int pair = ((lane * 8) % head_dim) / 2;
+            const int d = head_dim / 2;
+            ca = *(const f32x4 *)(cs + cr * d + pair);
+            sa = *(const f32x4 *)(sn + cr * d + pair);
+        }
+        u32x4 *orow = (u32x4 *)(out + row * dim);
+#pragma unroll
+        for (int c = 0; c < NC; ++c) {
+            const int e0 = c * 512 + lane * 8;
+            const f32x4 w0 = *(const f32x4 *)(w + e0);
+            const f32x4 w1 = *(const f32x4 *)(w + e0 + 4);
+            const float wv[8] = {w0[0], w0[1], w0[2], w0[3], w1[0], w1[1], w1[2], w1[3]};
+            float y[8];
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                y[2 * t] = lo(v[c][t]);
+                y[2 * t + 1] = hi(v[c][t]);
+            }
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float y1 = __builtin_bit_cast(float, bf(y[e] * r) << 16);
+                y[e] = __builtin_bit_cast(float, bf(y1 * wv[e]) << 16);
+            }
+            u32x4 o;
+            if (ROPE) {
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    const float x1 = y[2 * t], x2 = y[2 * t + 1];
+                    const float p1 = x1 * ca[t], p2 = x2 * sa[t], p3 = x1 * sa[t], p4 = x2 * ca[t];
+                    o[t] = pack(p1 - p2, p3 + p4);
+                }
+            } else {
+#pragma unroll
+                for (int t = 0; t < 4; ++t) o[t] = pack(y[2 * t], y[2 * t + 1]);
+            }
+            orow[c * 64 + lane] = o;
+        }
+    }
+}
+
+}  // namespace dit
+}  // namespace hif8
+
+using namespace hif8;
+
+extern "C" int hif8_rms_norm_rope(const uint16_t *x, const float *weight, const float *cos_t, const float *sin_t,
+                                  uint16_t *out, int64_t rows, int64_t dim, int64_t head_dim, int64_t seq,
+                                  int64_t rep, float eps, hif8_stream_t stream)
+{
+    if (!x || !weight || !out || rows <= 0) return HIF8_ERR_ARG;
+    if ((cos_t == nullptr) != (sin_t == nullptr)) return HIF8_ERR_ARG;
+    if (dim <= 0 || dim % 512 != 0 || dim > 512 * dit::kMaxChunks) return HIF8_ERR_SHAPE;
+    const bool rope = cos_t != nullptr;
+    if (rope && (head_dim < 8 || head_dim % 8 != 0 || 512 % head_dim != 0 || dim % head_dim != 0 || seq <= 0 ||
+                 rep <= 0 || rows % seq != 0))
+        return HIF8_ERR_SHAPE;
+    if (((uintptr_t)x | (uintptr_t)out | (uintptr_t)weight) & 15u) return HIF8_ERR_ALIGN;
+    if (rope && (((uintptr_t)cos_t | (uintptr_t)sin_t) & 15u)) return HIF8_ERR_ALIGN;
+    if (rows >= (int64_t(1) << 40)) return HIF8_ERR_SHAPE;
+    int dev = 0, cus = 256;
+    if (hipGetDevice(&dev) == hipSuccess) hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    const int64_t want = (rows + 3) / 4;
+    const int grid = int(want < int64_t(cus) * 8 ? want : int64_t(cus) * 8);
+    hipStream_t s = (hipStream_t)stream;
+    const int nc = int(dim / 512);
+    const int hd = int(head_dim);
+#define HIF8_RN(NC)                                                                                                   \
+    case NC:                                                                                                          \
+        if (rope)                                                                                                     \
+            hipLaunchKernelGGL((dit::k_rms_norm_rope<NC, true>), dim3(grid), dim3(dit::kThreads), 0, s, x, weight,   \
+                               cos_t, sin_t, out, rows, int(dim), hd, seq, rep, eps);                                 \
+        else                                                                                                          \
+            hipLaunchKernelGGL((dit::k_rms_norm_rope<NC, false>), dim3(grid), dim3(dit::kThreads), 0, s, x, weight,  \
+                               cos_t, sin_t, out, rows, int(dim), 8, int64_t(1), int64_t(1), eps);                     \
+        break;
+    switch (nc) {
+        HIF8_RN(1) HIF8_RN(2) HIF8_RN(3) HIF8_RN(4) HIF8_RN(5) HIF8_RN(6) HIF8_RN(7) HIF8_RN(8)
+        HIF8_RN(9) HIF8_RN(10) HIF8_RN(11) HIF8_RN(12) HIF8_RN(13) HIF8_RN(14) HIF8_RN(15) HIF8_RN(16)
+    default:
+        return HIF8_ERR_SHAPE;
+    }
+#undef HIF8_RN
+    return hipGetLastError() == hipSuccess ? HIF8_OK : HIF8_ERR_HIP;
+}

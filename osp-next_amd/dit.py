@@ -38,6 +38,7 @@ import torch.nn as nn
 import torch.nn.functional as F
 from torch import Tensor
 
+from . import _lib
 from .ffn import HIF8FFN
 from .hif8_attention import _HIF8QKVQuantFunction
 from .hif8_linear import (HIF8Linear, QuantState, absmax_scale, fake_quant, grouped_ok, linear_fwd_grouped,
@@ -254,6 +255,40 @@ class SkiparseRopeWrapper:
 # ----------------------------------------------------------------------- norms
 
 
+def fused_norm_ok(x: Tensor, norm: nn.Module) -> bool:
+    """Whether ``norm(x)`` (and the rope after it) can take hif8_rms_norm_rope: inference on a bf16
+    CUDA tensor, an OSPNextRMSNorm with its fp32 weight and bf16 output, a row of 512k <= 8192."""
+    return (isinstance(norm, OSPNextRMSNorm) and norm.output_dtype == torch.bfloat16 and x.is_cuda
+            and x.dtype == torch.bfloat16 and norm.weight.dtype == torch.float32 and x.shape[-1] % 512 == 0
+            and x.shape[-1] <= 8192 and not (torch.is_grad_enabled() and (x.requires_grad or norm.weight.requires_grad)))
+
+
+def rms_norm_rope(x: Tensor, norm: "OSPNextRMSNorm", cos_f: Optional[Tensor] = None,
+                  sin_f: Optional[Tensor] = None, head_dim: int = 128) -> Tensor:
+    """``norm(x)``, and with the angle tables of SkiparseRopeWrapper.prepare_freqs the rotation of
+    apply_rope and the attention's bf16 cast of its fp32 result, in one pass over x
+    (hif8_rms_norm_rope).  x bf16 [B, N, dim] -> bf16 [B, N, dim] (heads of ``head_dim``)."""
+    B, N, dim = x.shape
+    x = x.contiguous()
+    out = torch.empty_like(x)
+    w = norm.weight.detach().contiguous()
+    L = _lib.load()
+    s = _lib.stream_ptr(x.device)
+    if cos_f is None:
+        _lib.check(L.hif8_rms_norm_rope(x.data_ptr(), w.data_ptr(), None, None, out.data_ptr(), B * N, dim, head_dim,
+                                        1, 1, float(norm.eps), s), "hif8_rms_norm_rope")
+        return out
+    fb = cos_f.shape[0]
+    if cos_f.shape[1] != N or (fb > 1 and B % fb != 0):
+        raise ValueError(f"angle tables {tuple(cos_f.shape)} do not match x {tuple(x.shape)}")
+    c = cos_f.to(torch.float32).contiguous()
+    sn = sin_f.to(torch.float32).contiguous()
+    _lib.check(L.hif8_rms_norm_rope(x.data_ptr(), w.data_ptr(), c.data_ptr(), sn.data_ptr(), out.data_ptr(), B * N,
+                                    dim, head_dim, N, B if fb == 1 else B // fb, float(norm.eps), s),
+               "hif8_rms_norm_rope")
+    return out
+
+
 class OSPNextRMSNorm(nn.Module):
     """WanRMSNorm (want2v.py:77-93) with an fp32 weight and a bf16 output, as the model runs it
     under FSDP2's high-precision policy for norms (``output_dtype`` bf16)."""
@@ -389,6 +424,15 @@ class OSPNextSelfAttention(nn.Module):
         ql, kl, vl = qkv
         B, N = ql.shape[:2]
         H, D = self.num_heads, self.head_dim
+        if (qkv_given and self.quant_attn is None and isinstance(self.o, HIF8Linear) and fused_norm_ok(ql, self.norm_q)
+                and fused_norm_ok(kl, self.norm_k)):
+            # norms, rope and the attention's bf16 cast in one pass each; the attention output
+            # is the bf16 value of what the reference returns as fp32 (q's dtype)
+            cos_f, sin_f = rope_wrapper.prepare_freqs(grid_sizes_for_rope, D // 2, self.rearrange_rope)
+            q = rms_norm_rope(ql, self.norm_q, cos_f, sin_f, D).view(B, N, H, D)
+            k = rms_norm_rope(kl, self.norm_k, cos_f, sin_f, D).view(B, N, H, D)
+            x = self._attend(q, k, vl.view(B, N, H, D), attn_mask, out_dtype=torch.bfloat16)
+            return self.o.forward_f32_of_bf16(x.flatten(2))
         q = self.norm_q(ql).view(B, N, H, D)
         k = self.norm_k(kl).view(B, N, H, D)
         v = vl.view(B, N, H, D)
@@ -413,8 +457,13 @@ class OSPNextCrossAttention(OSPNextSelfAttention):
         kv = _grouped_kv(self.k, self.v, text) if fused else None
         if kv is None:
             kv = (self.k(text), self.v(text))
-        q = self.norm_q(self.q(x))
-        k = self.norm_k(kv[0])
+        ql = self.q(x)
+        if fused and self.quant_attn is None and fused_norm_ok(ql, self.norm_q) and fused_norm_ok(kv[0], self.norm_k):
+            q = rms_norm_rope(ql, self.norm_q, head_dim=D)
+            k = rms_norm_rope(kv[0], self.norm_k, head_dim=D)
+        else:
+            q = self.norm_q(ql)
+            k = self.norm_k(kv[0])
         v = kv[1]
         tb = text.shape[0]
         if tb != B:

@@ -60,6 +60,29 @@ def test_block_matches_oracle(dit, kind, f2s, s2f, grid):
     assert nw < TOL_HIF8[0] and mx < TOL_HIF8[1], (nw, mx)
 
 
+@pytest.mark.parametrize("kind,f2s,s2f,grid", [CASES[0], CASES[2], CASES[4]])
+def test_block_fused_norm_rope_matches_oracle(dit, kind, f2s, s2f, grid, monkeypatch):
+    """dim 512 (4 heads of 128): the fused route runs the q/k norms and the rope through
+    hif8_rms_norm_rope (self-attention q/k with rope, cross-attention q/k without)."""
+    calls = []
+    orig = dit.rms_norm_rope
+
+    def spy(*a, **k):
+        calls.append(a[3] is not None if len(a) > 3 else k.get("cos_f") is not None)
+        return orig(*a, **k)
+
+    monkeypatch.setattr(dit, "rms_norm_rope", spy)
+    blk = make_block(dit, kind, f2s, s2f, dim=512, heads=4, ffn=1024, quant="hif8", device=DEV, seed=4)
+    x, e, text = block_inputs(grid, dim=512, seed=5)
+    xin = _layout_in(dit, kind, f2s, x, grid)
+    sd = {k: v.detach().cpu() for k, v in blk.state_dict().items()}
+    want = dit_ref.block(sd, xin, e, text, grid, kind, f2s, s2f, num_heads=4)
+    got = run_block(dit, blk, xin, e, text, grid, kind, True)
+    assert sorted(calls) == [False, False, True, True], calls
+    nw, mx = block_errors(got, want, out_layout(kind, f2s, s2f, xin, grid))
+    assert nw < TOL_HIF8[0] and mx < TOL_HIF8[1], (nw, mx)
+
+
 def test_block_with_hif8_attention(dit):
     """quant_attn="hif8" (configs/infer/npu/osp_hif8_14b.yaml:42): Q/K/V quantised before SDPA."""
     kind, f2s, s2f, grid = CASES[0]
