@@ -280,11 +280,11 @@ def _linear_flops(rows, dim, ffn, L):
     return 2.0 * rows * dim * dim * 6 + 2.0 * L * dim * dim * 2 + 2.0 * rows * dim * ffn * 2
 
 
-def time_block(pkg, torch, reps):
+def time_block(pkg, torch, reps, routes=("fused", "reference")):
     """one 14B block at 720P (x [1, 75600, 5120], grid 21x45x80 padded to 48
     rows -> 4 x 20160 tokens), a Skiparse token block entered from full order, every linear HiF8
     with prepacked weights, dense bf16 attention within the 4 strided sub-grids, cross-attention
-    over 512 text tokens.  Times the fused route and the reference-order route."""
+    over 512 text tokens.  Times the fused route and the reference-order route (``routes``)."""
     D = pkg.dit
     dev = torch.device("cuda:0")
     dim, ffn, heads, grid, L = 5120, 13824, 40, (21, 45, 80), 512
@@ -310,7 +310,7 @@ def time_block(pkg, torch, reps):
     out = {"what": "one 14B DiT block at 720P (token block from full order), all linears HiF8, "
                    "prepacked weights, bf16 SDPA within the 2x2 strided sub-grids",
            "tokens": T * H * W, "rows_padded": rows}
-    for fused in (True, False):
+    for fused in [r == "fused" for r in routes]:
         run(fused)
         torch.cuda.synchronize()
         ea, eb = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -326,7 +326,8 @@ def time_block(pkg, torch, reps):
     af = sum(4.0 * n * v * dim for v in valid) + 4.0 * rows * L * dim
     out["linear_TFLOP"] = round(lf / 1e12, 3)
     out["attention_TFLOP"] = round(af / 1e12, 3)
-    out["TFLOPs_fused"] = round((lf + af) / (out["fused_ms"] * 1e-3) / 1e12, 1)
+    if "fused_ms" in out:
+        out["TFLOPs_fused"] = round((lf + af) / (out["fused_ms"] * 1e-3) / 1e12, 1)
     del blk, x, e, text
     torch.cuda.empty_cache()
     return out
@@ -493,6 +494,8 @@ def main():
     ap.add_argument("--shapes", default="up,modln,qkv,block",
                     help="comma list of up,down,qkvo,ffn,modln,qkv,block (config 4),step (config 5),"
                          "data (the GEMM with constant operands) to time in addition")
+    ap.add_argument("--block-routes", default="fused,reference",
+                    help="routes of the block (config 4) to time: fused, reference or both")
     ap.add_argument("--pmc-calibration", action="store_true",
                     help="also run one plain copy of x (774,144,000 B read + written): the reference "
                          "kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE")
@@ -613,7 +616,7 @@ def main():
     if "block" in args.shapes.split(","):
         log("[bench] timing one 14B DiT block at 720P (config 4)")
         try:
-            extra_shapes["block"] = time_block(pkg, torch, 3)
+            extra_shapes["block"] = time_block(pkg, torch, 3, tuple(args.block_routes.split(",")))
         except Exception as ex:  # the harness around the path (attention backend) may be missing
             extra_shapes["block"] = {"error": repr(ex)}
     if "step" in args.shapes.split(","):
