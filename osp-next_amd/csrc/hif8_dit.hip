@@ -133,8 +133,16 @@ extern "C" int hif8_rms_norm_rope(const uint16_t *x, const float *weight, const 
     if (((uintptr_t)x | (uintptr_t)out | (uintptr_t)weight) & 15u) return HIF8_ERR_ALIGN;
     if (rope && (((uintptr_t)cos_t | (uintptr_t)sin_t) & 15u)) return HIF8_ERR_ALIGN;
     if (rows >= (int64_t(1) << 40)) return HIF8_ERR_SHAPE;
+    static int cu_cache[64] = {0};
     int dev = 0, cus = 256;
-    if (hipGetDevice(&dev) == hipSuccess) hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    if (hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < 64) {
+        if (cu_cache[dev] == 0) {
+            int c = 0;
+            if (hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || c <= 0) c = 256;
+            cu_cache[dev] = c;
+        }
+        cus = cu_cache[dev];
+    }
     const int64_t want = (rows + 3) / 4;
     const int grid = int(want < int64_t(cus) * 8 ? want : int64_t(cus) * 8);
     hipStream_t s = (hipStream_t)stream;

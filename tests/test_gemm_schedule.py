@@ -105,6 +105,9 @@ def w16_asm(tmp_path_factory):
            "-Rpass-analysis=kernel-resource-usage"]
     r = subprocess.run(cmd, capture_output=True, text=True, timeout=600)
     assert r.returncode == 0, r.stderr[-2000:]
+    obj = subprocess.run(cmd[:-5] + ["-c", os.path.join(CSRC, "hif8_gemm_w16.hip"), "-o", str(out) + ".o"],
+                         capture_output=True, text=True, timeout=600)
+    assert obj.returncode == 0, obj.stderr[-2000:]
     return out.read_text(), r.stderr
 
 
