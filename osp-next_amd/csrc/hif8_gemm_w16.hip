@@ -8,8 +8,7 @@
 // it is the faster route.  The products are the same v_mfma_f32_16x16x32_bf16 on the same
 // operand values, in the same k order, so the two kernels agree bit for bit.
 //
-// Design (shared with k_linear_dtl except for W, the MFMA shape, the wave quadrants and the
-// LDS ring):
+// Design (shared with k_linear_dtl except for W, the wave quadrants and the LDS ring):
 //   - One workgroup per 256 x 256 output tile, 4 waves; wave w owns the 128 x 128 quadrant of
 //     rows 128 (w & 1) .. +127 and output features 128 (w >> 1) .. +127: 8 x 8 tiles of
 //     v_mfma_f32_16x16x32_bf16.  At the board's power limit the 16x16x32 form sustains about
