@@ -18,8 +18,10 @@ torch = pytest.importorskip("torch")
 pytestmark = pytest.mark.gpu
 
 DEV = "cuda:0"
+# K = 64, 128, 192, 256: one to four k-steps, the edges of both kernels' pipelines (the
+# decode-free ring's prologue loads two k-steps; the fused kernel pads an odd count)
 SHAPES = [(300, 256, 264), (777, 512, 1024), (256, 64, 256), (1000, 1536, 8960), (2048, 192, 520), (1, 64, 8),
-          (4101, 5120, 5120)]
+          (4101, 5120, 5120), (513, 128, 776), (257, 128, 8), (64, 320, 264)]
 
 
 def operands(pkg, M, K, N, seed, bias=True):
