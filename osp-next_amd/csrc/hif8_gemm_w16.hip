@@ -23,8 +23,14 @@
 //     last loads of a k-step had less than one phase, and the loop waited for the misses of
 //     every panel that L2 does not hold.
 //   - The main loop is the fixed schedule in hif8_gemm_schedule_w16.inc (gen_gemm_schedule.py).
-//   - Epilogue: bias, RNE to bf16, staged through LDS into whole 512-byte row stores; the GELU +
-//     amax variant and grouped outputs as in k_linear_dtl.
+//   - Epilogue: bias, RNE to bf16, staged through LDS into whole 512-byte row stores, non-temporal
+//     (the output is not read again here; it should not displace operand panels from L2); the
+//     GELU + amax variant and grouped outputs as in k_linear_dtl.
+//   - Tile order: groups of group_m m-tiles, n-tiles outer within a group.  Workgroups go to the
+//     8 XCDs round robin, so each XCD runs (group_m / 8) m-tiles x (256 / group_m) n-tiles of
+//     every 256 consecutive tiles and its L2 fetches that many X and W panels.  Measured on the
+//     14B shapes (ms, groups of 16 / 32 / 64 m-tiles): FFN up 7.37 / 7.22 / 7.17, FFN down
+//     (N = 5120) 7.22 / 7.19 / 7.30, o 2.74 / 2.74 / 2.71; 128 was 10 % slower on FFN up.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -40,7 +46,9 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 constexpr int kTile = 256;
 constexpr int kBK = 64;
 constexpr int kThreads = 256;
-constexpr int kGroupM = 16;  // m-tiles per group in the tile order
+// m-tiles per group of the tile order: wide output (>= 32 n-tiles) / narrow output
+constexpr int kGroupWide = 64;
+constexpr int kGroupNarrow = 32;
 
 // LDS map (bytes): operand stage s (0..4) at s * 32K, 256 rows x 128 B (64 k) with the 16-B
 // chunks of row m XOR-swizzled by f(m) = (m & 7) ^ ((m >> 3) & 1): the 32 rows of a fragment
@@ -159,7 +167,7 @@ template <int EPI>
 __global__ __launch_bounds__(kThreads, 1) void k_linear_w16(const uint16_t *__restrict__ X, const uint16_t *__restrict__ Wq,
                                                             const Groups G, const uint16_t *__restrict__ bias,
                                                             int M, int N, int K, int tiles_m, int tiles_n,
-                                                            State *__restrict__ y_st, float y_smax)
+                                                            int group_m, State *__restrict__ y_st, float y_smax)
 {
     __shared__ __attribute__((aligned(1024))) uint8_t smem[kLds];
     ASMV("; lds base %0" ::"v"(uint32_t(uintptr_t(smem))) : "memory");
@@ -168,12 +176,12 @@ __global__ __launch_bounds__(kThreads, 1) void k_linear_w16(const uint16_t *__re
     c.wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t r = lane & 15u, g = lane >> 4;
 
-    // tile order: groups of kGroupM m-tiles, n-tiles outer within a group (as k_linear_dtl)
+    // tile order: groups of group_m m-tiles, n-tiles outer within a group
     const int t = blockIdx.x;
-    const int group = t / (kGroupM * tiles_n);
-    const int first_m = group * kGroupM;
-    const int gm = (tiles_m - first_m) < kGroupM ? (tiles_m - first_m) : kGroupM;
-    const int within = t - group * kGroupM * tiles_n;
+    const int group = t / (group_m * tiles_n);
+    const int first_m = group * group_m;
+    const int gm = (tiles_m - first_m) < group_m ? (tiles_m - first_m) : group_m;
+    const int within = t - group * group_m * tiles_n;
     const int m0 = (first_m + within % gm) * kTile;
     const int n0 = (within / gm) * kTile;
     int gi = 0;
@@ -329,7 +337,8 @@ __global__ __launch_bounds__(kThreads, 1) void k_linear_w16(const uint16_t *__re
 #pragma unroll
             for (int it = 0; it < 8; ++it) {
                 const int m = m0 + int(c.wave * 64u + uint32_t(blk * 8 + it) * 2u + h);
-                if (m < M && n - col0 < ycols) *(u32x4 *)(Y + size_t(m) * size_t(ycols) + (n - col0)) = v[it];
+                if (m < M && n - col0 < ycols)
+                    __builtin_nontemporal_store(v[it], (u32x4 *)(Y + size_t(m) * size_t(ycols) + (n - col0)));
             }
         }
     }
@@ -356,13 +365,14 @@ static int launch_w16(const uint16_t *x, const uint16_t *w_q, const Groups &g, c
     const int tiles_m = int((M + w16::kTile - 1) / w16::kTile);
     const int tiles_n = int((N + w16::kTile - 1) / w16::kTile);
     const int64_t tiles = int64_t(tiles_m) * tiles_n;
+    const int group_m = tiles_n >= 32 ? w16::kGroupWide : w16::kGroupNarrow;
     if (tiles >= (int64_t(1) << 31)) return HIF8_ERR_SHAPE;
     if (y_st)
         hipLaunchKernelGGL(w16::k_linear_w16<1>, dim3(unsigned(tiles)), dim3(w16::kThreads), 0, s, x, w_q, g, bias,
-                           int(M), int(N), int(K), tiles_m, tiles_n, y_st, y_smax);
+                           int(M), int(N), int(K), tiles_m, tiles_n, group_m, y_st, y_smax);
     else
         hipLaunchKernelGGL(w16::k_linear_w16<0>, dim3(unsigned(tiles)), dim3(w16::kThreads), 0, s, x, w_q, g, bias,
-                           int(M), int(N), int(K), tiles_m, tiles_n, (State *)nullptr, 0.0f);
+                           int(M), int(N), int(K), tiles_m, tiles_n, group_m, (State *)nullptr, 0.0f);
     return hipGetLastError() == hipSuccess ? HIF8_OK : HIF8_ERR_HIP;
 }
 
