@@ -275,6 +275,29 @@ int hif8_modln_fake_quant(const uint16_t *x, const uint16_t *shift, const uint16
                           int64_t dim, int64_t rows_per_batch, const float *stats, const void *state,
                           int semantics, uint16_t *x_q, uint16_t *y, hif8_stream_t stream);
 
+/* ---------------------------------------------------------------------------
+ * Producer fusion for the affine LayerNorm in front of the cross-attention's q
+ * projection:
+ *     y = norm3(x)                                        (osp_next.py:949-951)
+ * with norm3 the WanLayerNorm with elementwise_affine (osp_next.py:860-864,
+ * want2v.py:96-106: fp32 layer norm with fp32 weight and bias, cast to bf16), then
+ * _quant(y) of the q projection (hif8_linear.py:42-50).  No single reference
+ * function: it fuses these steps.
+ *
+ * x is bf16 [rows, dim] (dim % 8 == 0, dim <= 6144); weight and bias are fp32 [dim];
+ * stats, x_q, y, state and alignment as for hif8_modln_*, weight and bias 16-byte
+ * aligned.  y = rnd_bf16(weight * ((x - mean) * rstd) + bias), the product-sum fused.
+ * hif8_ln_affine_amax writes stats and folds amax|y| into state (scale rule for
+ * scale_max); hif8_ln_affine_fake_quant writes x_q = qdq(y * s) / s (and y when
+ * non-NULL).  As for hif8_modln_*, y may differ from another fp32 layer norm's by one
+ * bf16 unit next to a rounding boundary; x_q is exactly the qdq of this y.
+ */
+int hif8_ln_affine_amax(const uint16_t *x, const float *weight, const float *bias, int64_t rows, int64_t dim,
+                        float eps, float *stats, float scale_max, void *state, hif8_stream_t stream);
+int hif8_ln_affine_fake_quant(const uint16_t *x, const float *weight, const float *bias, int64_t rows,
+                              int64_t dim, const float *stats, const void *state, int semantics, uint16_t *x_q,
+                              uint16_t *y, hif8_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -277,6 +277,23 @@ def layer_norm_bf16(x_bits, eps: float = 1e-6):
     return f32_to_bf16(n.astype(F32))
 
 
+def affine_layer_norm_bf16(x_bits, weight, bias, eps: float = 1e-6):
+    """The affine WanLayerNorm (norm3: ``osp_next.py:860-864``, applied at ``:949-951``;
+    ``want2v.py:96-106``) of a bf16 [rows, dim] tensor: ``layer_norm(x.float(), (dim,), weight,
+    bias, eps).type_as(x)`` with fp32 weight and bias.  Evaluated in float64 (mean, biased
+    variance, ``(x - mean) / sqrt(var + eps) * weight + bias``) and rounded to fp32 and then to
+    bf16, as ``layer_norm_bf16``."""
+    x = bf16_to_f32(x_bits).astype(np.float64)
+    w = np.asarray(weight, F32).astype(np.float64)
+    b = np.asarray(bias, F32).astype(np.float64)
+    mean = x.mean(axis=-1, keepdims=True)
+    var = np.square(x - mean).mean(axis=-1, keepdims=True)
+    with np.errstate(all="ignore"):
+        n = (x - mean) / np.sqrt(var + np.float64(F32(eps)))
+        y = n * w + b
+    return f32_to_bf16(y.astype(F32))
+
+
 def modulated_layer_norm_bf16(x_bits, shift_bits=None, scale_bits=None, rows_per_batch=None, eps: float = 1e-6):
     """``norm(x) * (1 + scale) + shift`` of ``block_forward`` (``osp_next.py:941``, ``:954``) with
     bf16 tensors: ``n = layer_norm_bf16(x)``, ``t = bf16(1 + scale)``, ``u = bf16(n * t)``,

@@ -48,7 +48,8 @@ from .hif8_linear import (  # noqa: F401
 from .ffn import HIF8FFN  # noqa: F401
 from . import dit  # noqa: F401
 from .dit import OSPNextAttentionBlock, OSPNextBlocks  # noqa: F401
-from .norm import WanLayerNorm, grouped_weight, modulate, modulated_norm_quant, qkv_from_modulated_norm  # noqa: F401
+from .norm import (WanLayerNorm, affine_norm_quant, grouped_weight, modulate, modulated_norm_quant,  # noqa: F401
+                   qkv_from_modulated_norm)
 from .hif8_attention import (  # noqa: F401
     _HIF8QKVQuantFunction,
     attention_with_mask,
@@ -74,7 +75,7 @@ __all__ = [
     "_HIF8QKVQuantFunction", "attention_with_mask", "hif8_attention_with_mask",
     "scaled_dot_product_attention_with_mask", "LinearForward", "LinearForwardFast", "QLinear", "replace_linear",
     "save_packed", "load_packed", "pack_state_dict", "packed_from_codes", "fused_shape_ok", "linear_any",
-    "linear_fwd_gelu_amax", "HIF8FFN", "WanLayerNorm", "modulate", "modulated_norm_quant",
+    "linear_fwd_gelu_amax", "HIF8FFN", "WanLayerNorm", "modulate", "modulated_norm_quant", "affine_norm_quant",
     "qkv_from_modulated_norm", "GroupedWeight", "grouped_ok", "linear_fwd_grouped", "grouped_weight",
     "dit", "OSPNextAttentionBlock", "OSPNextBlocks", "linear_fwd_wq",
 ]

@@ -20,6 +20,12 @@
 // across the wavefront, and the loads of the wavefront's next row are in flight meanwhile.
 // Rows are strided over a grid of 2 workgroups x 4 wavefronts per CU.  With one modulation
 // row, rnd(1 + scale) and shift are computed once per workgroup into LDS as fp32.
+//
+// The same two passes serve the affine LayerNorm in front of the cross-attention's q projection
+// (norm3, osp_next.py:860-864 and 949-951: WanLayerNorm with elementwise_affine, fp32 weight and bias):
+//   y = rnd(w * ((x - mean) * rstd) + b)    (fp32, the product-sum fused, then RNE to bf16)
+// as torch's layer-norm kernel evaluates gamma * (rstd * (x - mean)) + beta on the fp32 copy of
+// x; w and b sit in LDS where the modulation would (hif8_ln_affine_amax / _fake_quant).
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -219,6 +225,33 @@ __device__ __forceinline__ void modln8(const u32x4 &xv, float nmean, float rstd,
                    sh[4], sh[5], sh[6], sh[7], "s", "v");
 }
 
+// Affine LayerNorm of the 8 elements of one chunk: y = rnd(fma(w, (x - mean) * rstd, b)).
+// wb holds the fp32 bits of w, bb the fp32 b (the LDS slots of t and shift).
+__device__ __forceinline__ void lnaff8(const u32x4 &xv, float mean, float rstd, const uint32_t (&wb)[8],
+                                       const float (&bb)[8], uint32_t (&y)[4])
+{
+    const uint32_t w[4] = {xv.x, xv.y, xv.z, xv.w};
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const float t0 = (bf2f(w[k] & 0xFFFFu) - mean) * rstd;
+        const float t1 = (u2f(w[k] & 0xFFFF0000u) - mean) * rstd;
+        y[k] = f2bf_pk(__builtin_fmaf(u2f(wb[2 * k]), t0, bb[2 * k]), __builtin_fmaf(u2f(wb[2 * k + 1]), t1, bb[2 * k + 1]));
+    }
+}
+
+// w and b of the affine LayerNorm into the LDS slots of t and shift (fp32 bits).
+__device__ __forceinline__ void fill_aff(uint32_t *lmod, const float *lw, const float *lb, int dim)
+{
+    for (int c = threadIdx.x; c < (dim >> 3); c += kTPB) {
+        const u32x4 *wp = (const u32x4 *)(lw + 8 * c), *bp = (const u32x4 *)(lb + 8 * c);
+        u32x4 *tp = (u32x4 *)(lmod + 8 * c), *sp = (u32x4 *)(lmod + dim + 8 * c);
+        tp[0] = wp[0];
+        tp[1] = wp[1];
+        sp[0] = bp[0];
+        sp[1] = bp[1];
+    }
+}
+
 // Row statistics of the wavefront's row, chunks in registers.  sum(x) and sum(x^2) come from
 // the bf16 dot product (v_dot2_f32_bf16: the products of bf16 values are exact in fp32), so
 // var = sum(x^2) / dim - mean^2.  When that difference could cancel (mean^2 > var, or a
@@ -275,9 +308,10 @@ __device__ __forceinline__ void load_row(const uint16_t *x, int64_t row, int dim
 
 // Pass 1.  Each wavefront streams its rows with the next row's loads in flight while the
 // current row is reduced.
-template <int NCH, bool MODL, bool FULL>
+template <int NCH, bool MODL, bool FULL, bool AFF>
 __global__ __launch_bounds__(kTPB) void k_modln_amax(const uint16_t *__restrict__ x, const uint16_t *__restrict__ shift,
-                                                      const uint16_t *__restrict__ scale, int64_t rows, int dim,
+                                                      const uint16_t *__restrict__ scale, const float *__restrict__ lw,
+                                                      const float *__restrict__ lb, int64_t rows, int dim,
                                                       int64_t rows_per_batch, float eps, float *__restrict__ stats,
                                                       State *__restrict__ st, float smax)
 {
@@ -285,7 +319,8 @@ __global__ __launch_bounds__(kTPB) void k_modln_amax(const uint16_t *__restrict_
     __shared__ uint32_t red[kWaves + 2];
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int nch_row = dim >> 3;
-    fill_mod<MODL>(lmod, shift, scale, dim);
+    if (AFF) fill_aff(lmod, lw, lb, dim);
+    else fill_mod<MODL>(lmod, shift, scale, dim);
     __syncthreads();
     typedef uint16_t u16x2 __attribute__((ext_vector_type(2)));
     u16x2 m2 = {0, 0};
@@ -304,7 +339,8 @@ __global__ __launch_bounds__(kTPB) void k_modln_amax(const uint16_t *__restrict_
                 float sh[8];
                 load_mod<MODL>(lm, shift, scale, moff, lane + 64 * j, dim, tw, sh);
                 uint32_t y[4];
-                modln8(xv[j], -mean, rstd, tw, sh, one_lo, one_hi, y);
+                if (AFF) lnaff8(xv[j], mean, rstd, tw, sh, y);
+                else modln8(xv[j], -mean, rstd, tw, sh, one_lo, one_hi, y);
 #pragma unroll
                 for (int k = 0; k < 4; ++k)
                     m2 = __builtin_elementwise_max(m2, __builtin_bit_cast(u16x2, y[k] & 0x7FFF7FFFu));
@@ -394,7 +430,7 @@ constexpr uint32_t kQdqEnc = 512;
 constexpr uint32_t kQdqLds = (kQdqEnc + sizeof(EncTable) > 2 * kYTab) ? kQdqEnc + sizeof(EncTable) : 2 * kYTab;
 
 // MODE 0: y-table (NPU, finite); 1: codec tables (FAST); 2: scalar reference route.
-template <int NCH, bool MODL, bool FULL, int MODE>
+template <int NCH, bool MODL, bool FULL, bool AFF, int MODE>
 __device__ __forceinline__ void qdq_rows(const uint16_t *x, const uint16_t *shift, const uint16_t *scale, int64_t rows,
                                          int dim, int64_t rows_per_batch, const float *stats, float s, int sem,
                                          uint16_t *xq, uint16_t *yout, const uint32_t *lmod, const uint8_t *lds,
@@ -423,7 +459,8 @@ __device__ __forceinline__ void qdq_rows(const uint16_t *x, const uint16_t *shif
                 float sh[8];
                 load_mod<MODL>(lm, shift, scale, moff, c, dim, tw, sh);
                 uint32_t y[4], o[4];
-                modln8(xv[j], -mean, rstd, tw, sh, one_lo, one_hi, y);
+                if (AFF) lnaff8(xv[j], mean, rstd, tw, sh, y);
+                else modln8(xv[j], -mean, rstd, tw, sh, one_lo, one_hi, y);
                 if (MODE == 0) qdq8_ytab(y, ylo, yhi, ytab, o);
                 else qdq8_codec<MODE == 1>(y, s, sem, enc, lut16, o);
                 xo[c] = u32x4{o[0], o[1], o[2], o[3]};
@@ -449,9 +486,10 @@ __device__ __forceinline__ void qdq_rows(const uint16_t *x, const uint16_t *shif
 // to stream at HBM rate.
 template <int NCH, bool MODL> constexpr int qdq_waves() { return NCH > 10 ? 1 : (MODL ? 3 : 2); }
 
-template <int NCH, bool MODL, bool FULL>
+template <int NCH, bool MODL, bool FULL, bool AFF>
 __global__ __launch_bounds__(kTPB) __attribute__((amdgpu_waves_per_eu(qdq_waves<NCH, MODL>()))) void k_modln_qdq(const uint16_t *__restrict__ x, const uint16_t *__restrict__ shift,
-                                                     const uint16_t *__restrict__ scale, int64_t rows, int dim,
+                                                     const uint16_t *__restrict__ scale, const float *__restrict__ lw,
+                                                     const float *__restrict__ lb, int64_t rows, int dim,
                                                      int64_t rows_per_batch, const float *__restrict__ stats,
                                                      const State *__restrict__ st, int sem, uint16_t *__restrict__ xq,
                                                      uint16_t *__restrict__ yout)
@@ -462,7 +500,8 @@ __global__ __launch_bounds__(kTPB) __attribute__((amdgpu_waves_per_eu(qdq_waves<
     const int tid = threadIdx.x;
     const float s = st->scale;
     const bool fast = st->fast != 0 && st->finite != 0;
-    fill_mod<MODL>(lmod, shift, scale, dim);
+    if (AFF) fill_aff(lmod, lw, lb, dim);
+    else fill_mod<MODL>(lmod, shift, scale, dim);
     uint32_t ylo = 0;
     bool use_ytab = fast && sem == kSemNpu;
     if (use_ytab) {
@@ -493,11 +532,11 @@ __global__ __launch_bounds__(kTPB) __attribute__((amdgpu_waves_per_eu(qdq_waves<
     }
     __syncthreads();
     if (use_ytab)
-        qdq_rows<NCH, MODL, FULL, 0>(x, shift, scale, rows, dim, rows_per_batch, stats, s, sem, xq, yout, lmod, lds, ylo);
+        qdq_rows<NCH, MODL, FULL, AFF, 0>(x, shift, scale, rows, dim, rows_per_batch, stats, s, sem, xq, yout, lmod, lds, ylo);
     else if (fast)
-        qdq_rows<NCH, MODL, FULL, 1>(x, shift, scale, rows, dim, rows_per_batch, stats, s, sem, xq, yout, lmod, lds, ylo);
+        qdq_rows<NCH, MODL, FULL, AFF, 1>(x, shift, scale, rows, dim, rows_per_batch, stats, s, sem, xq, yout, lmod, lds, ylo);
     else
-        qdq_rows<NCH, MODL, FULL, 2>(x, shift, scale, rows, dim, rows_per_batch, stats, s, sem, xq, yout, lmod, lds, ylo);
+        qdq_rows<NCH, MODL, FULL, AFF, 2>(x, shift, scale, rows, dim, rows_per_batch, stats, s, sem, xq, yout, lmod, lds, ylo);
 }
 
 static int cu_count()
@@ -550,13 +589,13 @@ static void launch_amax(bool modl, int grid, hipStream_t s, const uint16_t *x, c
 {
     if constexpr (NCH * 512 <= 6144) {
         if (modl) {
-            hipLaunchKernelGGL((k_modln_amax<NCH, true, FULL>), dim3(grid), dim3(kTPB), size_t(8 * dim), s, x, shift,
-                               scale, rows, dim, rpb, eps, stats, st, smax);
+            hipLaunchKernelGGL((k_modln_amax<NCH, true, FULL, false>), dim3(grid), dim3(kTPB), size_t(8 * dim), s, x,
+                               shift, scale, nullptr, nullptr, rows, dim, rpb, eps, stats, st, smax);
             return;
         }
     }
-    hipLaunchKernelGGL((k_modln_amax<NCH, false, FULL>), dim3(grid), dim3(kTPB), 0, s, x, shift, scale, rows, dim,
-                       rpb, eps, stats, st, smax);
+    hipLaunchKernelGGL((k_modln_amax<NCH, false, FULL, false>), dim3(grid), dim3(kTPB), 0, s, x, shift, scale,
+                       nullptr, nullptr, rows, dim, rpb, eps, stats, st, smax);
 }
 
 template <int NCH, bool FULL>
@@ -566,13 +605,33 @@ static void launch_qdq(bool modl, int grid, hipStream_t s, const uint16_t *x, co
 {
     if constexpr (NCH * 512 <= 6144) {
         if (modl) {
-            hipLaunchKernelGGL((k_modln_qdq<NCH, true, FULL>), dim3(grid), dim3(kTPB), size_t(8 * dim), s, x, shift,
-                               scale, rows, dim, rpb, stats, st, sem, xq, y);
+            hipLaunchKernelGGL((k_modln_qdq<NCH, true, FULL, false>), dim3(grid), dim3(kTPB), size_t(8 * dim), s, x,
+                               shift, scale, nullptr, nullptr, rows, dim, rpb, stats, st, sem, xq, y);
             return;
         }
     }
-    hipLaunchKernelGGL((k_modln_qdq<NCH, false, FULL>), dim3(grid), dim3(kTPB), 0, s, x, shift, scale, rows, dim,
-                       rpb, stats, st, sem, xq, y);
+    hipLaunchKernelGGL((k_modln_qdq<NCH, false, FULL, false>), dim3(grid), dim3(kTPB), 0, s, x, shift, scale,
+                       nullptr, nullptr, rows, dim, rpb, stats, st, sem, xq, y);
+}
+
+// The affine LayerNorm: w and b in LDS (8 * dim bytes, sized at launch), dim <= kAffMaxDim
+// (checked by the entry points; dims above 4096 other than 5120 take the 16-chunk instantiation).
+constexpr int64_t kAffMaxDim = 6144;
+
+template <int NCH, bool FULL>
+static void launch_amax_aff(int grid, hipStream_t s, const uint16_t *x, const float *lw, const float *lb, int64_t rows,
+                            int dim, float eps, float *stats, State *st, float smax)
+{
+    hipLaunchKernelGGL((k_modln_amax<NCH, true, FULL, true>), dim3(grid), dim3(kTPB), size_t(8 * dim), s, x, nullptr,
+                       nullptr, lw, lb, rows, dim, rows, eps, stats, st, smax);
+}
+
+template <int NCH, bool FULL>
+static void launch_qdq_aff(int grid, hipStream_t s, const uint16_t *x, const float *lw, const float *lb, int64_t rows,
+                           int dim, const float *stats, const State *st, int sem, uint16_t *xq, uint16_t *y)
+{
+    hipLaunchKernelGGL((k_modln_qdq<NCH, true, FULL, true>), dim3(grid), dim3(kTPB), size_t(8 * dim), s, x, nullptr,
+                       nullptr, lw, lb, rows, dim, rows, stats, st, sem, xq, y);
 }
 
 // Calls F<NCH, FULL>::run(args...) for the instantiation covering dim.
@@ -597,6 +656,12 @@ template <int NCH, bool FULL> struct AmaxL {
 };
 template <int NCH, bool FULL> struct QdqL {
     template <typename... A> static void run(A... a) { launch_qdq<NCH, FULL>(a...); }
+};
+template <int NCH, bool FULL> struct AmaxAffL {
+    template <typename... A> static void run(A... a) { launch_amax_aff<NCH, false>(a...); }
+};
+template <int NCH, bool FULL> struct QdqAffL {
+    template <typename... A> static void run(A... a) { launch_qdq_aff<NCH, FULL>(a...); }
 };
 
 }  // namespace norm
@@ -632,6 +697,42 @@ int hif8_modln_fake_quant(const uint16_t *x, const uint16_t *shift, const uint16
     const int st = dispatch_dim<QdqL>(dim, modl, grid_for_rows(rows, kQdqWgPerCu), (hipStream_t)stream, x, shift,
                                       scale, rows, int(dim), rows_per_batch, stats, (const State *)state, semantics,
                                       x_q, y);
+    if (st != HIF8_OK) return st;
+    return hipGetLastError() == hipSuccess ? HIF8_OK : HIF8_ERR_HIP;
+}
+
+static int check_aff(const uint16_t *x, const float *weight, const float *bias, int64_t rows, int64_t dim,
+                     const void *stats, const void *state)
+{
+    const int rc = check_args(x, nullptr, nullptr, rows, dim, rows, stats, state);
+    if (rc != HIF8_OK) return rc;
+    if (!weight || !bias) return HIF8_ERR_ARG;
+    if (dim > kAffMaxDim) return HIF8_ERR_SHAPE;
+    if (!aligned16(weight) || !aligned16(bias)) return HIF8_ERR_ALIGN;
+    return HIF8_OK;
+}
+
+int hif8_ln_affine_amax(const uint16_t *x, const float *weight, const float *bias, int64_t rows, int64_t dim,
+                        float eps, float *stats, float scale_max, void *state, hif8_stream_t stream)
+{
+    const int rc = check_aff(x, weight, bias, rows, dim, stats, state);
+    if (rc != HIF8_OK) return rc;
+    const int st = dispatch_dim<AmaxAffL>(dim, grid_for_rows(rows, kWgPerCu), (hipStream_t)stream, x, weight, bias,
+                                          rows, int(dim), eps, stats, (State *)state, scale_max);
+    if (st != HIF8_OK) return st;
+    return hipGetLastError() == hipSuccess ? HIF8_OK : HIF8_ERR_HIP;
+}
+
+int hif8_ln_affine_fake_quant(const uint16_t *x, const float *weight, const float *bias, int64_t rows, int64_t dim,
+                              const float *stats, const void *state, int semantics, uint16_t *x_q, uint16_t *y,
+                              hif8_stream_t stream)
+{
+    const int rc = check_aff(x, weight, bias, rows, dim, stats, state);
+    if (rc != HIF8_OK) return rc;
+    if (!x_q || (semantics != HIF8_SEM_NPU && semantics != HIF8_SEM_TORCH)) return HIF8_ERR_ARG;
+    if (!aligned16(x_q) || (y && !aligned16(y))) return HIF8_ERR_ALIGN;
+    const int st = dispatch_dim<QdqAffL>(dim, grid_for_rows(rows, kQdqWgPerCu), (hipStream_t)stream, x, weight, bias,
+                                         rows, int(dim), stats, (const State *)state, semantics, x_q, y);
     if (st != HIF8_OK) return st;
     return hipGetLastError() == hipSuccess ? HIF8_OK : HIF8_ERR_HIP;
 }

@@ -15,7 +15,8 @@ Two routes through a block, chosen per call:
   same modulated norm.
 * **fused** (inference): ``modulated_norm_quant`` produces the quantised q/k/v input once and
   the three projections run as one grouped GEMM; cross-attention's k and v quantise the text
-  once and run grouped; the FFN takes the quantised modulated norm of ``norm2`` and runs its
+  once and run grouped; cross-attention's q takes the quantised affine norm of ``norm3`` from
+  ``affine_norm_quant``; the FFN takes the quantised modulated norm of ``norm2`` and runs its
   up-projection with the GELU + amax epilogue.  Every quantised operand is the one the
   reference would build (the producers are bit-exact after the layer norm).
 
@@ -43,7 +44,8 @@ from .ffn import HIF8FFN
 from .hif8_attention import _HIF8QKVQuantFunction
 from .hif8_linear import (HIF8Linear, QuantState, absmax_scale, fake_quant, grouped_ok, linear_fwd_grouped,
                           make_linear)
-from .norm import WanLayerNorm, grouped_weight, modulated_norm_quant, qkv_from_modulated_norm
+from .norm import (WanLayerNorm, affine_fused_ok, affine_norm_quant, grouped_weight, modulated_norm_quant,
+                   qkv_from_modulated_norm)
 
 
 # ----------------------------------------------------------------- block kinds
@@ -451,13 +453,16 @@ class OSPNextCrossAttention(OSPNextSelfAttention):
     the text per sub-sequence, ``osp_next.py:973``): every query then attends to the same keys,
     so the sub-sequences are attended as one."""
 
-    def forward(self, x: Tensor, attn_mask: Optional[Tensor], text: Tensor, fused: bool = False) -> Tensor:
-        B = x.shape[0]
+    def forward(self, x: Optional[Tensor], attn_mask: Optional[Tensor], text: Tensor, fused: bool = False,
+                x_q: Optional[Tensor] = None) -> Tensor:
+        """``x_q``: the q input already quantised with q's ``scale_max_forward`` (``_quant(x)[0]``,
+        e.g. from ``affine_norm_quant``) in place of x; q then runs the GEMM alone."""
+        B = (x if x_q is None else x_q).shape[0]
         H, D = self.num_heads, self.head_dim
         kv = _grouped_kv(self.k, self.v, text) if fused else None
         if kv is None:
             kv = (self.k(text), self.v(text))
-        ql = self.q(x)
+        ql = self.q(x) if x_q is None else self.q.forward_quantized(x_q)
         if fused and self.quant_attn is None and fused_norm_ok(ql, self.norm_q) and fused_norm_ok(kv[0], self.norm_k):
             q = rms_norm_rope(ql, self.norm_q, head_dim=D)
             k = rms_norm_rope(kv[0], self.norm_k, head_dim=D)
@@ -556,7 +561,13 @@ class OSPNextAttentionBlock(nn.Module):
         else:
             y = sa(self.norm1(x) * (1 + e[1]) + e[0], attn_mask, grid_sizes_for_rope, rope_wrapper)
         x = x + y * e[2]
-        x = x + self.cross_attn(self.norm3(x), cross_attn_mask, text, fused=fused)
+        ca = self.cross_attn
+        if (fused and isinstance(ca.q, HIF8Linear) and ca.q.a_format == "bf16"
+                and affine_fused_ok(x, self.norm3)):
+            xq3, _ = affine_norm_quant(x, self.norm3, ca.q.scale_max_forward)
+            x = x + ca(None, cross_attn_mask, text, fused=True, x_q=xq3)
+        else:
+            x = x + ca(self.norm3(x), cross_attn_mask, text, fused=fused)
         if fused and isinstance(self.ffn, HIF8FFN) and self.ffn.fused_ok(x):
             xq, _ = modulated_norm_quant(x, e[3], e[4], self.eps, self.ffn[0].scale_max_forward)
             y = self.ffn.forward_quantized(xq)

@@ -6,7 +6,8 @@ WanLayerNorm (``ospnext/modules/want2v.py:96-106``); every consuming HIF8Linear 
 ``_quant`` on that tensor (``hif8_linear.py:42-50``), so q, k and v quantise the same input
 three times.  ``modulated_norm_quant`` produces the quantised input directly, in two passes
 over x (``hif8_modln_amax`` and ``hif8_modln_fake_quant``), and ``qkv_from_modulated_norm``
-feeds it to the three projections with one quantisation.
+feeds it to the three projections with one quantisation.  ``affine_norm_quant`` does the same
+for the affine LayerNorm (norm3) in front of the cross-attention's q projection.
 
 The fused route is inference-only (no autograd through the producer) and takes bf16 x with
 ``dim % 8 == 0`` and ``dim <= 8192``; anything else runs the reference's op sequence with the
@@ -106,6 +107,55 @@ def modulated_norm_quant(x: Tensor, shift: Optional[Tensor] = None, scale: Optio
     _lib.check(L.hif8_modln_fake_quant(x.data_ptr(), sh_p, sc_p, rows, D, rpb, stats.data_ptr(), st.ptr,
                                        int(semantics), xq.data_ptr(), y.data_ptr() if y is not None else None, s),
                "hif8_modln_fake_quant")
+    return (xq, st, y) if return_y else (xq, st)
+
+
+AFFINE_MAX_DIM = 6144
+
+
+def affine_fused_ok(x: Tensor, norm: nn.Module) -> bool:
+    """The fused affine producer takes bf16 CUDA x with dim % 8 == 0, dim <= 6144, and a
+    WanLayerNorm with fp32 weight and bias."""
+    w, b = getattr(norm, "weight", None), getattr(norm, "bias", None)
+    return (fused_ok(x) and x.shape[-1] <= AFFINE_MAX_DIM and isinstance(norm, nn.LayerNorm)
+            and w is not None and b is not None and w.dtype == torch.float32 and b.dtype == torch.float32
+            and tuple(norm.normalized_shape) == (x.shape[-1],) and w.device == x.device)
+
+
+def affine_norm_quant(x: Tensor, norm: nn.Module, scale_max: float = 15.0, semantics: int = _lib.SEM_NPU,
+                      return_y: bool = False):
+    """x_q = _quant(norm(x))[0] in bf16 for the affine WanLayerNorm ``norm`` (norm3,
+    osp_next.py:860-864, 949-951): the input the cross-attention's q projection quantises.
+    Returns ``(x_q, state)``, plus y = norm(x) with ``return_y``.  Two passes over x
+    (``hif8_ln_affine_amax`` and ``hif8_ln_affine_fake_quant``); other shapes and dtypes run
+    the module and the library's ``_quant`` on the GPU."""
+    if torch.is_grad_enabled() and (x.requires_grad or any(p.requires_grad for p in norm.parameters())):
+        raise RuntimeError("affine_norm_quant has no autograd; use the norm module and HIF8Linear.forward "
+                           "when gradients are needed")
+    if not affine_fused_ok(x, norm):
+        y = norm(x).contiguous()
+        st = absmax_scale(y, scale_max, QuantState(y.device))
+        xq = fake_quant(y, st, semantics)
+        return (xq, st, y) if return_y else (xq, st)
+    x = x.contiguous()
+    if x.data_ptr() % 16:
+        x = x.clone()
+    w = norm.weight.detach().contiguous()
+    b = norm.bias.detach().contiguous()
+    D = x.shape[-1]
+    rows = x.numel() // D
+    stats = torch.empty(rows * 2, dtype=torch.float32, device=x.device)
+    st = QuantState(x.device)
+    L = _lib.load()
+    s = _lib.stream_ptr(x.device)
+    _lib.check(L.hif8_ln_affine_amax(x.data_ptr(), w.data_ptr(), b.data_ptr(), rows, D, float(norm.eps),
+                                     stats.data_ptr(), float(scale_max), st.ptr, s), "hif8_ln_affine_amax")
+    xq = torch.empty_like(x)
+    y = torch.empty_like(x) if return_y else None
+    _lib.check(L.hif8_ln_affine_fake_quant(x.data_ptr(), w.data_ptr(), b.data_ptr(), rows, D, stats.data_ptr(),
+                                           st.ptr, int(semantics), xq.data_ptr(),
+                                           y.data_ptr() if y is not None else None, s),
+               "hif8_ln_affine_fake_quant")
     return (xq, st, y) if return_y else (xq, st)
 
 

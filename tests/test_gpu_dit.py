@@ -63,7 +63,8 @@ def test_block_matches_oracle(dit, kind, f2s, s2f, grid):
 @pytest.mark.parametrize("kind,f2s,s2f,grid", [CASES[0], CASES[2], CASES[4]])
 def test_block_fused_norm_rope_matches_oracle(dit, kind, f2s, s2f, grid, monkeypatch):
     """dim 512 (4 heads of 128): the fused route runs the q/k norms and the rope through
-    hif8_rms_norm_rope (self-attention q/k with rope, cross-attention q/k without)."""
+    hif8_rms_norm_rope (self-attention q/k with rope, cross-attention q/k without) and norm3
+    with the cross-attention q's quantisation through hif8_ln_affine_*."""
     calls = []
     orig = dit.rms_norm_rope
 
@@ -72,6 +73,14 @@ def test_block_fused_norm_rope_matches_oracle(dit, kind, f2s, s2f, grid, monkeyp
         return orig(*a, **k)
 
     monkeypatch.setattr(dit, "rms_norm_rope", spy)
+    aff = []
+    orig_aff = dit.affine_norm_quant
+
+    def spy_aff(*a, **k):
+        aff.append(1)
+        return orig_aff(*a, **k)
+
+    monkeypatch.setattr(dit, "affine_norm_quant", spy_aff)
     blk = make_block(dit, kind, f2s, s2f, dim=512, heads=4, ffn=1024, quant="hif8", device=DEV, seed=4)
     x, e, text = block_inputs(grid, dim=512, seed=5)
     xin = _layout_in(dit, kind, f2s, x, grid)
@@ -79,6 +88,7 @@ def test_block_fused_norm_rope_matches_oracle(dit, kind, f2s, s2f, grid, monkeyp
     want = dit_ref.block(sd, xin, e, text, grid, kind, f2s, s2f, num_heads=4)
     got = run_block(dit, blk, xin, e, text, grid, kind, True)
     assert sorted(calls) == [False, False, True, True], calls
+    assert aff == [1], aff          # norm3 + the cross-attention q's quantisation in one producer
     nw, mx = block_errors(got, want, out_layout(kind, f2s, s2f, xin, grid))
     assert nw < TOL_HIF8[0] and mx < TOL_HIF8[1], (nw, mx)
 

@@ -188,3 +188,86 @@ def test_modln_full_size_consistency(pkg):
     err = (y[0, rows].double() - y_t.double()).abs()
     assert bool((err <= 2.0 ** -7 * (u.double().abs() + y_t.double().abs())).all())
     assert float((y[0, rows] != y_t).double().mean()) < 1e-3
+
+
+# ------------------------------------------------------------------ affine LayerNorm (norm3)
+
+def affine_norm(pkg, D, seed):
+    g = torch.Generator().manual_seed(seed)
+    norm = pkg.WanLayerNorm(D, eps=1e-6, elementwise_affine=True).to(DEV)
+    with torch.no_grad():
+        norm.weight.copy_(1 + 0.3 * torch.randn(D, generator=g))
+        norm.bias.copy_(0.2 * torch.randn(D, generator=g))
+    return norm
+
+
+def check_affine_y(R, yb, x, norm, frac=1e-3):
+    """y against the oracle's float64 affine layer norm: equal except on fewer than ``frac`` of
+    the elements, and there within one bf16 unit of y plus fp32-level error of the terms
+    n * w and b (their sum can cancel)."""
+    D = x.shape[-1]
+    w = norm.weight.detach().cpu().numpy()
+    b = norm.bias.detach().cpu().numpy()
+    want = R.affine_layer_norm_bf16(bits(x).reshape(-1, D), w, b, 1e-6)
+    n = R.bf16_to_f32(R.layer_norm_bf16(bits(x).reshape(-1, D), 1e-6)).astype(np.float64)
+    terms = np.abs(n * w[None]) + np.abs(b[None])
+    a, t = R.bf16_to_f32(yb).astype(np.float64), R.bf16_to_f32(want).astype(np.float64)
+    assert np.all(np.abs(a - t) <= 2.0 ** -7 * np.abs(t) + 2.0 ** -16 * terms)
+    assert (yb != want).mean() < frac, float((yb != want).mean())
+
+
+@pytest.mark.parametrize("B,N,D", [(1, 300, 1536), (2, 150, 5120), (1, 5, 8), (3, 7, 72), (1, 1, 512),
+                                   (1, 40, 6144)])
+@pytest.mark.parametrize("sem", ["npu", "torch"])
+def test_affine_norm_quant_matches_oracle(pkg, R, B, N, D, sem):
+    x, _, _ = make(B * 1000 + N + D + 7, B, N, D, with_mod=False)
+    norm = affine_norm(pkg, D, D + N)
+    semc = pkg._lib.SEM_NPU if sem == "npu" else pkg._lib.SEM_TORCH
+    print(f"[affine_norm] B={B} N={N} D={D} {sem}", flush=True)
+    with torch.no_grad():
+        xq, st, y = pkg.affine_norm_quant(x, norm, 15.0, semc, return_y=True)
+    torch.cuda.synchronize()
+    yb = bits(y).reshape(-1, D)
+    check_affine_y(R, yb, x, norm)
+    amax_bits, scale_f = st.read()
+    assert amax_bits == R.absmax_bf16(yb)
+    sb = R.hif8_scale_bf16(amax_bits, 15.0)
+    assert np.float32(scale_f) == R.bf16_to_f32(np.array([sb], np.uint16))[0]
+    want, _ = R.quant_bf16(yb, 15.0, sem)
+    assert np.array_equal(bits(xq).reshape(-1, D), want)
+
+
+def test_affine_norm_quant_constant_rows_give_the_bias(pkg, R):
+    """A constant row normalises to exactly 0, so y there is bf16(bias)."""
+    x, _, _ = make(21, 1, 32, 512, with_mod=False)
+    x[0, 5] = 3.25
+    norm = affine_norm(pkg, 512, 3)
+    with torch.no_grad():
+        _, _, y = pkg.affine_norm_quant(x, norm, return_y=True)
+    want = bits(norm.bias.detach().to(torch.bfloat16))
+    assert np.array_equal(bits(y[0, 5]), want)
+
+
+def test_affine_norm_quant_falls_back_and_rejects(pkg, R):
+    """dim > 6144 or a bf16 weight take the module + _quant on the GPU; the C-ABI rejects
+    shapes and pointers outside its contract."""
+    x, _, _ = make(22, 1, 16, 8192, with_mod=False)
+    norm = affine_norm(pkg, 8192, 4)
+    with torch.no_grad():
+        xq, st, y = pkg.affine_norm_quant(x, norm, return_y=True)
+        assert torch.equal(y, norm(x))
+        want, _ = pkg._quant(y, 15.0)
+    assert torch.equal(xq.view(torch.int16), want.view(torch.int16))
+    L = pkg._lib.load()
+    s = pkg._lib.stream_ptr(torch.device(DEV))
+    xs = torch.zeros(8, 1024, dtype=torch.bfloat16, device=DEV)
+    w = torch.ones(8192, dtype=torch.float32, device=DEV)
+    stats = torch.empty(16, dtype=torch.float32, device=DEV)
+    stq = pkg.QuantState(DEV)
+    assert L.hif8_ln_affine_amax(xs.data_ptr(), w.data_ptr(), None, 8, 1024, 1e-6, stats.data_ptr(), 15.0, stq.ptr, s) != 0
+    assert L.hif8_ln_affine_amax(xs.data_ptr(), w.data_ptr(), w.data_ptr(), 1, 8192, 1e-6, stats.data_ptr(), 15.0,
+                                 stq.ptr, s) != 0                       # dim above the LDS limit
+    assert L.hif8_ln_affine_amax(xs.data_ptr(), w.data_ptr() + 4, w.data_ptr(), 8, 1024, 1e-6, stats.data_ptr(),
+                                 15.0, stq.ptr, s) != 0                 # misaligned weight
+    assert L.hif8_ln_affine_amax(xs.data_ptr(), w.data_ptr(), w.data_ptr(), 8, 1020, 1e-6, stats.data_ptr(), 15.0,
+                                 stq.ptr, s) != 0                       # dim % 8

@@ -503,3 +503,60 @@ def test_modulated_layer_norm_planted_mistakes(R):
     u = R.f32_to_bf16(R.bf16_to_f32(nb) * R.bf16_to_f32(t))
     y_bad = R.f32_to_bf16(R.bf16_to_f32(u) + R.bf16_to_f32(shb))
     assert (_bf16_ulp(y_bad, want) > 0).mean() > 0.05
+
+
+def _affine_case(seed, B=2, N=96, D=1536):
+    torch, x, _, _ = _modln_case(seed, B, N, D)
+    g = torch.Generator().manual_seed(seed + 1)
+    w = 1 + 0.3 * torch.randn(D, generator=g)
+    b = 0.2 * torch.randn(D, generator=g)
+    return torch, x, w, b
+
+
+def test_affine_layer_norm_matches_torch_cpu(R):
+    """The affine LayerNorm (norm3, want2v.py:96-106 with elementwise_affine) against torch's
+    layer_norm on the CPU with fp32 weight and bias, cast back to bf16: a library routine, to
+    one bf16 unit on a small fraction of elements (fp32 evaluation order)."""
+    torch, x, w, b = _affine_case(11)
+    D = x.shape[-1]
+    y_t = torch.nn.functional.layer_norm(x.float(), (D,), w, b, eps=1e-6).type_as(x)
+    y_o = R.affine_layer_norm_bf16(_bits(x).reshape(-1, D), w.numpy(), b.numpy(), 1e-6)
+    yt = _bits(y_t).reshape(-1, D)
+    d = _bf16_ulp(y_o, yt)
+    assert (d > 0).mean() < 1e-3, (d > 0).mean()
+    # where n * w + b cancels, fp32 error relative to |n * w| is several units of the small y:
+    # bound each difference by one bf16 unit of y plus fp32-level error of the terms
+    n = R.bf16_to_f32(R.layer_norm_bf16(_bits(x).reshape(-1, D), 1e-6)).astype(np.float64)
+    terms = np.abs(n * w.numpy()[None]) + np.abs(b.numpy()[None])
+    a_o, a_t = R.bf16_to_f32(y_o).astype(np.float64), R.bf16_to_f32(yt).astype(np.float64)
+    assert np.all(np.abs(a_o - a_t) <= 2.0 ** -7 * np.abs(a_t) + 2.0 ** -16 * terms)
+
+
+def test_affine_layer_norm_closed_forms_and_planted_mistakes(R):
+    """Closed forms: a constant row normalises to 0, so y = bias exactly; a two-valued row +-a
+    (a >= 1) to +-1, so y = bf16(weight + bias) / bf16(bias - weight).  Plausible wrong
+    restatements (weight and bias swapped, bias dropped, weight applied before the
+    normalisation) fail the torch comparison."""
+    D = 64
+    x = np.zeros((2, D), np.float32)
+    x[0] = 7.25
+    x[1, ::2], x[1, 1::2] = 3.0, -3.0
+    w = np.linspace(0.5, 2.0, D, dtype=np.float32)
+    b = np.linspace(-1.0, 1.0, D, dtype=np.float32)
+    y = R.bf16_to_f32(R.affine_layer_norm_bf16(R.f32_to_bf16(x), w, b))
+    assert np.array_equal(y[0], R.bf16_to_f32(R.f32_to_bf16(b)))
+    want1 = np.where(x[1] > 0, w + b, b - w).astype(np.float32)
+    assert np.array_equal(y[1], R.bf16_to_f32(R.f32_to_bf16(want1)))
+
+    torch, xt, wt, bt = _affine_case(13, B=1, N=64, D=512)
+    Dt = xt.shape[-1]
+    want = _bits(torch.nn.functional.layer_norm(xt.float(), (Dt,), wt, bt, eps=1e-6).type_as(xt)).reshape(-1, Dt)
+    xb = _bits(xt).reshape(-1, Dt)
+
+    def frac(yb):
+        return float((_bf16_ulp(yb, want) > 1).mean())
+    assert frac(R.affine_layer_norm_bf16(xb, wt.numpy(), bt.numpy())) == 0.0
+    assert frac(R.affine_layer_norm_bf16(xb, bt.numpy(), wt.numpy())) > 0.1            # swapped
+    assert frac(R.affine_layer_norm_bf16(xb, wt.numpy(), np.zeros(Dt, np.float32))) > 0.1   # no bias
+    xw = R.f32_to_bf16(R.bf16_to_f32(xb) * wt.numpy()[None])                          # weight first
+    assert frac(R.affine_layer_norm_bf16(xw, np.ones(Dt, np.float32), bt.numpy())) > 0.1
