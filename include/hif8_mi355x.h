@@ -276,6 +276,17 @@ int hif8_modln_fake_quant(const uint16_t *x, const uint16_t *shift, const uint16
                           int semantics, uint16_t *x_q, uint16_t *y, hif8_stream_t stream);
 
 /* ---------------------------------------------------------------------------
+ * The block's residual updates (the harness around the path): x + y * e[2] and x + y * e[5]
+ * (osp_next.py:947, :955) and x + cross_attn(...) (osp_next.py:949), as torch's bf16 ops
+ * compute them: t = rnd_bf16(y * gate), out = rnd_bf16(x + t), each in fp32; with gate NULL,
+ * out = rnd_bf16(x + y).  x, y, out bf16 [rows, dim]; gate bf16 [rows / rows_per_batch, dim]
+ * (row r uses gate row r / rows_per_batch).  dim % 8 == 0, 16-byte aligned pointers; out may
+ * be x.  No counterpart of its own in the reference, which runs them as two torch ops.
+ */
+int hif8_gated_residual(const uint16_t *x, const uint16_t *y, const uint16_t *gate, uint16_t *out, int64_t rows,
+                        int64_t dim, int64_t rows_per_batch, hif8_stream_t stream);
+
+/* ---------------------------------------------------------------------------
  * Producer fusion for the affine LayerNorm in front of the cross-attention's q
  * projection:
  *     y = norm3(x)                                        (osp_next.py:949-951)

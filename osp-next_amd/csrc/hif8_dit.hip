@@ -114,6 +114,47 @@ __global__ __launch_bounds__(kThreads) void k_rms_norm_rope(const uint16_t *__re
     }
 }
 
+// Gated residual of the block (osp_next.py:947, :955): out = x + y * gate as torch's bf16 ops
+// compute it, t = rnd_bf16(y * g) then out = rnd_bf16(x + t), each in fp32 (no fused
+// multiply-add; this file is built with -ffp-contract=off).  gate is one bf16 row of dim per
+// batch of rows_per_batch rows; with no gate, out = rnd_bf16(x + y) (osp_next.py:949).  Each
+// thread takes 8 elements (16 bytes) per step.
+// RNE to bf16 as torch's software conversion does it, NaN as the canonical 0x7FC0.
+__device__ __forceinline__ uint32_t bf_t(float f)
+{
+    const uint32_t u = __builtin_bit_cast(uint32_t, f);
+    if ((u & 0x7FFFFFFFu) > 0x7F800000u) return 0x7FC0u;
+    return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
+}
+__device__ __forceinline__ uint32_t pack_t(float a, float b) { return bf_t(a) | (bf_t(b) << 16); }
+
+template <bool GATE>
+__global__ __launch_bounds__(kThreads) void k_gated_residual(const u32x4 *__restrict__ x, const u32x4 *__restrict__ y,
+                                                             const uint16_t *__restrict__ gate, u32x4 *__restrict__ out,
+                                                             int64_t nvec, int64_t dim, int64_t rows_per_batch)
+{
+    const int64_t stride = int64_t(gridDim.x) * kThreads;
+    for (int64_t i = int64_t(blockIdx.x) * kThreads + threadIdx.x; i < nvec; i += stride) {
+        const u32x4 xv = __builtin_nontemporal_load(&x[i]);
+        const u32x4 yv = __builtin_nontemporal_load(&y[i]);
+        u32x4 o;
+        if (GATE) {
+            const int64_t e0 = i * 8;
+            const int64_t row = e0 / dim, col = e0 - row * dim;
+            const u32x4 gv = *(const u32x4 *)(gate + (row / rows_per_batch) * dim + col);
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const uint32_t tp = pack_t(lo(yv[t]) * lo(gv[t]), hi(yv[t]) * hi(gv[t]));
+                o[t] = pack_t(lo(xv[t]) + lo(tp), hi(xv[t]) + hi(tp));
+            }
+        } else {
+#pragma unroll
+            for (int t = 0; t < 4; ++t) o[t] = pack_t(lo(xv[t]) + lo(yv[t]), hi(xv[t]) + hi(yv[t]));
+        }
+        __builtin_nontemporal_store(o, &out[i]);
+    }
+}
+
 }  // namespace dit
 }  // namespace hif8
 
@@ -164,5 +205,29 @@ extern "C" int hif8_rms_norm_rope(const uint16_t *x, const float *weight, const 
         return HIF8_ERR_SHAPE;
     }
 #undef HIF8_RN
+    return hipGetLastError() == hipSuccess ? HIF8_OK : HIF8_ERR_HIP;
+}
+
+extern "C" int hif8_gated_residual(const uint16_t *x, const uint16_t *y, const uint16_t *gate, uint16_t *out,
+                                   int64_t rows, int64_t dim, int64_t rows_per_batch, hif8_stream_t stream)
+{
+    if (!x || !y || !out || rows <= 0 || dim <= 0) return HIF8_ERR_ARG;
+    if (dim % 8 != 0 || rows >= (int64_t(1) << 40) || dim >= (int64_t(1) << 24)) return HIF8_ERR_SHAPE;
+    if (gate && (rows_per_batch <= 0 || rows % rows_per_batch != 0)) return HIF8_ERR_SHAPE;
+    if (((uintptr_t)x | (uintptr_t)y | (uintptr_t)out | (uintptr_t)gate) & 15u) return HIF8_ERR_ALIGN;
+    const int64_t nvec = rows * dim / 8;
+    int dev = 0, cus = 256;
+    if (hipGetDevice(&dev) == hipSuccess && hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+        cus = 256;
+    const int64_t want = (nvec + dit::kThreads - 1) / dit::kThreads;
+    const int grid = int(want < int64_t(cus) * 8 ? want : int64_t(cus) * 8);
+    hipStream_t s = (hipStream_t)stream;
+    typedef dit::u32x4 V;
+    if (gate)
+        hipLaunchKernelGGL(dit::k_gated_residual<true>, dim3(grid), dim3(dit::kThreads), 0, s, (const V *)x,
+                           (const V *)y, gate, (V *)out, nvec, dim, rows_per_batch);
+    else
+        hipLaunchKernelGGL(dit::k_gated_residual<false>, dim3(grid), dim3(dit::kThreads), 0, s, (const V *)x,
+                           (const V *)y, (const uint16_t *)nullptr, (V *)out, nvec, dim, int64_t(1));
     return hipGetLastError() == hipSuccess ? HIF8_OK : HIF8_ERR_HIP;
 }

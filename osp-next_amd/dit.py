@@ -265,6 +265,33 @@ def fused_norm_ok(x: Tensor, norm: nn.Module) -> bool:
             and x.shape[-1] <= 8192 and not (torch.is_grad_enabled() and (x.requires_grad or norm.weight.requires_grad)))
 
 
+def gated_residual(x: Tensor, y: Tensor, gate: Optional[Tensor] = None) -> Tensor:
+    """``x + y * gate`` (``osp_next.py:947, :955``; ``x + y`` without gate, ``:949``) as torch's
+    bf16 ops compute it, in one pass (``hif8_gated_residual``): the same bits as the two torch
+    ops.  ``gate`` is [B, 1, D] / [1, 1, D] for x of [B, N, D].  Other dtypes, layouts or
+    shapes run the torch ops."""
+    ok = (x.is_cuda and x.dtype == y.dtype == torch.bfloat16 and x.shape == y.shape and x.dim() == 3
+          and x.is_contiguous() and y.is_contiguous() and x.shape[-1] % 8 == 0 and x.numel() > 0
+          and x.data_ptr() % 16 == 0 and y.data_ptr() % 16 == 0)
+    if ok and gate is not None:
+        B, N, D = x.shape
+        ok = (gate.dtype == torch.bfloat16 and gate.dim() == 3 and gate.shape[1] == 1 and gate.shape[2] == D
+              and gate.shape[0] in (1, B) and gate.device == x.device)
+    if not ok:
+        return x + y if gate is None else x + y * gate
+    B, N, D = x.shape
+    out = torch.empty_like(x)
+    g = None
+    rpb = B * N
+    if gate is not None:
+        g = gate.reshape(-1, D).contiguous()
+        rpb = N if g.shape[0] == B else B * N
+    _lib.check(_lib.load().hif8_gated_residual(x.data_ptr(), y.data_ptr(), g.data_ptr() if g is not None else None,
+                                               out.data_ptr(), B * N, D, rpb, _lib.stream_ptr(x.device)),
+               "hif8_gated_residual")
+    return out
+
+
 def rms_norm_rope(x: Tensor, norm: "OSPNextRMSNorm", cos_f: Optional[Tensor] = None,
                   sin_f: Optional[Tensor] = None, head_dim: int = 128) -> Tensor:
     """``norm(x)``, and with the angle tables of SkiparseRopeWrapper.prepare_freqs the rotation of
@@ -560,12 +587,12 @@ class OSPNextAttentionBlock(nn.Module):
             y = sa(None, attn_mask, grid_sizes_for_rope, rope_wrapper, qkv=qkv)
         else:
             y = sa(self.norm1(x) * (1 + e[1]) + e[0], attn_mask, grid_sizes_for_rope, rope_wrapper)
-        x = x + y * e[2]
+        x = gated_residual(x, y, e[2]) if fused else x + y * e[2]
         ca = self.cross_attn
         if (fused and isinstance(ca.q, HIF8Linear) and ca.q.a_format == "bf16"
                 and affine_fused_ok(x, self.norm3)):
             xq3, _ = affine_norm_quant(x, self.norm3, ca.q.scale_max_forward)
-            x = x + ca(None, cross_attn_mask, text, fused=True, x_q=xq3)
+            x = gated_residual(x, ca(None, cross_attn_mask, text, fused=True, x_q=xq3))
         else:
             x = x + ca(self.norm3(x), cross_attn_mask, text, fused=fused)
         if fused and isinstance(self.ffn, HIF8FFN) and self.ffn.fused_ok(x):
@@ -573,7 +600,7 @@ class OSPNextAttentionBlock(nn.Module):
             y = self.ffn.forward_quantized(xq)
         else:
             y = self.ffn(self.norm2(x) * (1 + e[4]) + e[3])
-        return x + y * e[5]
+        return gated_residual(x, y, e[5]) if fused else x + y * e[5]
 
     def forward(self, x: Tensor, attn_mask: Optional[Tensor], cross_attn_mask: Optional[Tensor], e: Tensor,
                 sub_grid_sizes, grid_sizes_for_rope, rope_wrapper: SkiparseRopeWrapper, text: Tensor,

@@ -93,3 +93,42 @@ def test_rejects_bad_shapes(pkg):
                                 1e-6, s) != 0   # rows % seq
     assert L.hif8_rms_norm_rope(x.data_ptr() + 2, w.data_ptr(), None, None, o.data_ptr(), 4, 1024, 128, 1, 1, 1e-6, s) != 0
     assert L.hif8_rms_norm_rope(None, w.data_ptr(), None, None, o.data_ptr(), 8, 1024, 128, 1, 1, 1e-6, s) != 0
+
+
+@pytest.mark.parametrize("B,N,D,gate", [(2, 300, 5120, "batch"), (1, 777, 1536, "one"), (3, 65, 512, "none"),
+                                        (1, 5, 8, "batch")])
+def test_gated_residual_equals_torch_ops(pkg, B, N, D, gate):
+    """hif8_gated_residual against the block's own torch ops (osp_next.py:947, :949, :955):
+    x + y * gate with bf16 tensors, bit for bit (the same fp32 op and RNE at each step)."""
+    D_ = pkg.dit
+    g = torch.Generator().manual_seed(B * 7 + N + D)
+    x = (torch.randn(B, N, D, generator=g) * 4).to(torch.bfloat16).to(DEV)
+    y = (torch.randn(B, N, D, generator=g) * 3).to(torch.bfloat16).to(DEV)
+    y[0, 0, :4] = torch.tensor([float("inf"), -0.0, 1e-38, 3e38])
+    x[0, 0, 4:6] = torch.tensor([float("nan"), float("-inf")])          # NaN in, and inf - inf
+    y[0, 0, 5] = float("inf")
+    gt = None
+    if gate == "batch":
+        gt = torch.randn(B, 1, D, generator=g).to(torch.bfloat16).to(DEV)
+    elif gate == "one":
+        gt = torch.randn(1, 1, D, generator=g).to(torch.bfloat16).to(DEV)
+    print(f"[gated_residual] B={B} N={N} D={D} {gate}", flush=True)
+    got = D_.gated_residual(x, y, gt)
+    want = x + y if gt is None else x + y * gt
+    torch.cuda.synchronize()
+    assert torch.equal(got.view(torch.int16), want.view(torch.int16))
+
+
+def test_gated_residual_fallback_and_rejects(pkg):
+    D_ = pkg.dit
+    x = torch.randn(2, 10, 12, device=DEV).to(torch.bfloat16)       # D % 8 != 0: torch ops
+    y = torch.randn(2, 10, 12, device=DEV).to(torch.bfloat16)
+    gt = torch.randn(2, 1, 12, device=DEV).to(torch.bfloat16)
+    assert torch.equal(D_.gated_residual(x, y, gt), x + y * gt)
+    L = pkg._lib.load()
+    s = pkg._lib.stream_ptr(torch.device(DEV))
+    a = torch.zeros(4, 64, dtype=torch.bfloat16, device=DEV)
+    assert L.hif8_gated_residual(a.data_ptr(), a.data_ptr(), a.data_ptr(), a.data_ptr(), 4, 64, 3, s) != 0  # rows % rpb
+    assert L.hif8_gated_residual(a.data_ptr(), a.data_ptr(), None, a.data_ptr(), 4, 60, 1, s) != 0          # dim % 8
+    assert L.hif8_gated_residual(a.data_ptr() + 2, a.data_ptr(), None, a.data_ptr(), 2, 64, 1, s) != 0      # alignment
+    assert L.hif8_gated_residual(None, a.data_ptr(), None, a.data_ptr(), 4, 64, 1, s) != 0
