@@ -12,7 +12,7 @@ route (the weight codes decoded to bf16 once per call, then the decode-free GEMM
 dequant-GEMM route is timed beside it (other_route).  The per-kernel times come from HIP
 events on the stream the kernels run on (torch's current stream).
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--a-format bf16|codes]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu]
                     [--route auto|fused|decode_once] [--shapes ...]
 """
 from __future__ import annotations
@@ -45,36 +45,27 @@ def make_inputs(torch, M, K, N, seed=0, dev="cuda:0"):
     return x, w, b
 
 
-def time_linear(pkg, torch, x, packed, b, steps, warmup, a_format, route="fused"):
+def time_linear(pkg, torch, x, packed, b, steps, warmup, route="fused"):
     """Times steps of [amax+scale, quantise, GEMM]; returns per-phase ms lists.
 
-    a_format "tiled": x_q written in the GEMM operand layout + tiled fused GEMM; "bf16"/"codes":
-    row-major x_q / codes and the row-major fused GEMM.  route "decode_once" (bf16 only): the GEMM
-    phase is hif8_decode of the weight codes into a bf16 buffer, then the decode-free GEMM
-    hif8_linear_fwd_wq (the HIF8Linear route from DECODE_ONCE_MIN_ROWS rows up); its two parts
-    are timed separately as well."""
+    route "fused": the fused dequant-GEMM hif8_linear_fwd on the packed weight codes;
+    "decode_once": the GEMM phase is hif8_decode of the weight codes into a bf16 buffer, then the
+    decode-free GEMM hif8_linear_fwd_wq (the HIF8Linear route from DECODE_ONCE_MIN_ROWS rows up);
+    its two parts are timed separately as well."""
     st = pkg.QuantState(x.device)
     L = pkg._lib.load()
     stream = pkg._lib.stream_ptr(x.device)
     M, K = x.shape
     N = packed.shape[0]
     y = torch.empty(M, N, dtype=torch.bfloat16, device=x.device)
-    if a_format == "tiled":
-        a = torch.empty(pkg.tiled_rows(M) * K, dtype=torch.bfloat16, device=x.device)
-    else:
-        a = torch.empty((M, K), dtype=torch.uint8 if a_format == "codes" else torch.bfloat16, device=x.device)
+    a = torch.empty((M, K), dtype=torch.bfloat16, device=x.device)
     wq = torch.empty((N, K), dtype=torch.bfloat16, device=x.device) if route == "decode_once" else None
 
     def amax():
         pkg._lib.check(L.hif8_absmax_scale(x.data_ptr(), 0, x.numel(), 15.0, st.ptr, stream), "amax")
 
     def quant():
-        if a_format == "tiled":
-            pkg._lib.check(L.hif8_fake_quant_tiled(x.data_ptr(), 0, M, K, st.ptr, a.data_ptr(), 0, stream), "qt")
-        elif a_format == "codes":
-            pkg._lib.check(L.hif8_encode(x.data_ptr(), 0, x.numel(), st.ptr, a.data_ptr(), stream), "encode")
-        else:
-            pkg._lib.check(L.hif8_fake_quant(x.data_ptr(), 0, x.numel(), st.ptr, a.data_ptr(), 0, stream), "qdq")
+        pkg._lib.check(L.hif8_fake_quant(x.data_ptr(), 0, x.numel(), st.ptr, a.data_ptr(), 0, stream), "qdq")
 
     def wdecode():
         pkg._lib.check(L.hif8_decode(packed.codes.data_ptr(), N * K, packed.state.ptr, 0, wq.data_ptr(), stream),
@@ -84,13 +75,9 @@ def time_linear(pkg, torch, x, packed, b, steps, warmup, a_format, route="fused"
         if route == "decode_once":
             pkg._lib.check(L.hif8_linear_fwd_wq(a.data_ptr(), wq.data_ptr(), b.data_ptr(), y.data_ptr(), M, N, K,
                                                 stream), "linear_wq")
-        elif a_format == "tiled":
-            pkg._lib.check(L.hif8_linear_fwd_tiled(a.data_ptr(), packed.wt.data_ptr(), packed.state.ptr,
-                                                   b.data_ptr(), y.data_ptr(), M, N, K, stream), "linear")
         else:
-            fmt = pkg._lib.A_CODES if a_format == "codes" else pkg._lib.A_BF16
-            pkg._lib.check(L.hif8_linear_fwd(a.data_ptr(), fmt, st.ptr, packed.codes.data_ptr(), packed.state.ptr,
-                                             b.data_ptr(), y.data_ptr(), M, N, K, stream), "linear")
+            pkg._lib.check(L.hif8_linear_fwd(a.data_ptr(), packed.codes.data_ptr(), packed.state.ptr, b.data_ptr(),
+                                             y.data_ptr(), M, N, K, stream), "linear")
 
     def wdec_maybe():
         if route == "decode_once":
@@ -166,6 +153,89 @@ def time_ffn(pkg, torch, x, reps):
     out["speedup"] = round(out["sequence_ms"] / out["fused_ms"], 4)
     out["what"] = "FFN 5120->13824->5120 on x[75600,5120] bf16, prepacked weights, no autograd"
     del mod
+    return out
+
+
+def time_backward(pkg, torch, x, packed, reps):
+    """The backward of the FFN-up HIF8Linear (hif8_linear.py:88-111) at the 14B 720P shape: the
+    gradient's _quant with scale_max 224, dgrad grad_q [M, N] @ w_q [N, K] (the transposed codes
+    decoded once, then the decode-free GEMM) and wgrad grad_q^T @ x_q (both operands transposed
+    with the tokens padded to the k-step, then the decode-free GEMM); each phase timed with HIP
+    events on the launch stream.  hipBLASLt on the same operands for context."""
+    dev = x.device
+    M, K = x.shape
+    N = packed.shape[0]
+    L = pkg._lib.load()
+    stream = pkg._lib.stream_ptr(dev)
+    gen = torch.Generator(device=dev).manual_seed(6)
+    gy = (torch.randn(M, N, generator=gen, device=dev) * 1e-3).to(torch.bfloat16)
+    xq = pkg.fake_quant(x, pkg.absmax_scale(x, 15.0, pkg.QuantState(dev)))
+    st = pkg.QuantState(dev)
+    gq = torch.empty_like(gy)
+    codes_t = packed.codes_t()
+    w_qt = torch.empty((K, N), dtype=torch.bfloat16, device=dev)
+    Mp = (M + 63) // 64 * 64
+    g_t = torch.empty((N, Mp), dtype=torch.bfloat16, device=dev)
+    x_t = torch.empty((K, Mp), dtype=torch.bfloat16, device=dev)
+    gx = torch.empty((M, K), dtype=torch.bfloat16, device=dev)
+    gw = torch.empty((N, K), dtype=torch.bfloat16, device=dev)
+    ck = pkg._lib.check
+    phases = {
+        "grad_quant": lambda: (ck(L.hif8_absmax_scale(gy.data_ptr(), 0, gy.numel(), 224.0, st.ptr, stream), "amax"),
+                               ck(L.hif8_fake_quant(gy.data_ptr(), 0, gy.numel(), st.ptr, gq.data_ptr(), 0, stream),
+                                  "qdq")),
+        "dgrad_wdecode": lambda: ck(L.hif8_decode(codes_t.data_ptr(), N * K, packed.state.ptr, 0, w_qt.data_ptr(),
+                                                  stream), "decode"),
+        "dgrad_gemm": lambda: ck(L.hif8_linear_fwd_wq(gq.data_ptr(), w_qt.data_ptr(), None, gx.data_ptr(), M, K, N,
+                                                      stream), "dgrad"),
+        "wgrad_transposes": lambda: (ck(L.hif8_transpose_bf16(gq.data_ptr(), M, N, Mp, g_t.data_ptr(), stream), "tg"),
+                                     ck(L.hif8_transpose_bf16(xq.data_ptr(), M, K, Mp, x_t.data_ptr(), stream), "tx")),
+        "wgrad_gemm": lambda: ck(L.hif8_linear_fwd_wq(g_t.data_ptr(), x_t.data_ptr(), None, gw.data_ptr(), N, K, Mp,
+                                                      stream), "wgrad"),
+    }
+    for _ in range(2):
+        for fn in phases.values():
+            fn()
+    torch.cuda.synchronize()
+    times = {k: [] for k in phases}
+    for _ in range(reps):
+        for k, fn in phases.items():
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            fn()
+            e1.record()
+            torch.cuda.synchronize()
+            times[k].append(e0.elapsed_time(e1))
+    ms = {k: round(sum(v) / len(v), 4) for k, v in times.items()}
+    flops = 2.0 * M * N * K
+    out = {"what": f"FFN-up HIF8Linear backward at x[{M},{K}], W[{N},{K}]: grad_q (224), dgrad, wgrad",
+           "phases_ms": ms,
+           "dgrad_TFLOPs": round(flops / (ms["dgrad_gemm"] * 1e-3) / 1e12, 1),
+           "dgrad_frac": round(flops / (ms["dgrad_gemm"] * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+           "wgrad_TFLOPs": round(flops / (ms["wgrad_gemm"] * 1e-3) / 1e12, 1),
+           "wgrad_frac": round(flops / (ms["wgrad_gemm"] * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+           "wgrad_with_transposes_TFLOPs": round(flops / ((ms["wgrad_gemm"] + ms["wgrad_transposes"]) * 1e-3) / 1e12, 1),
+           "backward_ms": round(sum(ms.values()), 4)}
+    # hipBLASLt on the same operands (context only): grad_q @ w_q and grad_q^T @ x_q
+    try:
+        w_q = packed.dequantize()
+        vt = {}
+        for label, fn in (("dgrad", lambda: gq @ w_q), ("wgrad", lambda: gq.t() @ xq)):
+            fn()
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(reps):
+                fn()
+            e1.record()
+            torch.cuda.synchronize()
+            vt[f"{label}_ms"] = round(e0.elapsed_time(e1) / reps, 4)
+        out["vendor_bf16_gemm"] = vt
+        del w_q
+    except Exception as ex:  # informative only
+        out["vendor_bf16_gemm"] = {"error": str(ex)}
+    del gy, gq, g_t, x_t, gx, gw, w_qt, xq
+    torch.cuda.empty_cache()
     return out
 
 
@@ -395,8 +465,8 @@ def time_data_dependence(pkg, torch, x, w, reps):
 
     def gemm_ms(xq, pw):
         def run():
-            pkg._lib.check(L.hif8_linear_fwd(xq.data_ptr(), pkg._lib.A_BF16, None, pw.codes.data_ptr(), pw.state.ptr,
-                                             None, y.data_ptr(), M, N, K, stream), "linear")
+            pkg._lib.check(L.hif8_linear_fwd(xq.data_ptr(), pw.codes.data_ptr(), pw.state.ptr, None, y.data_ptr(),
+                                             M, N, K, stream), "linear")
         run()
         torch.cuda.synchronize()
         ea, eb = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -425,27 +495,79 @@ def median(v):
     return s[len(s) // 2]
 
 
-def _cpu_model() -> str:
+def _cpu_info():
+    """The host CPU as ``lscpu`` names it, and the instruction-set flags that decide its bf16 GEMM
+    rate (AMX, AVX-512 BF16): ``(model, {flag: present})``.  /proc/cpuinfo when lscpu is absent."""
+    model, flags = None, set()
     try:
-        with open("/proc/cpuinfo") as f:
-            for line in f:
-                if line.startswith("model name"):
-                    return line.split(":", 1)[1].strip()
-    except OSError:
+        import subprocess
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=20).stdout
+        for line in out.splitlines():
+            key, _, val = line.partition(":")
+            if key.strip() == "Model name" and model is None:
+                model = val.strip()
+            elif key.strip() == "Flags":
+                flags = set(val.split())
+    except Exception:
         pass
-    return platform.machine()
+    if model is None or not flags:
+        try:
+            with open("/proc/cpuinfo") as f:
+                for line in f:
+                    key, _, val = line.partition(":")
+                    if key.strip() == "model name" and model is None:
+                        model = val.strip()
+                    elif key.strip() == "flags" and not flags:
+                        flags = set(val.split())
+        except OSError:
+            pass
+    names = ("amx_bf16", "amx_tile", "amx_int8", "avx512_bf16", "avx512f", "avx512_vnni", "avx2")
+    return model or platform.machine(), {n: n in flags for n in names}
+
+
+def _cpu_threads():
+    """Threads for the CPU baseline: every CPU this process may run on (its affinity set), capped
+    by OMP_NUM_THREADS when the environment sets it (the GPU box grants each one-GPU job a CPU
+    share and sets OMP_NUM_THREADS to it)."""
+    try:
+        n = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        n = os.cpu_count() or 1
+    omp = os.environ.get("OMP_NUM_THREADS", "")
+    if omp.isdigit() and int(omp) > 0:
+        n = min(n, int(omp))
+    return max(1, n)
+
+
+def _time_cpu(fn, warm, max_runs=3, budget_s=15.0):
+    """One warm-up call of ``warm``, then the median of up to ``max_runs`` calls of ``fn`` (fewer when
+    a call takes more than ``budget_s``); returns (median seconds, runs)."""
+    warm()
+    ts = []
+    for _ in range(max_runs):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+        if ts[-1] > budget_s:
+            break
+    return median(ts), len(ts)
 
 
 def cpu_baseline(torch, M, K, N, sample_rows=4096, target_s=10.0):
-    """The reference CPU path (torch ops: _quant + quant_hif8 + F.linear in bf16) on a bounded
-    sample of the same workload: a [sample_rows, K] slice of x (quantise + GEMM against the
-    quantised W) repeated until about ``target_s`` seconds of CPU work, and the per-call weight
-    quantisation twice; the full step is the weight part plus the slice time scaled to M."""
-    sys.path.insert(0, ROOT)
-    from oracle import hif8_ref as R
-    import torch.nn.functional as F
+    """The reference CPU path (torch ops: _quant + quant_hif8 + F.linear in bf16) on the host.
 
-    threads = min(os.cpu_count() or 1, 16)
+    Headline (``value``): the 14B FFN-up shape on a bounded sample -- a [sample_rows, K] slice of
+    x (quantise + GEMM against the quantised W) repeated until about ``target_s`` seconds of CPU
+    work, and the per-call weight quantisation twice; the full step is the weight part plus the
+    slice time scaled to M (both the qdq and the GEMM are linear in M).  Beside it, BASELINE
+    config 1 (the qdq of a [4096, 5120] tensor) and config 2 (the three Wan-1.3B 480P linears) at
+    full size: a warm-up on a slice, then the median of three runs."""
+    sys.path.insert(0, ROOT)
+    import numpy as np
+    import torch.nn.functional as F
+    from oracle import hif8_ref as R
+
+    threads = _cpu_threads()
     torch.set_num_threads(threads)
     g = torch.Generator().manual_seed(0)
     x = torch.randn(sample_rows, K, generator=g)
@@ -472,13 +594,41 @@ def cpu_baseline(torch, M, K, N, sample_rows=4096, target_s=10.0):
     tw, ts = median(t_w), median(t_slice)
     t_full = tw + (M / sample_rows) * ts
     value = 2.0 * M * N * K / t_full / 1e12
+    del x, w, wq, xq
+
+    # config 1: _quant of the [4096, 5120] bf16 tensor (N(0, 0.02), 0.1 % outliers x50, seed 0)
+    c1_bits = R.c1_input(0)
+    c1 = torch.from_numpy(c1_bits.view(np.int16)).view(torch.bfloat16)
+    t_c1, n_c1 = _time_cpu(lambda: R.quant_torch_cpu(c1, 15.0), lambda: R.quant_torch_cpu(c1[:256], 15.0))
+    c1_out = {"what": "_quant (torch-path qdq) of x[4096,5120] bf16", "s": round(t_c1, 4), "runs": n_c1,
+              "GBps_algorithmic": round(4.0 * c1.numel() / t_c1 / 1e9, 3)}
+    del c1
+    # config 2: Wan-1.3B 480P, x [32760, 1536] N(0,1) with 8 outlier channels x20 (seed 1); the FFN-down
+    # input is [32760, 8960] from the same recipe; W N(0, 0.02) (seeds 2, 3, 4), zero bias
+    c2 = {}
+    Mc = 32760
+    for name, n_, k_, seed in (("qkvo", 1536, 1536, 2), ("ffn_up", 8960, 1536, 3), ("ffn_down", 1536, 8960, 4)):
+        gx = torch.Generator().manual_seed(1)
+        xc = torch.randn(Mc, k_, generator=gx)
+        xc[:, torch.randperm(k_, generator=gx)[:8]] *= 20
+        xc = xc.to(torch.bfloat16)
+        wc = (torch.randn(n_, k_, generator=torch.Generator().manual_seed(seed)) * 0.02).to(torch.bfloat16)
+        bc = torch.zeros(n_, dtype=torch.bfloat16)
+        t_c, n_c = _time_cpu(lambda: R.linear_torch_cpu(xc, wc, bc), lambda: R.linear_torch_cpu(xc[:512], wc, bc))
+        c2[name] = {"M": Mc, "N": n_, "K": k_, "s": round(t_c, 4), "runs": n_c,
+                    "TFLOPs": round(2.0 * Mc * n_ * k_ / t_c / 1e12, 4)}
+        del xc, wc, bc
+    model, flags = _cpu_info()
     return {
         "value": round(value, 4), "unit": "TFLOP/s", "cores": threads, "kind": "port",
         "sample": (f"reference CPU path (torch ops, bf16 F.linear) on the FFN-up shape: W[{N},{K}] qdq x2 "
                    f"(median {tw:.2f}s) and {len(t_slice)} reps of an x[{sample_rows},{K}] slice, qdq + GEMM "
                    f"(median {ts:.3f}s), {total:.1f}s of CPU work; one step at M={M} = W qdq + "
                    f"{M / sample_rows:.2f} slices = {t_full:.2f}s"),
-        "cpu_model": _cpu_model(),
+        "cpu_model": model, "cpu_flags": flags, "os_cpu_count": os.cpu_count(),
+        "affinity_cpus": len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else None,
+        "omp_num_threads": os.environ.get("OMP_NUM_THREADS"),
+        "c1": c1_out, "c2": c2,
     }
 
 
@@ -487,12 +637,12 @@ def main():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--a-format", default="bf16", choices=["tiled", "bf16", "codes"])
     ap.add_argument("--route", default="auto", choices=["auto", "fused", "decode_once"],
                     help="GEMM route for bf16 activations (auto: HIF8Linear's rule, decode_once at this M)")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--shapes", default="up,modln,qkv,block",
-                    help="comma list of up,down,qkvo,ffn,modln,qkv,block (config 4),step (config 5),"
+    ap.add_argument("--shapes", default="up,bwd,modln,qkv,block,step",
+                    help="comma list of up,bwd (the FFN-up backward),down,qkvo,ffn,modln,qkv,block (config 4),"
+                         "step (config 5),"
                          "data (the GEMM with constant operands) to time in addition")
     ap.add_argument("--block-routes", default="fused,reference",
                     help="routes of the block (config 4) to time: fused, reference or both")
@@ -523,11 +673,9 @@ def main():
     torch.cuda.synchronize()
     route = args.route
     if route == "auto":   # HIF8Linear's own choice for bf16 activations (hif8_linear.decode_once)
-        route = "decode_once" if (args.a_format == "bf16" and M >= pkg.hif8_linear.DECODE_ONCE_MIN_ROWS) else "fused"
-    if route == "decode_once" and args.a_format != "bf16":
-        raise SystemExit("--route decode_once takes --a-format bf16")
+        route = "decode_once" if M >= pkg.hif8_linear.DECODE_ONCE_MIN_ROWS else "fused"
     log(f"[bench] timing FFN-up step ({route})")
-    r = time_linear(pkg, torch, x, packed, b, args.steps, args.warmup, args.a_format, route)
+    r = time_linear(pkg, torch, x, packed, b, args.steps, args.warmup, route)
     step_ms = [a + q + d + g for a, q, d, g in zip(r["amax"], r["quant"], r["wdecode"], r["gemm"])]
     ms_step = r["wall_ms"] / args.steps
     flops = 2.0 * M * N * K
@@ -538,10 +686,10 @@ def main():
     wdec_ms = sum(r["wdecode"]) / len(r["wdecode"])
     gemm_tflops = flops / (gemm_ms * 1e-3) / 1e12
     # the other route on the same operands, for comparison
-    other = "fused" if route == "decode_once" else ("decode_once" if args.a_format == "bf16" else None)
+    other = "fused" if route == "decode_once" else "decode_once"
     other_route = None
     if other:
-        ro = time_linear(pkg, torch, x, packed, b, max(3, args.steps // 2), 1, args.a_format, other)
+        ro = time_linear(pkg, torch, x, packed, b, max(3, args.steps // 2), 1, other)
         og = sum(ro["gemm"]) / len(ro["gemm"])
         od = sum(ro["wdecode"]) / len(ro["wdecode"])
         other_route = {"route": other, "gemm_ms": round(og, 4), "wdecode_ms": round(od, 4),
@@ -549,7 +697,7 @@ def main():
                        "kernel": "k_linear_w16" if other == "decode_once" else "k_linear_dtl"}
         del ro
     n = M * K
-    enc_bytes = 5 * n if args.a_format == "codes" else 6 * n   # amax read + quantise read/write
+    enc_bytes = 6 * n   # amax read + fake-quant read/write
     enc_gbps = enc_bytes / ((amax_ms + quant_ms) * 1e-3) / 1e9
 
     # encode (codes) throughput, the bandwidth headline: amax + encode of x
@@ -604,6 +752,12 @@ def main():
     extra_shapes = {}
     if "ffn" in args.shapes.split(","):
         extra_shapes["ffn"] = time_ffn(pkg, torch, x, max(3, args.steps // 2))
+    if "bwd" in args.shapes.split(","):
+        log("[bench] timing the FFN-up backward (dgrad, wgrad)")
+        try:
+            extra_shapes["bwd"] = time_backward(pkg, torch, x, packed, max(3, args.steps // 4))
+        except Exception as ex:
+            extra_shapes["bwd"] = {"error": repr(ex)}
     if "modln" in args.shapes.split(","):
         log("[bench] timing the modulated LayerNorm producer")
         extra_shapes["modln"] = time_modln(pkg, torch, x, max(5, args.steps))
@@ -626,11 +780,11 @@ def main():
         except Exception as ex:
             extra_shapes["step"] = {"error": repr(ex)}
     for name in [s for s in args.shapes.split(",")
-                 if s and s not in ("up", "ffn", "modln", "qkv", "block", "step", "data")]:
+                 if s and s not in ("up", "bwd", "ffn", "modln", "qkv", "block", "step", "data")]:
         n_, k_ = {"down": (5120, 13824), "qkvo": (5120, 5120)}[name]
         xs, ws, bs = make_inputs(torch, M, k_, n_, seed=1)
         ps = pkg.PackedWeight(ws, 15.0)
-        rr = time_linear(pkg, torch, xs, ps, bs, max(3, args.steps // 2), 2, args.a_format, route)
+        rr = time_linear(pkg, torch, xs, ps, bs, max(3, args.steps // 2), 2, route)
         gm = sum(rr["gemm"]) / len(rr["gemm"])
         extra_shapes[name] = {"M": M, "N": n_, "K": k_, "gemm_ms": round(gm, 4),
                               "gemm_TFLOPs": round(2.0 * M * n_ * k_ / (gm * 1e-3) / 1e12, 1),
@@ -666,7 +820,7 @@ def main():
         except Exception as ex:
             cpu = {"error": str(ex)}
 
-    kernel_name = {"tiled": "k_linear_tiled", "codes": "k_linear", "bf16": "k_linear_dtl"}[args.a_format]
+    kernel_name = "k_linear_dtl"
     if route == "decode_once":
         kernel_name = "k_linear_w16"
     gemm_desc = ("weight codes decoded once to bf16 (hif8_decode) -> decode-free HiF8 GEMM (k_linear_w16)"
@@ -686,9 +840,9 @@ def main():
         "data": "synthetic",
         "config": {
             "workload": ("Wan-14B 720P FFN-up HIF8Linear forward: x[75600,5120] bf16 -> amax+scale -> "
-                         f"{'encode' if args.a_format == 'codes' else 'fake-quant'} ({args.a_format}) -> {gemm_desc} "
+                         f"fake-quant (bf16) -> {gemm_desc} "
                          "(W[13824,5120] held as packed 8-bit HiF8, bias) -> y bf16"),
-            "M": M, "K": K, "N": N, "a_format": args.a_format, "route": route, "scale_max": 15.0,
+            "M": M, "K": K, "N": N, "route": route, "scale_max": 15.0,
         },
         "roofline": {
             "kernel": kernel_name,
@@ -697,7 +851,7 @@ def main():
             "peak": PEAK_BF16_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(gemm_tflops / PEAK_BF16_TFLOPS, 4),
-            "traffic": measured_traffic(kernel_name) if args.a_format == "bf16" else None,
+            "traffic": measured_traffic(kernel_name),
             "traffic_source": "profiles/hif8_kernels_14b_720p_hbm_traffic.md (rocprofv3 FETCH_SIZE x2 + WRITE_SIZE)",
             "gemm_ms": round(gemm_ms, 4),
         },

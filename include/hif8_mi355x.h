@@ -54,8 +54,11 @@ enum { HIF8_DTYPE_BF16 = 0, HIF8_DTYPE_F32 = 1, HIF8_DTYPE_BF16_AS_F32 = 2 };
  * (ospnext/modules/attention.py:473,518 and osp_next.py:644): quantising the bf16 tensor
  * directly gives the same x_q without materialising the fp32 copy.  Taken by
  * hif8_absmax_scale, hif8_encode, hif8_fake_quant (y fp32) and hif8_fake_quant_to_bf16. */
-enum { HIF8_SEM_NPU = 0, HIF8_SEM_TORCH = 1 };
-enum { HIF8_A_BF16 = 0, HIF8_A_CODES = 1 };
+enum { HIF8_SEM_NPU = 0, HIF8_SEM_TORCH = 1, HIF8_SEM_TORCH_BF16 = 2 };
+/* HIF8_SEM_TORCH_BF16: QFuncs/hif8.py:6-23 evaluated in bf16 arithmetic, every op rounded to bf16
+ * -- quant_dequant_float(x, QType('hif8'), force_py=True, force_fp32=False) of a bf16 tensor
+ * (QTensor.py:99-102 skipped).  It differs from HIF8_SEM_TORCH only for |x| < 2^-43.  Taken by
+ * hif8_quant_bf16 only. */
 
 /* Text for a status code (static storage). */
 const char *hif8_strerror(int status);
@@ -117,7 +120,8 @@ int hif8_decode(const uint8_t *codes, int64_t n, const void *state, int out_dtyp
  * (ospnext/quant_cy_npu/base/cusrc/npu_quant.cpp:19-33 -> run_hif8_kernel[_bf16],
  * hif8_quant_op.h:208-214).  Unlike the reference, n is 64-bit, every length is
  * handled (no 512-element batches past the end) and semantics is selectable
- * (HIF8_SEM_TORCH gives QFuncs/hif8.py:6-23). */
+ * (HIF8_SEM_TORCH gives QFuncs/hif8.py:6-23 in fp32; hif8_quant_bf16 also takes
+ * HIF8_SEM_TORCH_BF16, the same function in bf16 arithmetic). */
 int hif8_quant_f32(const float *x, float *y, int64_t n, int semantics, hif8_stream_t stream);
 int hif8_quant_bf16(const uint16_t *x, uint16_t *y, int64_t n, int semantics,
                     hif8_stream_t stream);
@@ -125,18 +129,17 @@ int hif8_quant_bf16(const uint16_t *x, uint16_t *y, int64_t n, int semantics,
 /* ---------------------------------------------------------------------------
  * Fused HiF8 linear forward: hif8_linear.py:68-86
  *   y[M,N] = F.linear(x_q, w_q, bias) = x_q @ w_q^T + bias
- * with w_q = decode(w_codes)/scale_w taken from w_state's table, and x_q either
- * bf16 values (a_fmt = HIF8_A_BF16, e.g. from hif8_fake_quant) or HiF8 codes
- * decoded through a_state's table (a_fmt = HIF8_A_CODES; a_state ignored for
- * bf16).  bf16 MFMA, fp32 accumulation, bias added in fp32, bf16 output (RNE).
- *   a: [M,K] row-major; w_codes: [N,K] row-major bytes; bias: [N] bf16 or NULL;
+ * with x_q the bf16 quantised activation (hif8_fake_quant, or hif8_fake_quant_to_bf16 for an
+ * fp32 input) and w_q = decode(w_codes)/scale_w taken from w_state's table: the packed 8-bit
+ * weight is decoded inside the GEMM.  bf16 MFMA, fp32 accumulation, bias added in fp32, bf16
+ * output (RNE).
+ *   a: [M,K] row-major bf16; w_codes: [N,K] row-major bytes; bias: [N] bf16 or NULL;
  *   y: [M,N] row-major bf16.
- * Shapes: K % 64 == 0, N % 8 == 0; M, N, K >= 1 and < 2^31, and K < 2^22 for
- * bf16 activations.  16-byte aligned a, w_codes and y; 8-byte aligned bias.
+ * Shapes: K % 64 == 0, N % 8 == 0; M, N >= 1 and < 2^31, 1 <= K < 2^22.  16-byte aligned
+ * a, w_codes and y; 8-byte aligned bias.
  */
-int hif8_linear_fwd(const void *a, int a_fmt, const void *a_state, const uint8_t *w_codes,
-                    const void *w_state, const uint16_t *bias, uint16_t *y, int64_t M,
-                    int64_t N, int64_t K, hif8_stream_t stream);
+int hif8_linear_fwd(const uint16_t *a, const uint8_t *w_codes, const void *w_state, const uint16_t *bias,
+                    uint16_t *y, int64_t M, int64_t N, int64_t K, hif8_stream_t stream);
 
 /* Several HIF8Linear layers on the same quantised input in one launch: the self-attention
  * q, k, v projections of osp_next.py:742-744 (each an F.linear(x_q, w_q, b) of
@@ -203,38 +206,6 @@ int hif8_rms_norm_rope(const uint16_t *x, const float *weight, const float *cos_
                        hif8_stream_t stream);
 
 /* ---------------------------------------------------------------------------
- * GEMM-native operand layouts and the tiled fused linear (the fast path of
- * hif8_linear.py:68-86).
- *
- * XT (activation x_q, bf16): blocks of 32 rows x 64 k, 4 KB each; block
- *   (rb, ks) at byte (rb*K/64 + ks)*4096; its 1 KB sub-block kk holds at byte
- *   16*l the eight values x_q[32rb + l%32][64ks + 16kk + 8(l/32) + 0..7].
- *   Rows are padded with zeros to hif8_tiled_rows(M).
- * WT (weight codes): the same blocking over [N,K] with one byte per code
- *   (2 KB blocks, 512 B sub-blocks, 8 codes per lane); rows padded with code 0
- *   to hif8_tiled_rows(N).
- */
-
-/* Row count of a tiled buffer: rows rounded up to a multiple of 256. */
-int64_t hif8_tiled_rows(int64_t rows);
-
-/* Fake quant of a row-major [M,K] tensor (scale from state) written as bf16
- * GEMM operands in the XT layout: the x_q of hif8_linear.py:47-48 (for fp32 x,
- * its bf16 autocast rounding).  xt: hif8_tiled_rows(M)*K bf16.  K % 64 == 0. */
-int hif8_fake_quant_tiled(const void *x, int dtype, int64_t M, int64_t K, const void *state, uint16_t *xt,
-                          int semantics, hif8_stream_t stream);
-
-/* Permute row-major [N,K] weight codes into the WT layout (packed 8-bit weight
- * storage of the fused GEMM).  wt: hif8_tiled_rows(N)*K bytes.  K % 64 == 0. */
-int hif8_tile_weight_codes(const uint8_t *codes, int64_t N, int64_t K, uint8_t *wt, hif8_stream_t stream);
-
-/* Fused HiF8 linear on the tiled layouts: y[M,N] = x_q @ w_q^T + bias
- * (hif8_linear.py:86), bf16 MFMA, fp32 accumulation, bf16 output, row-major y.
- * K % 64 == 0, N % 8 == 0; 16-byte aligned xt, wt, y. */
-int hif8_linear_fwd_tiled(const uint16_t *xt, const uint8_t *wt, const void *w_state, const uint16_t *bias,
-                          uint16_t *y, int64_t M, int64_t N, int64_t K, hif8_stream_t stream);
-
-/* ---------------------------------------------------------------------------
  * Backward support.  The reference's dgrad is grad_q @ w_q (hif8_linear.py:97), a
  * product with the weight's [out, in] rows as the reduction dimension.  The fused
  * GEMM reduces over its weight operand's rows, so dgrad runs hif8_linear_fwd on
@@ -243,6 +214,17 @@ int hif8_linear_fwd_tiled(const uint16_t *xt, const uint8_t *wt, const void *w_s
  * it writes out[c][r] = codes[r][c] for a [rows, cols] byte matrix.
  */
 int hif8_transpose_codes(const uint8_t *codes, int64_t rows, int64_t cols, uint8_t *out, hif8_stream_t stream);
+
+/* wgrad support.  The reference's weight gradient is grad_q^T @ x_q over the flattened tokens
+ * (hif8_linear.py:100-105), a product whose reduction runs over the rows of both operands.  The
+ * decode-free GEMM reduces over its operands' rows of contiguous k, so wgrad runs
+ * hif8_linear_fwd_wq(grad_q^T, x_q^T) on the two operands transposed, with the token dimension
+ * padded with zeros to a multiple of 64 (zeros add nothing to the sums).  This entry point writes
+ * out[c][r] = x[r][c] for r < rows and 0 for rows <= r < rows_pad: x bf16 [rows, cols],
+ * out bf16 [cols, rows_pad].  Any shape and alignment; 16-byte aligned pointers, cols % 8 == 0
+ * and rows_pad % 8 == 0 take the vector path.  No counterpart of its own in the reference. */
+int hif8_transpose_bf16(const uint16_t *x, int64_t rows, int64_t cols, int64_t rows_pad, uint16_t *out,
+                        hif8_stream_t stream);
 
 /* ---------------------------------------------------------------------------
  * Producer fusion for the modulated LayerNorm in front of the self-attention q/k/v

@@ -83,6 +83,41 @@ def quant_hif8_torch(x) -> np.ndarray:
     return res.astype(F32)
 
 
+def quant_hif8_torch_bf16(x_bits) -> np.ndarray:
+    """QFuncs/hif8.py:6-23 on a bf16 tensor without ``force_fp32`` (QTensor.py:101-102 not
+    taken): every op computes in float32 and rounds its result to bf16, as torch's bf16 tensor
+    ops do.  bf16 bits in, bf16 bits out.  log2 is evaluated in float64 and rounded straight to
+    bf16 (torch rounds its float32 log2 to bf16; the tests pin that the two agree on every input)."""
+    x = bf16_to_f32(x_bits)
+    rb = lambda v: bf16_to_f32(f32_to_bf16(v))                            # noqa: E731
+    with np.errstate(all="ignore"):
+        xu = np.abs(x)                                                      # :7
+        sign = (x > 0).astype(F32) - (x < 0).astype(F32)                    # :8
+        t = rb(xu + F32(2.0 ** -45))                                        # :13, the sum in bf16
+        lg = np.log2(t.astype(np.float64))
+        e = np.floor(bf16_to_f32(_f64_to_bf16(lg)))                         # :13, log2 then floor
+        abse = np.abs(e)
+        mant_bits = np.zeros_like(abse)
+        mant_bits[abse <= 15] = 1
+        mant_bits[abse <= 7] = 2
+        mant_bits[abse <= 3] = 3
+        m = rb(xu * np.power(F32(2.0), -e + mant_bits))                     # :21
+        f = np.floor(rb(m + F32(0.5)))
+        r = rb(f * np.power(F32(2.0), e - mant_bits))
+        res = rb(r * sign)
+    out = f32_to_bf16(res)
+    out[~np.isfinite(x)] = 0x7FC0
+    return out
+
+
+def _f64_to_bf16(v) -> np.ndarray:
+    """float64 -> bf16 bits, one round-to-nearest-even from the exact value (finite inputs)."""
+    v = np.asarray(v, dtype=np.float64)
+    m, e = np.frexp(v)                                  # v = m 2^e, 0.5 <= |m| < 1
+    r = np.ldexp(np.round(m * 256.0), e - 8)            # 8 significant bits, ties to even
+    return f32_to_bf16(r.astype(F32))
+
+
 # --------------------------------------------------------------- NPU-path qdq
 
 _lib = None

@@ -4,7 +4,8 @@ Imported under the module name ``ospnext_amd`` (the directory name is not a
 Python identifier; see ``__graft_entry__.load_package``).
 
 Public surface, mirroring the reference:
-  QType, quant_dequant_float, quant_func            (ospnext/quant_cy_npu/base/QTensor.py)
+  QType, quant_dequant_float, quant_func,
+  quant_slide_window                                (ospnext/quant_cy_npu/base/QTensor.py)
   hif8_quant, hif8_quant_bf16                       (cusrc/npu_quant.cpp pybind entry points)
   HIF8Linear, _quant, make_linear                   (ospnext/modules/hif8_linear.py, osp_next.py)
   hif8_attention_with_mask, _HIF8QKVQuantFunction   (ospnext/modules/hif8_attention.py)
@@ -15,7 +16,8 @@ plus the tensor-level HIP ops (absmax_scale, encode, fake_quant, decode,
 linear_fwd), QuantState and PackedWeight.
 """
 from . import _lib  # noqa: F401
-from .quant import QType, quant_dequant_float, quant_func, hif8_quant, hif8_quant_bf16  # noqa: F401
+from .quant import (QType, QuantSlideWindow, quant_dequant_float, quant_func, quant_slide_window,  # noqa: F401
+                    hif8_quant, hif8_quant_bf16)
 from .hif8_linear import (  # noqa: F401
     HIF8Linear,
     PackedWeight,
@@ -26,14 +28,10 @@ from .hif8_linear import (  # noqa: F401
     decode,
     encode,
     fake_quant,
-    fake_quant_tiled,
     fake_quant_to_bf16,
     linear_fwd,
-    linear_fwd_tiled,
     make_linear,
     quantize_activation,
-    tile_weight_codes,
-    tiled_rows,
     transpose_codes,
     linear_dgrad,
     dgrad_fused_ok,
@@ -44,6 +42,9 @@ from .hif8_linear import (  # noqa: F401
     grouped_ok,
     linear_fwd_grouped,
     linear_fwd_wq,
+    linear_wgrad,
+    transpose_bf16,
+    wgrad_ok,
 )
 from .ffn import HIF8FFN  # noqa: F401
 from . import dit  # noqa: F401
@@ -68,14 +69,15 @@ from .qlinear import (  # noqa: F401
 )
 
 __all__ = [
-    "QType", "quant_dequant_float", "quant_func", "hif8_quant", "hif8_quant_bf16",
+    "QType", "quant_dequant_float", "quant_func", "quant_slide_window", "QuantSlideWindow", "hif8_quant",
+    "hif8_quant_bf16",
     "HIF8Linear", "PackedWeight", "QuantState", "_quant", "absmax_scale", "decode", "encode",
-    "fake_quant", "fake_quant_to_bf16", "linear_fwd", "make_linear", "quantize_activation", "fake_quant_tiled",
-    "tile_weight_codes", "tiled_rows", "linear_fwd_tiled", "transpose_codes", "linear_dgrad", "dgrad_fused_ok",
+    "fake_quant", "fake_quant_to_bf16", "linear_fwd", "make_linear", "quantize_activation", "transpose_codes",
+    "linear_dgrad", "dgrad_fused_ok",
     "_HIF8QKVQuantFunction", "attention_with_mask", "hif8_attention_with_mask",
     "scaled_dot_product_attention_with_mask", "LinearForward", "LinearForwardFast", "QLinear", "replace_linear",
     "save_packed", "load_packed", "pack_state_dict", "packed_from_codes", "fused_shape_ok", "linear_any",
     "linear_fwd_gelu_amax", "HIF8FFN", "WanLayerNorm", "modulate", "modulated_norm_quant", "affine_norm_quant",
     "qkv_from_modulated_norm", "GroupedWeight", "grouped_ok", "linear_fwd_grouped", "grouped_weight",
-    "dit", "OSPNextAttentionBlock", "OSPNextBlocks", "linear_fwd_wq",
+    "dit", "OSPNextAttentionBlock", "OSPNextBlocks", "linear_fwd_wq", "linear_wgrad", "transpose_bf16", "wgrad_ok",
 ]

@@ -16,7 +16,8 @@ LIB_PATH = os.path.join(_HERE, "libhif8_mi355x.so")
 
 HIF8_OK = 0
 DTYPE_BF16, DTYPE_F32, DTYPE_BF16_AS_F32 = 0, 1, 2
-SEM_NPU, SEM_TORCH = 0, 1
+SEM_NPU, SEM_TORCH, SEM_TORCH_BF16 = 0, 1, 2
+# formats of a quantised activation held by the Python layer: bf16 x_q, or its 8-bit codes
 A_BF16, A_CODES = 0, 1
 
 # Every symbol the header declares, with (restype, argtypes).
@@ -34,12 +35,9 @@ SIGNATURES = {
     "hif8_decode": (_i, [_p, _i64, _p, _i, _p, _p]),
     "hif8_quant_f32": (_i, [_p, _p, _i64, _i, _p]),
     "hif8_quant_bf16": (_i, [_p, _p, _i64, _i, _p]),
-    "hif8_linear_fwd": (_i, [_p, _i, _p, _p, _p, _p, _p, _i64, _i64, _i64, _p]),
-    "hif8_tiled_rows": (_i64, [_i64]),
-    "hif8_fake_quant_tiled": (_i, [_p, _i, _i64, _i64, _p, _p, _i, _p]),
-    "hif8_tile_weight_codes": (_i, [_p, _i64, _i64, _p, _p]),
-    "hif8_linear_fwd_tiled": (_i, [_p, _p, _p, _p, _p, _i64, _i64, _i64, _p]),
+    "hif8_linear_fwd": (_i, [_p, _p, _p, _p, _p, _i64, _i64, _i64, _p]),
     "hif8_transpose_codes": (_i, [_p, _i64, _i64, _p, _p]),
+    "hif8_transpose_bf16": (_i, [_p, _i64, _i64, _i64, _p, _p]),
     "hif8_linear_fwd_gelu_amax": (_i, [_p, _p, _p, _p, _p, _i64, _i64, _i64, _f, _p, _p]),
     "hif8_modln_amax": (_i, [_p, _p, _p, _i64, _i64, _i64, _f, _p, _f, _p, _p]),
     "hif8_linear_fwd_grouped": (_i, [_p, _p, ctypes.POINTER(_p), _p, ctypes.POINTER(_p), ctypes.POINTER(_i64), _i,

@@ -175,8 +175,8 @@ __global__ __launch_bounds__(kTPB) void k_quant(const void *__restrict__ xv, int
     const int tid = threadIdx.x;
     float s = use_state ? st->scale : 1.0f;
     bool fast = use_state ? (st->fast != 0) : true;
-    // NaN inputs map to the Inf entry of the table; unless an amax pass proved
-    // the tensor finite, each 16-element group is checked and patched.
+    // NaN inputs map to the +Inf entry of the table; unless an amax pass proved
+    // the tensor finite, each 16-element group is checked and patched to kNanCode.
     const bool nan_guard = use_state ? (st->finite == 0) : true;
     // decode tables for this scale
     {
@@ -307,7 +307,7 @@ __global__ __launch_bounds__(kTPB) void k_quant(const void *__restrict__ xv, int
                 if (mx > 0x7F80u) {
 #pragma unroll
                     for (int t = 0; t < 16; ++t)
-                        if (wide[t] > 0x7F80u) codes[t >> 2] = (codes[t >> 2] & ~(0xFFu << (8 * (t & 3)))) | (0x80u << (8 * (t & 3)));
+                        if (wide[t] > 0x7F80u) codes[t >> 2] = (codes[t >> 2] & ~(0xFFu << (8 * (t & 3)))) | (kNanCode << (8 * (t & 3)));
                 }
             }
             if (MODE == 0) {
@@ -359,158 +359,37 @@ __global__ __launch_bounds__(kTPB) void k_quant(const void *__restrict__ xv, int
         scalar_elem<DT, MODE>(xv, outv, j, s, sem);
 }
 
-// ------------------------------------------------ GEMM operand layouts
-
-// Activation tile layout of the fused GEMM ("XT"): blocks of 32 rows x 64 k
-// (4 KB of bf16); block (rb, ks) starts at byte (rb * K/64 + ks) * 4096 and its
-// sub-block kk (1 KB) holds, at byte 16*l, lane l's eight values
-//   X[32 rb + (l & 31)][64 ks + 16 kk + 8 (l >> 5) + 0..7],
-// i.e. the B operand of v_mfma_f32_32x32x16_bf16, so a wavefront fetches one
-// operand with a single fully coalesced 1 KB load.  Rows from M up to the padded
-// row count are zero.
-
-// 8 input elements -> 8 bf16 GEMM operands x_q (4 dwords), table route.
-template <int DT>
-__device__ __forceinline__ void quant8_operand(const uint32_t *in, float s, const uint8_t *lds,
-                                               const uint16_t *lut16, bool nan_guard, int sem,
-                                               uint32_t out[4])
+// QFuncs/hif8.py:6-23 evaluated on a bf16 tensor without force_fp32 (quant_dequant_float with
+// force_py=True, force_fp32=False, QTensor.py:99-102,118-119): each torch op on bf16 computes in
+// fp32 and rounds its result to bf16.  bf16 bits in, bf16 bits out.  Roundings that can change
+// the result are those of |x| + 2^-45, of log2 and of x * 2^(mb - e) + 0.5 (below 2^-43 only);
+// the other ops are exact in bf16.  For every bf16 input, log2 of the rounded |x| + 2^-45 lies at
+// least 10 fp32 ulps from a bf16 rounding boundary, so any faithfully rounded log2f gives the
+// bf16 value torch's log2 gives.
+static __device__ uint32_t qdq_torch_bf16(uint32_t xb)
 {
-    uint32_t codes[2], wide[8], full[8];
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-        uint32_t mags = 0, signs;
-        if (DT == kBF16) {
-            uint32_t p0 = in[2 * j], p1 = in[2 * j + 1];
-            uint32_t q01 = f2bf_pk(u2f(p0 << 16) * s, u2f(p0 & 0xFFFF0000u) * s);
-            uint32_t q23 = f2bf_pk(u2f(p1 << 16) * s, u2f(p1 & 0xFFFF0000u) * s);
-            uint32_t u[4] = {q01 & 0x7FFFu, (q01 >> 16) & 0x7FFFu, q23 & 0x7FFFu, (q23 >> 16) & 0x7FFFu};
-#pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                wide[4 * j + t] = u[t];
-                full[4 * j + t] = u[t];
-                mags |= uint32_t(lds[clampu(u[t])]) << (8 * t);
-            }
-            signs = __builtin_amdgcn_perm(p1, p0, 0x07050301u) & 0x80808080u;
-        } else {
-#pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                uint32_t xs = f2u(u2f(in[4 * j + t]) * s);
-                full[4 * j + t] = xs & 0x7FFFFFFFu;
-                uint32_t u = (xs >> 16) & 0x7FFFu;
-                wide[4 * j + t] = u;
-                mags |= uint32_t(lds[clampu(u)]) << (8 * t);
-            }
-            signs = (__builtin_amdgcn_perm(in[4 * j + 3], in[4 * j + 2], 0x07030C0Cu) & 0x80800000u) |
-                    (__builtin_amdgcn_perm(in[4 * j + 1], in[4 * j], 0x0C0C0703u) & 0x00008080u);
-        }
-        codes[j] = apply_signs(mags, signs);
-    }
-    if (nan_guard) {
-#pragma unroll
-        for (int t = 0; t < 8; ++t)
-            if (wide[t] > 0x7F80u) codes[t >> 2] = (codes[t >> 2] & ~(0xFFu << (8 * (t & 3)))) | (0x80u << (8 * (t & 3)));
-    }
-    uint32_t y[8];
-#pragma unroll
-    for (int t = 0; t < 8; ++t) y[t] = lut16[(codes[t >> 2] >> (8 * (t & 3))) & 0xFFu];
-    if (sem == kSemTorch) {
-#pragma unroll
-        for (int t = 0; t < 8; ++t) {
-            uint32_t u = wide[t];
-            if ((full[t] != 0u && u < 0x3480u) || u >= 0x4720u) {
-                // the torch route differs here: redo this element exactly
-                uint32_t yb, code;
-                uint32_t xb = DT == kBF16 ? ((t & 1) ? (in[t >> 1] >> 16) : (in[t >> 1] & 0xFFFFu)) : in[t];
-                slow_elem<DT>(xb, s, kSemTorch, yb, code);
-                y[t] = DT == kBF16 ? yb : f2bf(u2f(yb));
-            }
-        }
-    }
-#pragma unroll
-    for (int t = 0; t < 4; ++t) out[t] = y[2 * t] | (y[2 * t + 1] << 16);
+    const float x = bf2f(xb);
+    const float xu = fabsf(x);
+    if (!(xu <= 3.402823466e38f)) return 0x7FC0u;                  // NaN, Inf -> NaN
+    const float sign = float(x > 0.0f) - float(x < 0.0f);
+    const float t = bf2f(f2bf(xu + 0x1p-45f));                      // x_unsigned + 2**-45
+    const int e = int(__builtin_floorf(bf2f(f2bf(log2f(t)))));     // floor(log2(.))
+    const int ae = e < 0 ? -e : e;
+    const int mb = ae <= 3 ? 3 : ae <= 7 ? 2 : ae <= 15 ? 1 : 0;
+    const float m = bf2f(f2bf(xu * __builtin_ldexpf(1.0f, mb - e)));    // x_unsigned * 2**(-e + mb)
+    const float f = __builtin_floorf(bf2f(f2bf(m + 0.5f)));             // floor(. + 0.5)
+    const float r = bf2f(f2bf(f * __builtin_ldexpf(1.0f, e - mb)));     // * 2**(e - mb)
+    return f2bf(r * sign);                                              // * sign
 }
 
-template <int DT>
-__global__ __launch_bounds__(kTPB) void k_quant_tiled(const void *__restrict__ xv, int M, int K, int Mpad,
-                                                       const State *__restrict__ st, uint8_t *__restrict__ xt,
-                                                       int sem)
+// Unscaled qdq of a bf16 tensor with QFuncs/hif8.py evaluated in bf16 arithmetic (the
+// HIF8_SEM_TORCH_BF16 route of hif8_quant_bf16): elementwise, off the linear's path.
+__global__ __launch_bounds__(kTPB) void k_qdq_torch_bf16(const uint16_t *__restrict__ x, uint16_t *__restrict__ y,
+                                                         int64_t n)
 {
-    __shared__ __attribute__((aligned(16))) uint8_t lds[kLdsBytes];
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    const float s = st->scale;
-    const bool fast = st->fast != 0;
-    const bool nan_guard = st->finite == 0;
-    ((uint16_t *)(lds + kLdsLutBf16))[tid] = st->lut_bf16[tid];
-    {
-        const uint4 *src = (const uint4 *)&kEncTable;
-        uint4 *dst = (uint4 *)(lds + kTabLo);
-        for (uint32_t i = tid; i < sizeof(EncTable) / 16; i += kTPB) dst[i] = src[i];
-    }
-    __syncthreads();
-    const uint16_t *lut16 = (const uint16_t *)(lds + kLdsLutBf16);
-    const int KS = K >> 6;
-    const int64_t nblk = int64_t(Mpad >> 5) * KS;
-    const int64_t stride = int64_t(gridDim.x) * (kTPB / 64);
-    for (int64_t b = int64_t(blockIdx.x) * (kTPB / 64) + wave; b < nblk; b += stride) {
-        const int rb = int(b / KS), ks = int(b - int64_t(rb) * KS);
-        const int row = rb * 32 + (lane & 31);
-        uint8_t *dst = xt + b * 4096 + lane * 16;
-#pragma unroll
-        for (int kk = 0; kk < 4; ++kk) {
-            const int k = ks * 64 + kk * 16 + 8 * (lane >> 5);
-            uint32_t out[4] = {0, 0, 0, 0};
-            if (row < M) {
-                uint32_t in[8];
-                if (DT == kBF16) {
-                    u32x4 v = *(const u32x4 *)((const uint16_t *)xv + size_t(row) * K + k);
-                    in[0] = v.x; in[1] = v.y; in[2] = v.z; in[3] = v.w;
-                } else {
-                    const u32x4 *p = (const u32x4 *)((const float *)xv + size_t(row) * K + k);
-                    u32x4 v0 = p[0], v1 = p[1];
-                    in[0] = v0.x; in[1] = v0.y; in[2] = v0.z; in[3] = v0.w;
-                    in[4] = v1.x; in[5] = v1.y; in[6] = v1.z; in[7] = v1.w;
-                }
-                if (fast) {
-                    quant8_operand<DT>(in, s, lds, lut16, nan_guard, sem, out);
-                } else {
-                    uint32_t y[8];
-#pragma unroll
-                    for (int t = 0; t < 8; ++t) {
-                        uint32_t xb = DT == kBF16 ? ((t & 1) ? (in[t >> 1] >> 16) : (in[t >> 1] & 0xFFFFu)) : in[t];
-                        uint32_t yb, code;
-                        slow_elem<DT>(xb, s, sem, yb, code);
-                        y[t] = DT == kBF16 ? yb : f2bf(u2f(yb));
-                    }
-#pragma unroll
-                    for (int t = 0; t < 4; ++t) out[t] = y[2 * t] | (y[2 * t + 1] << 16);
-                }
-            }
-            *(u32x4 *)(dst + kk * 1024) = u32x4{out[0], out[1], out[2], out[3]};
-        }
-    }
-}
-
-// Weight code tile layout of the fused GEMM ("WT"): blocks of 32 rows x 64 k
-// (2 KB of codes); block (nb, ks) at byte (nb * K/64 + ks) * 2048; sub-block kk
-// (512 B) holds, at byte 8*l, lane l's eight codes
-//   W[32 nb + (l & 31)][64 ks + 16 kk + 8 (l >> 5) + 0..7]
-// -- the A operand of v_mfma_f32_32x32x16_bf16 once decoded.  Rows from N up to
-// the padded row count hold code 0 (value 0).
-__global__ __launch_bounds__(kTPB) void k_tile_wcodes(const uint8_t *__restrict__ codes, int N, int K, int Npad,
-                                                       uint8_t *__restrict__ wt)
-{
-    const int KS = K >> 6;
-    const int64_t ngrp = int64_t(Npad >> 5) * KS * 256;   // 8-code groups
-    for (int64_t g = int64_t(blockIdx.x) * kTPB + threadIdx.x; g < ngrp; g += int64_t(gridDim.x) * kTPB) {
-        const int lane = int(g & 63), kk = int((g >> 6) & 3);
-        const int64_t blk = g >> 8;
-        const int nb = int(blk / KS), ks = int(blk - int64_t(nb) * KS);
-        const int n = nb * 32 + (lane & 31);
-        const int k = ks * 64 + kk * 16 + 8 * (lane >> 5);
-        uint2 v = make_uint2(0u, 0u);
-        if (n < N) v = *(const uint2 *)(codes + size_t(n) * K + k);
-        *(uint2 *)(wt + g * 8) = v;
-    }
+    const int64_t stride = int64_t(gridDim.x) * kTPB;
+    for (int64_t i = int64_t(blockIdx.x) * kTPB + threadIdx.x; i < n; i += stride)
+        y[i] = uint16_t(qdq_torch_bf16(x[i]));
 }
 
 // Byte-matrix transpose, codes [R][C] -> [C][R]: the packed weight W^T that the fused GEMM
@@ -554,6 +433,57 @@ __global__ __launch_bounds__(kTPB) void k_transpose_codes(const uint8_t *__restr
     } else if (orow < C) {
         for (int j = 0; j < 16; ++j)
             if (ocol + j < R) out[orow * R + ocol + j] = uint8_t(o[j >> 2] >> (8 * (j & 3)));
+    }
+}
+
+// bf16 transpose with zero padding, [R][C] -> [C][Rp]: out[c][r] = in[r][c] for r < R and 0 for
+// R <= r < Rp.  The wgrad operands g_q^T and x_q^T (hif8_linear.py:104), with the token
+// dimension padded to the GEMM's k-step.  64 x 64 tiles through LDS; rows of 66 elements put the
+// 8 rows a wavefront reads together in 8 different banks.
+__global__ __launch_bounds__(kTPB) void k_transpose_bf16(const uint16_t *__restrict__ in, int64_t R, int64_t C,
+                                                         int64_t Rp, uint16_t *__restrict__ out, int64_t tiles_c,
+                                                         int vec)
+{
+    __shared__ uint32_t tile[64 * 33];   // 64 rows (r) x 66 bf16 (c), dword-aligned rows
+    uint16_t *t16 = (uint16_t *)tile;
+    const int64_t t = blockIdx.x;
+    const int64_t tr = t / tiles_c, tc = t - tr * tiles_c;
+    const int64_t r0 = tr * 64, c0 = tc * 64;
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        const int ch = tid + kTPB * k;
+        const int rr = ch >> 3, cq = ch & 7;            // tile row, 8-element column chunk
+        const int64_t r = r0 + rr, c = c0 + 8 * cq;
+        uint32_t w[4] = {0u, 0u, 0u, 0u};
+        if (r < R) {
+            if (vec && c + 8 <= C) {
+                const uint4 v = *(const uint4 *)(in + r * C + c);
+                w[0] = v.x; w[1] = v.y; w[2] = v.z; w[3] = v.w;
+            } else {
+                for (int j = 0; j < 8; ++j)
+                    if (c + j < C) w[j >> 1] |= uint32_t(in[r * C + c + j]) << (16 * (j & 1));
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) tile[rr * 33 + 4 * cq + j] = w[j];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+        const int ch = tid + kTPB * k;
+        const int cc = ch >> 3, rq = ch & 7;            // output row (column of in), 8-element chunk of r
+        const int64_t c = c0 + cc, r = r0 + 8 * rq;
+        if (c >= C || r >= Rp) continue;
+        uint32_t w[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            w[j] = uint32_t(t16[(8 * rq + 2 * j) * 66 + cc]) | (uint32_t(t16[(8 * rq + 2 * j + 1) * 66 + cc]) << 16);
+        if (vec && r + 8 <= Rp) {
+            *(uint4 *)(out + c * Rp + r) = make_uint4(w[0], w[1], w[2], w[3]);
+        } else {
+            for (int j = 0; j < 8 && r + j < Rp; ++j) out[c * Rp + r + j] = uint16_t(w[j >> 1] >> (16 * (j & 1)));
+        }
     }
 }
 
@@ -711,41 +641,25 @@ int hif8_quant_f32(const float *x, float *y, int64_t n, int semantics, hif8_stre
 
 int hif8_quant_bf16(const uint16_t *x, uint16_t *y, int64_t n, int semantics, hif8_stream_t stream)
 {
+    if (semantics == HIF8_SEM_TORCH_BF16) {
+        if (!x || !y || n <= 0) return HIF8_ERR_ARG;
+        const int grid = grid_for(n, cu_count() * kQdqWgPerCu);
+        hipLaunchKernelGGL(k_qdq_torch_bf16, dim3(grid), dim3(kTPB), 0, (hipStream_t)stream, x, y, n);
+        return last_launch();
+    }
     return launch_quant(x, HIF8_DTYPE_BF16, n, nullptr, y, 1, semantics, 0, stream);
 }
 
-int64_t hif8_tiled_rows(int64_t rows) { return rows <= 0 ? 0 : ((rows + 255) / 256) * 256; }
-
-int hif8_fake_quant_tiled(const void *x, int dtype, int64_t M, int64_t K, const void *state, uint16_t *xt,
-                          int semantics, hif8_stream_t stream)
+int hif8_transpose_bf16(const uint16_t *x, int64_t rows, int64_t cols, int64_t rows_pad, uint16_t *out,
+                        hif8_stream_t stream)
 {
-    if (!x || !state || !xt || M <= 0 || K <= 0) return HIF8_ERR_ARG;
-    if (dtype != HIF8_DTYPE_BF16 && dtype != HIF8_DTYPE_F32) return HIF8_ERR_ARG;
-    if (semantics != HIF8_SEM_NPU && semantics != HIF8_SEM_TORCH) return HIF8_ERR_ARG;
-    if (K % 64 != 0 || M >= (int64_t(1) << 31) || K >= (int64_t(1) << 31)) return HIF8_ERR_SHAPE;
-    if (!aligned16(x) || !aligned16(xt)) return HIF8_ERR_ALIGN;
-    const int64_t Mpad = hif8_tiled_rows(M);
-    const int64_t blocks = (Mpad / 32) * (K / 64);
-    int grid = grid_for(blocks * 64, cu_count() * 8);
-    hipStream_t s = (hipStream_t)stream;
-    if (dtype == HIF8_DTYPE_BF16)
-        hipLaunchKernelGGL(k_quant_tiled<kBF16>, dim3(grid), dim3(kTPB), 0, s, x, int(M), int(K), int(Mpad),
-                           (const State *)state, (uint8_t *)xt, semantics);
-    else
-        hipLaunchKernelGGL(k_quant_tiled<kF32>, dim3(grid), dim3(kTPB), 0, s, x, int(M), int(K), int(Mpad),
-                           (const State *)state, (uint8_t *)xt, semantics);
-    return last_launch();
-}
-
-int hif8_tile_weight_codes(const uint8_t *codes, int64_t N, int64_t K, uint8_t *wt, hif8_stream_t stream)
-{
-    if (!codes || !wt || N <= 0 || K <= 0) return HIF8_ERR_ARG;
-    if (K % 64 != 0 || N >= (int64_t(1) << 31) || K >= (int64_t(1) << 31)) return HIF8_ERR_SHAPE;
-    if (!aligned16(codes) || !aligned16(wt)) return HIF8_ERR_ALIGN;
-    const int64_t Npad = hif8_tiled_rows(N);
-    int grid = grid_for((Npad / 32) * (K / 64) * 256, cu_count() * 8);
-    hipLaunchKernelGGL(k_tile_wcodes, dim3(grid), dim3(kTPB), 0, (hipStream_t)stream, codes, int(N), int(K),
-                       int(Npad), wt);
+    if (!x || !out || rows <= 0 || cols <= 0 || rows_pad < rows) return HIF8_ERR_ARG;
+    if (rows_pad >= (int64_t(1) << 40) || cols >= (int64_t(1) << 31)) return HIF8_ERR_SHAPE;
+    const int64_t tiles_r = (rows_pad + 63) / 64, tiles_c = (cols + 63) / 64;
+    if (tiles_r * tiles_c >= (int64_t(1) << 31)) return HIF8_ERR_SHAPE;
+    const int vec = (cols % 8 == 0 && rows_pad % 8 == 0 && aligned16(x) && aligned16(out)) ? 1 : 0;
+    hipLaunchKernelGGL(k_transpose_bf16, dim3(unsigned(tiles_r * tiles_c)), dim3(kTPB), 0, (hipStream_t)stream, x,
+                       rows, cols, rows_pad, out, tiles_c, vec);
     return last_launch();
 }
 

@@ -47,13 +47,16 @@ __host__ __device__ constexpr int mant_bits(int e)
 //   otherwise round-half-away to the tapered grid of x's binade.
 // Only the top 16 bits of xb matter (the rounding bit sits at mantissa bit
 // 22-mb >= 19 and every threshold has zero low bits), so the same function
-// serves bf16 and fp32 inputs.  NaN -> 0x80 (the reference kernel's NaN output
-// is an artifact of its select order and is not reproduced).
+// serves bf16 and fp32 inputs.  NaN -> 0xEF (-Inf), as the reference kernel:
+// NaN fails both of its range compares (x < 40960, x > -40960), so its +Inf
+// select and then its -Inf select apply (hif8_quant_op.h:109-110,143-150).
+constexpr uint32_t kNanCode = 0xEFu;
+
 __host__ __device__ constexpr uint32_t encode_npu_bits(uint32_t xb)
 {
     uint32_t s = xb >> 31;
     uint32_t a = xb & 0x7FFFFFFFu;
-    if (a > 0x7F800000u) return 0x80u;
+    if (a > 0x7F800000u) return kNanCode;
     if (a >= 0x47200000u) return s ? 0xEFu : 0x6Fu;       // |x| >= 40960
     int E = int(a >> 23);
     if (E < 104) return 0x00u;                             // |x| < 2^-23, incl. +-0

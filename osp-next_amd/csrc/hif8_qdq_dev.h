@@ -48,6 +48,7 @@ static __device__ float qdq_torch(float x)
 
 __device__ __forceinline__ float qdq_npu(float x) { return u2f(decode_bits(encode_npu_bits(f2u(x)))); }
 
+
 // Scalar reference route for one element: returns the qdq output in the
 // tensor's dtype (bf16 bits in the low half, or fp32 bits) and the code.
 template <int DT>

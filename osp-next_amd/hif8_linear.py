@@ -13,9 +13,11 @@ bit-identical to the reference's; only the fp32 accumulation order differs.
 
 Backward (hif8_linear.py:88-111) quantises the incoming gradient with
 ``scale_max_backward`` through the same HIP kernels.  dgrad ``grad_q @ w_q``
-runs on the fused GEMM against the transposed weight codes when the gradient
-and weight are bf16 (the reference's autocast case); wgrad ``g^T @ x_q`` is a
-plain bf16 product on already-decoded operands and goes to the vendor GEMM.
+runs on the forward's GEMM against the transposed weight codes, and wgrad
+``grad_q^T @ x_q`` on the decode-free GEMM over the two operands transposed
+(token dimension padded to the k-step), when the operands are bf16 (the
+reference's autocast case); other dtypes use torch matmuls on the same
+dequantised operands.
 """
 from __future__ import annotations
 
@@ -148,51 +150,22 @@ def _quant(x: Tensor, scale_max: float, semantics: int = _lib.SEM_NPU) -> Tuple[
     return xq.view(x.shape), st.scale().to(x.dtype)
 
 
-def tiled_rows(rows: int) -> int:
-    return int(_lib.load().hif8_tiled_rows(rows))
-
-
-def fake_quant_tiled(x2: Tensor, state: QuantState, semantics: int = _lib.SEM_NPU) -> Tensor:
-    """x_q of a row-major [M, K] tensor as bf16 GEMM operands in the XT tile layout
-    (flat bf16 buffer of tiled_rows(M) * K elements)."""
-    _lib.require_gpu_tensor(x2, "x")
-    x2 = _aligned(x2)
-    M, K = x2.shape
-    xt = torch.empty(tiled_rows(M) * K, dtype=torch.bfloat16, device=x2.device)
-    _lib.check(_lib.load().hif8_fake_quant_tiled(x2.data_ptr(), _lib.dtype_code(x2.dtype), M, K, state.ptr,
-                                                 xt.data_ptr(), semantics, _lib.stream_ptr(x2.device)),
-               "hif8_fake_quant_tiled")
-    return xt
-
-
-def tile_weight_codes(codes: Tensor) -> Tensor:
-    """Row-major [N, K] codes -> WT tile layout (flat uint8, tiled_rows(N) * K)."""
-    _lib.require_gpu_tensor(codes, "codes")
-    N, K = codes.shape
-    wt = torch.empty(tiled_rows(N) * K, dtype=torch.uint8, device=codes.device)
-    _lib.check(_lib.load().hif8_tile_weight_codes(codes.data_ptr(), N, K, wt.data_ptr(),
-                                                  _lib.stream_ptr(codes.device)), "hif8_tile_weight_codes")
-    return wt
-
-
 # ------------------------------------------------------------ packed weight
 
 
 class PackedWeight:
-    """8-bit HiF8 weight storage: codes [N, K] (uint8) + the weight's state, and the
-    same codes in the fused GEMM's WT tile layout.
+    """8-bit HiF8 weight storage: codes [N, K] (uint8) + the weight's state.
 
     Halves the bytes of a bf16 weight; ``dequantize()`` gives the reference's
     ``w_q`` exactly.
     """
 
-    def __init__(self, weight: Tensor, scale_max: float, tiled: bool = True):
+    def __init__(self, weight: Tensor, scale_max: float):
         w = weight.detach().contiguous()
         self.shape = tuple(w.shape)
         self.src_dtype = w.dtype
         self.state = absmax_scale(w, scale_max, QuantState(w.device))
         self.codes = encode(w, self.state)
-        self.wt = tile_weight_codes(self.codes) if (tiled and w.shape[1] % 64 == 0) else None
         self.scale_max = float(scale_max)
         self.key = (w.data_ptr(), weight._version, w.device)
         self._codes_t: Optional[Tensor] = None
@@ -226,15 +199,48 @@ def dgrad_fused_ok(grad_q: Tensor, w: "PackedWeight") -> bool:
 
 
 def linear_dgrad(grad_q2: Tensor, w: "PackedWeight") -> Tensor:
-    """grad_q [M, N] @ w_q [N, K] -> [M, K] bf16 on the fused GEMM (hif8_linear.py:97)."""
+    """grad_q [M, N] @ w_q [N, K] -> [M, K] bf16 (hif8_linear.py:97): the forward GEMM with the
+    transposed weight codes [K, N] as its weight, on the route the forward takes at this M (the
+    fused GEMM, or the transposed codes decoded once and the decode-free GEMM)."""
     M, N = grad_q2.shape
     K = w.shape[1]
     g = _aligned(grad_q2.contiguous())
+    if decode_once(M):
+        return linear_fwd_wq(g, decode(w.codes_t(), w.state, torch.bfloat16), None)
     y = torch.empty((M, K), dtype=torch.bfloat16, device=g.device)
-    _lib.check(_lib.load().hif8_linear_fwd(g.data_ptr(), _lib.A_BF16, None, w.codes_t().data_ptr(), w.state.ptr,
-                                           None, y.data_ptr(), M, K, N, _lib.stream_ptr(g.device)),
-               "hif8_linear_fwd (dgrad)")
+    _lib.check(_lib.load().hif8_linear_fwd(g.data_ptr(), w.codes_t().data_ptr(), w.state.ptr, None, y.data_ptr(),
+                                           M, K, N, _lib.stream_ptr(g.device)), "hif8_linear_fwd (dgrad)")
     return y
+
+
+def transpose_bf16(x2: Tensor, rows_pad: Optional[int] = None) -> Tensor:
+    """[R, C] bf16 -> [C, rows_pad] bf16 with zeros past R (hif8_transpose_bf16)."""
+    _lib.require_gpu_tensor(x2, "x")
+    if x2.dtype != torch.bfloat16 or x2.dim() != 2:
+        raise ValueError("transpose_bf16 takes a 2-D bfloat16 tensor")
+    R, C = x2.shape
+    rp = R if rows_pad is None else int(rows_pad)
+    out = torch.empty((C, rp), dtype=torch.bfloat16, device=x2.device)
+    _lib.check(_lib.load().hif8_transpose_bf16(x2.data_ptr(), R, C, rp, out.data_ptr(), _lib.stream_ptr(x2.device)),
+               "hif8_transpose_bf16")
+    return out
+
+
+def wgrad_ok(grad_q2: Tensor, x_q2: Tensor) -> bool:
+    """Shapes and dtypes linear_wgrad takes: bf16 operands, in_features a multiple of 8."""
+    return (grad_q2.dtype == torch.bfloat16 and x_q2.dtype == torch.bfloat16 and x_q2.shape[1] % 8 == 0
+            and grad_q2.shape[0] == x_q2.shape[0] and grad_q2.shape[0] > 0)
+
+
+def linear_wgrad(grad_q2: Tensor, x_q2: Tensor) -> Tensor:
+    """grad_weight = grad_q^T [N, M] @ x_q [M, K] -> [N, K] bf16 (hif8_linear.py:100-105, fp32
+    accumulation): both operands transposed with the token dimension padded to a multiple of 64,
+    then the decode-free GEMM, which reduces over the padded tokens (the zeros add nothing)."""
+    M = grad_q2.shape[0]
+    Mp = (M + 63) // 64 * 64
+    g_t = transpose_bf16(grad_q2.contiguous(), Mp)
+    x_t = transpose_bf16(x_q2.contiguous(), Mp)
+    return linear_fwd_wq(g_t, x_t, None)
 
 
 # GEMM route for bf16 activations: "fused" decodes the packed weight inside the GEMM (each
@@ -294,21 +300,28 @@ def linear_any(a: Tensor, a_fmt: int, a_state: Optional[QuantState], w: PackedWe
 
 def linear_fwd(a: Tensor, a_fmt: int, a_state: Optional[QuantState], w: PackedWeight,
                bias: Optional[Tensor]) -> Tensor:
-    """hif8_linear_fwd: y[M,N] = x_q[M,K] @ w_q[N,K]^T + bias, bf16 out (bf16 activations from
-    DECODE_ONCE_MIN_ROWS rows up: the weight decoded once, then hif8_linear_fwd_wq)."""
+    """y[M,N] = x_q[M,K] @ w_q[N,K]^T + bias, bf16 out: hif8_linear_fwd (the fused dequant-GEMM),
+    or from DECODE_ONCE_MIN_ROWS rows up the weight decoded once and hif8_linear_fwd_wq.  An
+    activation given as codes (``a_fmt`` A_CODES, with its ``a_state``) is decoded to its bf16
+    x_q first (bit-exact: decode(encode(x)) is the fake quant of x)."""
     M, K = a.shape
     N = w.shape[0]
     if w.shape[1] != K:
         raise ValueError(f"in_features mismatch: x has {K}, weight has {w.shape[1]}")
-    if a_fmt == _lib.A_BF16 and decode_once(M):
+    if a_fmt == _lib.A_CODES:
+        if a_state is None:
+            raise ValueError("codes activations need their quantisation state")
+        a = decode(a, a_state, torch.bfloat16)
+    elif a_fmt != _lib.A_BF16:
+        raise ValueError(f"unknown activation format {a_fmt}")
+    if decode_once(M):
         return linear_fwd_wq(a, w.dequantize(torch.bfloat16), bias)
     y = torch.empty((M, N), dtype=torch.bfloat16, device=a.device)
-    b_ptr = 0
+    b_ptr = None
     if bias is not None:
         bias = bias.detach().to(torch.bfloat16).contiguous()
         b_ptr = bias.data_ptr()
-    _lib.check(_lib.load().hif8_linear_fwd(a.data_ptr(), a_fmt, a_state.ptr if a_state is not None else None,
-                                           w.codes.data_ptr(), w.state.ptr, b_ptr or None, y.data_ptr(),
+    _lib.check(_lib.load().hif8_linear_fwd(a.data_ptr(), w.codes.data_ptr(), w.state.ptr, b_ptr, y.data_ptr(),
                                            M, N, K, _lib.stream_ptr(a.device)), "hif8_linear_fwd")
     return y
 
@@ -400,21 +413,6 @@ def linear_fwd_gelu_amax(a: Tensor, w: PackedWeight, bias: Optional[Tensor], y_s
     return y
 
 
-def linear_fwd_tiled(xt: Tensor, M: int, w: PackedWeight, bias: Optional[Tensor]) -> Tensor:
-    """hif8_linear_fwd_tiled: the fused GEMM on XT activations and WT codes."""
-    N, K = w.shape
-    if w.wt is None:
-        raise ValueError("packed weight has no tiled codes (K % 64 != 0)")
-    y = torch.empty((M, N), dtype=torch.bfloat16, device=xt.device)
-    b_ptr = None
-    if bias is not None:
-        bias = bias.detach().to(torch.bfloat16).contiguous()
-        b_ptr = bias.data_ptr()
-    _lib.check(_lib.load().hif8_linear_fwd_tiled(xt.data_ptr(), w.wt.data_ptr(), w.state.ptr, b_ptr, y.data_ptr(),
-                                                 M, N, K, _lib.stream_ptr(xt.device)), "hif8_linear_fwd_tiled")
-    return y
-
-
 def quantize_activation(x2: Tensor, scale_max: float, a_format: str, as_f32: bool = False):
     """Quantise a [M,K] activation for the fused GEMM: returns (a, a_fmt, state).  An fp32
     activation (or a bf16 one with ``as_f32``) is quantised in fp32 and handed over as its
@@ -428,24 +426,6 @@ def quantize_activation(x2: Tensor, scale_max: float, a_format: str, as_f32: boo
 
 
 # --------------------------------------------------------------- autograd
-
-
-def hif8_linear_inference(x: Tensor, packed: PackedWeight, bias: Optional[Tensor],
-                          scale_max_forward: float = 15.0) -> Tensor:
-    """Forward without autograd on the tiled fast path: amax+scale, fake quant into
-    the GEMM operand layout, fused dequant-GEMM (three kernels)."""
-    if x.dtype not in (torch.bfloat16, torch.float32):
-        raise TypeError(f"HIF8Linear takes bfloat16 or float32 input, got {x.dtype}")
-    K = x.shape[-1]
-    x2 = x.reshape(-1, K).contiguous()
-    if packed.wt is None or packed.shape[0] % 8 != 0:
-        a, a_fmt, a_st = quantize_activation(x2, scale_max_forward, "bf16")
-        y = linear_any(a, a_fmt, a_st, packed, bias)
-    else:
-        st = absmax_scale(x2, scale_max_forward, QuantState(x2.device))
-        xt = fake_quant_tiled(x2, st)
-        y = linear_fwd_tiled(xt, x2.shape[0], packed, bias)
-    return y.view(*x.shape[:-1], y.shape[-1])
 
 
 def _forward_no_grad(x: Tensor, packed: PackedWeight, bias: Optional[Tensor], scale_max_forward: float,
@@ -502,8 +482,12 @@ class _HIF8LinearFunction(torch.autograd.Function):
             w_q = ctx.packed.dequantize(ctx.w_dtype)
             ct = torch.promote_types(g_2d.dtype, w_q.dtype)
             grad_input = (g_2d.to(ct) @ w_q.to(ct).contiguous()).to(ctx.x_dtype).view(ctx.x_shape)
-        ctw = torch.promote_types(g_2d.dtype, x_q.dtype)                  # :104, g^T @ x_q
-        grad_weight = (g_2d.t().contiguous().to(ctw) @ x_q.to(ctw)).to(ctx.w_dtype)
+        x_2d = x_q.reshape(-1, x_q.shape[-1])
+        if wgrad_ok(g_2d, x_2d):                                            # :104, g^T @ x_q
+            grad_weight = linear_wgrad(g_2d, x_2d).to(ctx.w_dtype)
+        else:
+            ctw = torch.promote_types(g_2d.dtype, x_2d.dtype)
+            grad_weight = (g_2d.t().contiguous().to(ctw) @ x_2d.to(ctw)).to(ctx.w_dtype)
         grad_bias = g_2d.sum(0).to(ctx.b_dtype) if ctx.has_bias else None                   # :107
         return grad_input, grad_weight, grad_bias, None, None, None, None
 
@@ -520,10 +504,10 @@ class HIF8Linear(nn.Linear):
         (inference); without it the packed weight is rebuilt whenever the weight
         tensor changes (version counter or storage), which matches the
         reference's per-call re-quantisation.
-      * ``a_format`` = ``"bf16"`` (default: row-major bf16 x_q and the row-major
-        fused GEMM), ``"tiled"`` (x_q written straight into the tiled GEMM's
-        operand layout, used when no gradient is needed) or ``"codes"`` (8-bit
-        activation codes decoded in the GEMM).
+      * ``a_format`` = ``"bf16"`` (default: the bf16 x_q is the GEMM operand and, with
+        autograd, what the backward keeps) or ``"codes"`` (x_q is held as its 8-bit
+        codes -- half the bytes a training step keeps for the backward -- and decoded
+        to bf16 for the GEMM).
     """
 
     def __init__(self, in_features: int, out_features: int, bias: bool = True,
@@ -561,8 +545,6 @@ class HIF8Linear(nn.Linear):
         grad = torch.is_grad_enabled() and (x.requires_grad or self.weight.requires_grad
                                             or (self.bias is not None and self.bias.requires_grad))
         if not grad:
-            if self.a_format == "tiled":
-                return hif8_linear_inference(x, packed, self.bias, self.scale_max_forward)
             return _forward_no_grad(x, packed, self.bias, self.scale_max_forward, self.a_format)
         return _HIF8LinearFunction.apply(x, self.weight, self.bias, self.scale_max_forward,
                                          self.scale_max_backward, packed, self.a_format)

@@ -172,7 +172,6 @@ def packed_from_codes(codes: Tensor, scale: float, dtype: torch.dtype, scale_max
     _lib.check(_lib.load().hif8_set_scale(pw.state.ptr, _lib.dtype_code(dtype), float(scale),
                                           _lib.stream_ptr(codes.device)), "hif8_set_scale")
     pw.codes = codes.contiguous()
-    pw.wt = None
     pw.scale_max = float(scale_max)
     pw.key = None
     pw._codes_t = None
@@ -213,7 +212,7 @@ def pack_state_dict(state_dict: Dict[str, Tensor], names: List[str], path: str, 
     meta = {"format": FORMAT}
     for name in names:
         w = state_dict[f"{name}.weight"].to(device)
-        packed = PackedWeight(w, scale_max, tiled=False)
+        packed = PackedWeight(w, scale_max)
         _layer_entries(name, packed, state_dict.get(f"{name}.bias"), tensors, meta)
         del w, packed
     save_file(tensors, path, metadata=meta)

@@ -4,6 +4,7 @@
   fields the ``'hif8'`` path reads).
 * ``quant_dequant_float`` -- ``ospnext/quant_cy_npu/base/QTensor.py:94-128``.
 * ``quant_func``          -- ``QTensor.py:131-144`` (straight-through estimator).
+* ``quant_slide_window``  -- ``QTensor.py:147-174`` (qdq outside a trailing window, in place).
 * ``hif8_quant`` / ``hif8_quant_bf16`` -- the pybind entry points
   ``npu_quant.hif8_quant(x, y)`` / ``npu_quant.hif8_quant_bf16(x, y)``
   (``cusrc/npu_quant.cpp:19-39``): in-place into a caller-allocated ``y``.
@@ -79,6 +80,8 @@ def _qdq_inplace(x: Tensor, y: Tensor, semantics: int) -> None:
     s = _lib.stream_ptr(x.device)
     if x.dtype == torch.bfloat16:
         _lib.check(L.hif8_quant_bf16(x.data_ptr(), y.data_ptr(), n, semantics, s), "hif8_quant_bf16")
+    elif semantics == _lib.SEM_TORCH_BF16:
+        raise ValueError("the bf16-arithmetic torch route takes a bfloat16 tensor")
     elif x.dtype == torch.float32:
         _lib.check(L.hif8_quant_f32(x.data_ptr(), y.data_ptr(), n, semantics, s), "hif8_quant_f32")
     else:
@@ -106,16 +109,24 @@ def quant_dequant_float(x: Tensor, Q: QType, force_py: bool = False, force_fp32:
 
     ``force_py=False`` follows the NPU kernel (``hif8_quant_op.h``), ``True`` the
     torch function ``quant_hif8`` (``QFuncs/hif8.py:6-23``).  The output has the
-    input's dtype (QTensor.py:126-127).  bf16 inputs are computed from their
-    exact fp32 values whether or not ``force_fp32`` is set; the reference's
-    bf16-precision torch route (force_py=True, force_fp32=False) is not
-    reproduced.  fp16 and other dtypes go through fp32 like QTensor.py:72-79.
+    input's dtype (QTensor.py:126-127).  The torch function runs in the tensor's
+    own precision unless ``force_fp32`` (QTensor.py:101-102): on a bf16 tensor every
+    op then rounds to bf16 (HIF8_SEM_TORCH_BF16).  The NPU kernel computes in fp32
+    for bf16 and fp32 alike; fp16 and other dtypes go through fp32 like
+    QTensor.py:72-79.  The fp16-precision torch route (force_py=True on an fp16
+    tensor without force_fp32, with its 2^-14 offset) is not implemented and raises.
     """
     if Q.desc in ("fp16", "bf16", "fp32"):
         return x
     if Q.desc != "hif8":
         raise NotImplementedError(f"only the 'hif8' format is implemented, got {Q.desc!r}")
     semantics = _lib.SEM_TORCH if force_py else _lib.SEM_NPU
+    if force_py and not force_fp32:
+        if x.dtype == torch.bfloat16:
+            semantics = _lib.SEM_TORCH_BF16
+        elif x.dtype == torch.float16:
+            raise NotImplementedError("the fp16-precision torch route (force_py=True, force_fp32=False on an "
+                                      "fp16 tensor) is not implemented; pass force_fp32=True")
     dtype_ori = x.dtype
     xc = x.contiguous()
     if xc.dtype not in (torch.bfloat16, torch.float32):
@@ -141,3 +152,40 @@ class QuantFunc(Function):
 
 def quant_func(x: Tensor, Q: QType, force_py: bool = False, force_fp32: bool = False) -> Tensor:
     return QuantFunc.apply(x, Q, force_py, force_fp32)
+
+
+class QuantSlideWindow(Function):
+    """qdq of everything but a trailing window, in place, with a straight-through gradient
+    (QTensor.py:147-167).  ``dim`` -1: the last ``win_size`` columns keep their values; -2: the
+    last ``win_size`` rows of the last two dims; a pair ``(rows, cols)``: the region outside the
+    top-left ``[:-rows, :-cols]`` block keeps its values.  A tensor no larger than the window
+    along a windowed dim is returned unchanged.  ``x`` itself is modified and returned."""
+
+    @staticmethod
+    def forward(ctx, x, Q, force_py, force_fp32, dim, win_size):
+        if isinstance(win_size, (list, tuple)):
+            wr, wc = int(win_size[0]), int(win_size[1])
+            if x.shape[-2] > wr and x.shape[-1] > wc:
+                x[..., :-wr, :-wc] = quant_dequant_float(x[..., :-wr, :-wc], Q, force_py, force_fp32)
+        elif dim == -1:
+            if x.shape[-1] > win_size:
+                x[..., :-win_size] = quant_dequant_float(x[..., :-win_size], Q, force_py, force_fp32)
+        elif dim == -2:
+            if x.shape[-2] > win_size:
+                x[..., :-win_size, :] = quant_dequant_float(x[..., :-win_size, :], Q, force_py, force_fp32)
+        else:
+            raise NotImplementedError(f"quant_slide_window takes qdim -1 or -2, got {dim}")
+        return x
+
+    @staticmethod
+    def backward(ctx, grad):
+        return grad, None, None, None, None, None
+
+
+def quant_slide_window(x: Tensor, Q: QType, force_py: bool = False, force_fp32: bool = False, qdim: int = -2,
+                       win_size=128) -> Tensor:
+    """QTensor.py:170-174: a non-negative ``qdim`` counts from the front (converted to the
+    negative index); the window is kept at full precision, the rest quantised."""
+    if qdim > 0:
+        qdim = qdim - x.dim()
+    return QuantSlideWindow.apply(x, Q, force_py, force_fp32, qdim, win_size)

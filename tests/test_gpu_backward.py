@@ -1,5 +1,6 @@
-"""GPU parity of the backward path (hif8_linear.py:88-111): the code transpose, the fused
-dgrad grad_q @ w_q on the transposed codes, and HIF8Linear's gradients.
+"""GPU parity of the backward path (hif8_linear.py:88-111): the code and bf16 transposes, dgrad
+grad_q @ w_q on the transposed codes, wgrad grad_q^T @ x_q on the decode-free GEMM over the
+transposed operands, and HIF8Linear's gradients.
 
 Oracle: the gradient quantisation is checked bit for bit against the CPU restatement;
 products against fp32 torch on the same (bit-exact) quantised operands, with the
@@ -117,3 +118,54 @@ def test_dgrad_config2_shape(pkg):
     ref = gq[rows].float() @ packed.dequantize().float()
     elem, norm = rel_errors(gx[rows], ref)
     assert elem <= TOL_ELEM and norm <= TOL_NORM, (elem, norm)
+
+
+@pytest.mark.parametrize("R,C,pad", [(1, 8, 0), (17, 33, 47), (64, 64, 0), (100, 300, 28), (513, 1024, 63),
+                                     (75, 8, 5), (640, 48, 0)])
+def test_transpose_bf16(pkg, R, C, pad):
+    """[R, C] -> [C, R + pad] with zero columns past R; misaligned sizes take the scalar path."""
+    g = torch.Generator(device="cpu").manual_seed(R + C + pad)
+    x = torch.randn(R, C, generator=g).to(torch.bfloat16)
+    out = pkg.transpose_bf16(x.to(DEV), R + pad)
+    want = torch.zeros(C, R + pad, dtype=torch.bfloat16)
+    want[:, :R] = x.t()
+    assert torch.equal(out.cpu().view(torch.int16), want.view(torch.int16))
+
+
+def wgrad_bound(gq, xq, got):
+    """Every element of grad_q^T @ x_q within one bf16 unit (2^-7 relative) plus 2^-16 of
+    sum |g||x| of the fp64 product (fp32 accumulation over the tokens); a wrong row, column or
+    token index gives errors of the order of the values themselves."""
+    ref = gq.double().t() @ xq.double()
+    tol = ref.abs() * 2.0 ** -7 + (gq.double().abs().t() @ xq.double().abs()) * 2.0 ** -16
+    err = (got.double() - ref).abs()
+    assert bool((err <= tol).all()), float((err / tol).max())
+
+
+@pytest.mark.parametrize("M,N,K", [(64, 256, 256), (300, 320, 264), (1000, 1536, 1536), (4100, 520, 8),
+                                   (65, 8, 64), (2049, 5120, 1024)])
+def test_wgrad_vs_fp64(pkg, M, N, K):
+    """grad_q^T [N, M] @ x_q [M, K] with M padded to the k-step inside (M % 64 != 0 included)."""
+    print(f"[wgrad] M={M} N={N} K={K}", flush=True)
+    g = torch.Generator(device="cpu").manual_seed(M * 3 + N + K)
+    gy = torch.randn(M, N, generator=g).to(torch.bfloat16).to(DEV)
+    x = torch.randn(M, K, generator=g).to(torch.bfloat16).to(DEV)
+    gq, _ = pkg._quant(gy, 224.0)
+    xq, _ = pkg._quant(x, 15.0)
+    assert pkg.wgrad_ok(gq, xq)
+    gw = pkg.linear_wgrad(gq, xq)
+    assert gw.shape == (N, K) and gw.dtype == torch.bfloat16
+    wgrad_bound(gq, xq, gw)
+
+
+def test_wgrad_config3_full_size_rows(pkg):
+    """Wan-14B 720P FFN up backward: grad [75600, 13824], x_q [75600, 5120] (1182 k-steps of 64
+    tokens, the last one padded), sampled output rows against fp64."""
+    M, N, K = 75600, 13824, 5120
+    print(f"[wgrad] full size M={M} N={N} K={K}", flush=True)
+    g = torch.Generator(device=DEV).manual_seed(8)
+    gq, _ = pkg._quant(torch.randn(M, N, generator=g, device=DEV).to(torch.bfloat16), 224.0)
+    xq, _ = pkg._quant(torch.randn(M, K, generator=g, device=DEV).to(torch.bfloat16), 15.0)
+    gw = pkg.linear_wgrad(gq, xq)
+    rows = torch.cat([torch.randint(0, N, (48,), generator=g, device=DEV), torch.arange(N - 16, N, device=DEV)])
+    wgrad_bound(gq[:, rows], xq, gw[rows])

@@ -58,15 +58,35 @@ def test_raw_qdq_every_bf16(pkg, golden):
     y = torch.empty_like(x)
     pkg.hif8_quant_bf16(x, y)
     got = host_bits(y)
-    assert np.array_equal(got[~nan], ex["npu_qdq"][~nan])
-    assert np.all((got[nan] & 0x7FFF) > 0x7F80)           # NaN stays NaN (documented deviation)
+    assert np.array_equal(got, ex["npu_qdq"])              # NaN included: -Inf, as the Ascend kernel
+    assert np.all(got[nan] == 0xFF80)
     yt = pkg.quant_dequant_float(x, pkg.QType("hif8"), force_py=True, force_fp32=True)
     assert np.array_equal(host_bits(yt), ex["torch_qdq"])
     # fp32 drop-in on the same values
     xf = x.float()
     y32 = torch.empty_like(xf)
     pkg.hif8_quant(xf, y32)
-    assert np.array_equal(host_bits(y32.to(torch.bfloat16))[~nan], ex["npu_qdq"][~nan])
+    assert np.array_equal(host_bits(y32.to(torch.bfloat16)), ex["npu_qdq"])
+
+
+def test_torch_bf16_route_every_bf16(pkg, R, golden):
+    """quant_dequant_float(bf16, force_py=True) without force_fp32 runs QFuncs/hif8.py in bf16
+    arithmetic (HIF8_SEM_TORCH_BF16), every bf16 input against the oracle; with force_fp32 it
+    is the fp32 route of the fixture."""
+    x = dev_bf16(ALL_BF16)
+    want = R.quant_hif8_torch_bf16(ALL_BF16)
+    got = host_bits(pkg.quant_dequant_float(x, pkg.QType("hif8"), force_py=True))
+    fin = np.isfinite(R.bf16_to_f32(ALL_BF16))
+    assert np.array_equal(got[fin], want[fin])
+    assert np.all((got[~fin] & 0x7FFF) > 0x7F80)
+    y = torch.empty_like(x)
+    pkg._lib.check(pkg._lib.load().hif8_quant_bf16(x.data_ptr(), y.data_ptr(), x.numel(), pkg._lib.SEM_TORCH_BF16,
+                                                   pkg._lib.stream_ptr(x.device)), "hif8_quant_bf16")
+    assert np.array_equal(host_bits(y), got)
+    yt = pkg.quant_dequant_float(x, pkg.QType("hif8"), force_py=True, force_fp32=True)
+    assert np.array_equal(host_bits(yt), golden["ex"]["torch_qdq"])
+    with pytest.raises(NotImplementedError):
+        pkg.quant_dequant_float(x.half(), pkg.QType("hif8"), force_py=True)
 
 
 def test_codes_every_bf16_unit_scale(pkg, golden):
@@ -149,20 +169,14 @@ def test_edge_tensors(pkg, R):
 
 def test_nonfinite_tensors_take_the_exact_route(pkg, R):
     """Inf/NaN in the tensor make amax non-finite and the scale 0 or NaN; every
-    element then follows the reference's arithmetic one by one.  One deliberate
-    deviation: where the scaled value is NaN, the NPU kernel's select order
-    (hif8_quant_op.h:143-150) yields -Inf; these kernels keep NaN."""
+    element then follows the reference's arithmetic one by one, including the NPU
+    kernel's -Inf for a NaN scaled value (hif8_quant_op.h:143-150)."""
     for special in (0x7F80, 0xFF80, 0x7FC0):
         xb = np.concatenate([R.f32_to_bf16(np.linspace(-2, 2, 1000).astype(np.float32)), [special]]).astype(np.uint16)
         x = dev_bf16(xb)
         st = pkg.absmax_scale(x, 15.0, pkg.QuantState(x.device))
-        s_bits = R.hif8_scale_bf16(R.absmax_bf16(xb), 15.0)
-        with np.errstate(all="ignore"):
-            xs_nan = np.isnan(R.bf16_to_f32(xb) * R.bf16_to_f32(np.array([s_bits], np.uint16))[0])
         for sem, sname in ((0, "npu"), (1, "torch")):
             want, _ = R.quant_bf16(xb, 15.0, sname)
-            if sname == "npu":
-                want = np.where(xs_nan, np.uint16(0x7FC0), want)
             got = host_bits(pkg.fake_quant(x, st, sem))
             wn = (want & 0x7FFF) > 0x7F80
             gn = (got & 0x7FFF) > 0x7F80

@@ -1,0 +1,336 @@
+"""GPU correctness at the full BASELINE workloads.
+
+- Config 3 (Wan-14B 720P linears, x [75600, K]): FFN-down [13824 -> 5120] and the
+  q/k/v/o shape [5120 -> 5120] on HIF8Linear's default route for that M (the weight decoded
+  once, then the decode-free GEMM) and on the fused dequant-GEMM: the two routes equal bit for
+  bit on the whole output, sampled rows of the output against fp32 torch on the same
+  operands, and sampled x_q and w_q rows bit-exact against the oracle under the full tensors'
+  scales (FFN-up at this size is in test_gpu_linear.py).
+- Config 4 (one 14B block at 720P: dim 5120, 40 heads, grid 21x45x80 padded to 48, text 512,
+  osp_next.py:926-957): every linear of both routes is intercepted where it runs; each x_q is
+  checked against the oracle on sampled rows with the full tensor's scale and, for the fused
+  producers, against the standalone _quant of the producer's own output on the whole tensor;
+  each GEMM's output rows against fp32 torch; the two routes' block outputs agree within the
+  block tolerance of tests/test_dit_cpu.py and are finite.
+- Config 5 (the 40-block 14B step at 768P, osp_next.py:1287-1331): the fused step's output
+  is finite, and the fused and reference-order routes agree on one full and one skiparse
+  block at that size.
+"""
+from __future__ import annotations
+
+import pytest
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+import numpy as np  # noqa: E402
+
+import workload_checks as W  # noqa: E402
+from test_dit_cpu import TOL_HIF8, block_errors  # noqa: E402
+
+DEV = "cuda:0"
+
+
+def _route(pkg, name):
+    class _Ctx:
+        def __enter__(self):
+            self.old = pkg.hif8_linear.GEMM_ROUTE
+            pkg.hif8_linear.GEMM_ROUTE = name
+
+        def __exit__(self, *exc):
+            pkg.hif8_linear.GEMM_ROUTE = self.old
+    return _Ctx()
+
+
+def _config3_operands(M, K, N, seed):
+    g = torch.Generator(device=DEV).manual_seed(seed)
+    x = torch.randn(M, K, generator=g, device=DEV)
+    ch = torch.randperm(K, generator=g, device=DEV)[:16]
+    x[:, ch] *= 20
+    x = x.to(torch.bfloat16)
+    w = (torch.randn(N, K, generator=g, device=DEV) * 0.02).to(torch.bfloat16)
+    b = (torch.randn(N, generator=g, device=DEV) * 0.1).to(torch.bfloat16)
+    return x, w, b
+
+
+@pytest.mark.parametrize("name,N,K", [("ffn_down", 5120, 13824), ("qkvo", 5120, 5120)])
+def test_config3_full_size_both_routes(pkg, R, name, N, K):
+    M = 75600
+    print(f"[config3] {name} M={M} K={K} N={N}", flush=True)
+    x, w, b = _config3_operands(M, K, N, seed=31 + N + K)
+    packed = pkg.PackedWeight(w, 15.0)
+    a, fmt, st = pkg.quantize_activation(x, 15.0, "bf16")
+    assert pkg.hif8_linear.decode_once(M)          # the default route at this M
+    y_auto = pkg.linear_fwd(a, fmt, st, packed, b)
+    with _route(pkg, "fused"):
+        y_fused = pkg.linear_fwd(a, fmt, st, packed, b)
+    torch.cuda.synchronize()
+    # the same MFMA products in the same order: identical bits on the whole output
+    assert torch.equal(y_auto.view(torch.int16), y_fused.view(torch.int16))
+    assert bool(torch.isfinite(y_auto).all())
+    rows = W.sample_rows(M, seed=N + K)
+    w_q = packed.dequantize()
+    W.check_linear_rows(a, w_q, b, y_auto, rows)
+    # operands: x_q and w_q rows bit-exact against the oracle under the full tensors' scales
+    W.check_xq_rows(R, x, a, st, 15.0, rows)
+    W.check_xq_rows(R, w, w_q, packed.state, 15.0, W.sample_rows(N, seed=K, n=64, tail=16))
+    # the layer itself (autograd off) takes the same route and gives the same bits
+    lin = pkg.HIF8Linear(K, N, bias=True, device=DEV, dtype=torch.bfloat16)
+    with torch.no_grad():
+        lin.weight.copy_(w)
+        lin.bias.copy_(b)
+        y_mod = lin(x)
+    assert torch.equal(y_mod.view(torch.int16), y_auto.view(torch.int16))
+
+
+# ----------------------------------------------------------------------- config 4
+
+
+class BlockProbe:
+    """Intercepts the functions through which a DiT block's linears and their producers run
+    and checks each call (see the module docstring).  ``calls`` counts the sites visited."""
+
+    def __init__(self, pkg, R, monkeypatch, seed):
+        self.pkg, self.R, self.seed = pkg, R, seed
+        self.calls = {}
+        self.errors = []
+        from ospnext_amd import dit, ffn, hif8_linear, norm
+        self.mods = dict(dit=dit, ffn=ffn, hif8_linear=hif8_linear, norm=norm)
+        hl = hif8_linear
+        wrap_mn = self._modln(norm.modulated_norm_quant)
+        monkeypatch.setattr(norm, "modulated_norm_quant", wrap_mn)
+        monkeypatch.setattr(dit, "modulated_norm_quant", wrap_mn)
+        monkeypatch.setattr(dit, "affine_norm_quant", self._affine(dit.affine_norm_quant))
+        wrap_g = self._grouped(hl.linear_fwd_grouped)
+        monkeypatch.setattr(norm, "linear_fwd_grouped", wrap_g)
+        monkeypatch.setattr(dit, "linear_fwd_grouped", wrap_g)
+        wrap_any = self._linear_any(hl.linear_any)
+        monkeypatch.setattr(hl, "linear_any", wrap_any)
+        monkeypatch.setattr(ffn, "linear_any", wrap_any)
+        monkeypatch.setattr(ffn, "linear_fwd_gelu_amax", self._gelu(hl.linear_fwd_gelu_amax))
+        monkeypatch.setattr(ffn, "fake_quant", self._down_quant(hl.fake_quant))
+        monkeypatch.setattr(dit, "fake_quant", self._text_quant(dit.fake_quant))
+        wrap_q = self._qact(hl.quantize_activation)
+        monkeypatch.setattr(hl, "quantize_activation", wrap_q)
+        monkeypatch.setattr(ffn, "quantize_activation", wrap_q)
+
+    def _hit(self, site):
+        self.calls[site] = self.calls.get(site, 0) + 1
+        print(f"[config4]   {site}", flush=True)
+
+    def _rows(self, M):
+        return W.sample_rows(M, seed=self.seed + sum(self.calls.values()))
+
+    def _modln(self, orig):
+        def wrapped(x, shift=None, scale=None, eps=1e-6, scale_max=15.0, semantics=0, return_y=False):
+            xq, st, y = orig(x, shift, scale, eps, scale_max, semantics, return_y=True)
+            self._hit("modulated_norm_quant")
+            ref_y = self.pkg.modulate(self.pkg.WanLayerNorm(x.shape[-1], eps).to(x.device)(x), shift, scale)
+            self._check_y(y, ref_y, shift)
+            self._check_producer(xq, st, y, scale_max)
+            return (xq, st, y) if return_y else (xq, st)
+        return wrapped
+
+    def _affine(self, orig):
+        def wrapped(x, norm, scale_max=15.0, semantics=0, return_y=False):
+            xq, st, y = orig(x, norm, scale_max, semantics, return_y=True)
+            self._hit("affine_norm_quant")
+            self._check_y(y, norm(x), norm.bias.detach())
+            self._check_producer(xq, st, y, scale_max)
+            return (xq, st, y) if return_y else (xq, st)
+        return wrapped
+
+    def _check_y(self, y, ref_y, shift=None):
+        """The producer's y against torch's fp32 layer norm (+ bf16 modulation): equal except next
+        to a bf16 rounding boundary (fewer than 1e-3 of the elements), and there within one bf16
+        unit of the product n * (1 + scale) (or w * n) plus one of y, together below 2^-6 of
+        |y| + |shift| (``shift``: the modulation shift, or the affine norm's bias, which y can
+        cancel down to a small value)."""
+        ref_y = ref_y.reshape(y.shape)
+        d = (y.float() - ref_y.float()).abs()
+        frac = float((d != 0).float().mean())
+        mag = ref_y.float().abs()
+        if shift is not None:
+            mag = mag + shift.float().abs().reshape(1, 1, -1)
+        assert frac < 1e-3, frac
+        assert bool((d <= mag * 2.0 ** -6).all()), float((d / mag.clamp(min=1e-30)).max())
+
+    def _check_producer(self, xq, st, y, scale_max):
+        xq_std, st_std = W.standalone_quant(self.pkg, y, scale_max)
+        assert torch.equal(xq.reshape(-1).view(torch.int16), xq_std.reshape(-1).view(torch.int16))
+        assert st.read()[1] == st_std.read()[1]
+        W.check_xq_rows(self.R, y, xq, st, scale_max, self._rows(y.numel() // y.shape[-1]))
+
+    def _grouped(self, orig):
+        def wrapped(a, gw):
+            ys = orig(a, gw)
+            self._hit(f"linear_fwd_grouped[{len(ys)}]")
+            rows = self._rows(a.shape[0])
+            for p, y, i in zip(gw.packs, ys, range(len(ys))):
+                b = None
+                if gw.bias is not None:
+                    off = sum(gw.ns[:i])
+                    b = gw.bias[off:off + gw.ns[i]]
+                W.check_linear_rows(a, p.dequantize(torch.bfloat16), b, y, rows)
+            return ys
+        return wrapped
+
+    def _linear_any(self, orig):
+        def wrapped(a, a_fmt, a_state, w, bias):
+            y = orig(a, a_fmt, a_state, w, bias)
+            self._hit("linear_any")
+            assert a_fmt == self.pkg._lib.A_BF16
+            W.check_linear_rows(a, w.dequantize(torch.bfloat16), bias, y, self._rows(a.shape[0]))
+            return y
+        return wrapped
+
+    def _gelu(self, orig):
+        def wrapped(a, w, bias, y_state, scale_max):
+            y = orig(a, w, bias, y_state, scale_max)
+            self._hit("linear_fwd_gelu_amax")
+            W.check_linear_rows(a, w.dequantize(torch.bfloat16), bias, y, self._rows(a.shape[0]), gelu=True)
+            # the epilogue's amax fold gives the scale the standalone amax pass gives for y
+            _, st_std = W.standalone_quant(self.pkg, y, scale_max)
+            assert y_state.read()[1] == st_std.read()[1]
+            return y
+        return wrapped
+
+    def _down_quant(self, orig):
+        def wrapped(y, state, semantics=0):
+            yq = orig(y, state, semantics)
+            self._hit("ffn_down_quant")
+            xq_std, _ = W.standalone_quant(self.pkg, y, 15.0)
+            assert torch.equal(yq.reshape(-1).view(torch.int16), xq_std.reshape(-1).view(torch.int16))
+            W.check_xq_rows(self.R, y, yq, state, 15.0, self._rows(y.shape[0]))
+            return yq
+        return wrapped
+
+    def _text_quant(self, orig):
+        def wrapped(t2, state, semantics=0):
+            tq = orig(t2, state, semantics)
+            self._hit("text_quant")
+            W.check_xq_rows(self.R, t2, tq, state, 15.0, self._rows(t2.shape[0]))
+            return tq
+        return wrapped
+
+    def _qact(self, orig):
+        def wrapped(x2, scale_max, a_format, as_f32=False):
+            a, fmt, st = orig(x2, scale_max, a_format, as_f32)
+            self._hit("quantize_activation" + ("[f32]" if (as_f32 or x2.dtype == torch.float32) else ""))
+            W.check_xq_rows(self.R, x2, a, st, scale_max, self._rows(x2.shape[0]), as_f32=as_f32)
+            if as_f32:
+                # the bf16 attention output quantised as its fp32 copy: the fp32 _quant, then the cast
+                xq32, _ = W.standalone_quant(self.pkg, x2.float(), scale_max)
+                assert torch.equal(a.view(torch.int16), xq32.to(torch.bfloat16).view(torch.int16))
+            return a, fmt, st
+        return wrapped
+
+
+def _block_720p(pkg):
+    D = pkg.dit
+    dim, ffn, heads, grid, L = 5120, 13824, 40, (21, 45, 80), 512
+    torch.manual_seed(4)
+    blk = D.OSPNextAttentionBlock(dim, ffn, heads, cross_attn_norm=True, sparse_ratio=2,
+                                  skiparse_block_type="token", is_full2skiparse_block=True, quant="hif8",
+                                  device=DEV)
+    g = torch.Generator(device=DEV).manual_seed(4)
+    D.init_block_weights(blk, 0.02, g)
+    with torch.no_grad():
+        for n, p in blk.named_parameters():
+            if n.endswith("bias"):
+                p.normal_(0.0, 0.02, generator=g)
+            elif "norm" in n:
+                p.copy_(1 + 0.1 * torch.randn(p.shape, generator=g, device=DEV))
+    for m in blk.modules():
+        if isinstance(m, pkg.HIF8Linear):
+            m.prepack()
+    T, H, W_ = grid
+    x = torch.randn(1, T * H * W_, dim, generator=g, device=DEV).to(torch.bfloat16)
+    e = torch.randn(1, 6, dim, generator=g, device=DEV).to(torch.bfloat16)
+    text = torch.randn(1, L, dim, generator=g, device=DEV).to(torch.bfloat16)
+    return blk, x, e, text, grid
+
+
+def test_config4_block_720p_every_linear(pkg, R, monkeypatch):
+    D = pkg.dit
+    print("[config4] building the 14B block at 720P", flush=True)
+    blk, x, e, text, grid = _block_720p(pkg)
+    rope = D.SkiparseRopeWrapper(D.rope_freqs(128).to(DEV))
+    tm, _ = D.skiparse_masks(1, grid, 2, DEV)
+    assert tm is not None and tm.shape == (4, 20160)       # H 45 padded to 48
+    probe = BlockProbe(pkg, R, monkeypatch, seed=44)
+    outs = {}
+    for fused in (True, False):
+        probe.calls = {}
+        print(f"[config4] route fused={fused}", flush=True)
+        with torch.no_grad():
+            y = blk(x, tm, tm, e, grid, grid, rope, text, fused=fused)
+        torch.cuda.synchronize()
+        assert y.shape == (4, 20160, 5120) and y.dtype == torch.bfloat16
+        assert bool(torch.isfinite(y).all())
+        outs[fused] = y
+        print(f"[config4] fused={fused} sites {probe.calls}", flush=True)
+        if fused:
+            assert probe.calls == {"modulated_norm_quant": 2, "linear_fwd_grouped[3]": 1, "quantize_activation[f32]": 1,
+                                   "linear_any": 4, "linear_fwd_grouped[2]": 1, "text_quant": 1,
+                                   "affine_norm_quant": 1, "quantize_activation": 1, "linear_fwd_gelu_amax": 1,
+                                   "ffn_down_quant": 1}, probe.calls
+        else:
+            # q, k, v, o (fp32 input), cross q, k, v, o, FFN up: each quantises its own input
+            assert probe.calls.get("quantize_activation", 0) + probe.calls.get("quantize_activation[f32]", 0) == 9
+            assert probe.calls["quantize_activation[f32]"] == 1
+            assert probe.calls["linear_fwd_gelu_amax"] == 1 and probe.calls["ffn_down_quant"] == 1
+    x_ref = D.SkiparseRearrange(2, D.RearrangeType.Skiparse2DToken)(x, grid)
+    nw, mx = block_errors(outs[True], outs[False], x_ref)
+    frac = float((outs[True].view(torch.int16) != outs[False].view(torch.int16)).float().mean())
+    print(f"[config4] routes: normwise {nw:.3e} max {mx:.3e}, {frac:.4%} of outputs differ", flush=True)
+    assert nw < TOL_HIF8[0] and mx < TOL_HIF8[1], (nw, mx)
+
+
+# ----------------------------------------------------------------------- config 5
+
+
+def test_config5_step_768p(pkg):
+    D = pkg.dit
+    dim, ffn, heads, grid, L, text_dim = 5120, 13824, 40, (21, 48, 84), 512, 4096
+    print("[config5] building the 40-block 14B stack", flush=True)
+    torch.manual_seed(5)
+    stack = D.OSPNextBlocks(dim, ffn, heads, num_layers=40, num_full_blocks=8, quant="hif8", device=DEV)
+    g = torch.Generator(device=DEV).manual_seed(5)
+    D.init_block_weights(stack, 0.02, g)
+    for m in stack.modules():
+        if isinstance(m, pkg.HIF8Linear):
+            m.prepack(drop_weight=True)
+    torch.cuda.empty_cache()
+    emb = torch.nn.Sequential(torch.nn.Linear(text_dim, dim), torch.nn.GELU(approximate="tanh"),
+                              torch.nn.Linear(dim, dim)).to(DEV, torch.bfloat16)
+    D.init_block_weights(emb, 0.02, g)
+    T, H, W_ = grid
+    x = torch.randn(1, T * H * W_, dim, generator=g, device=DEV).to(torch.bfloat16)
+    e = torch.randn(1, 6, dim, generator=g, device=DEV).to(torch.bfloat16)
+    text_in = torch.randn(1, L, text_dim, generator=g, device=DEV).to(torch.bfloat16)
+    with torch.no_grad():
+        text = emb(text_in)
+        print("[config5] the fused 40-block step", flush=True)
+        y = stack(x, e, text, grid)
+        torch.cuda.synchronize()
+        assert y.shape == x.shape and bool(torch.isfinite(y).all())
+        assert float((y.float() - x.float()).norm()) > 0
+        # route agreement at 768P on the first full block and the first skiparse block
+        rope = stack.rope
+        tm, gm = D.skiparse_masks(1, grid, 2, DEV)
+        assert tm is None and gm is None                 # 48 and 84 are multiples of 4: no padding
+        for i in (0, 4):
+            blk = stack.blocks[i]
+            kind = blk.skiparse_block_type
+            print(f"[config5] block {i} ({kind}) routes", flush=True)
+            outs = [blk(x, None, None, e, grid, grid, rope, text, fused=f) for f in (True, False)]
+            torch.cuda.synchronize()
+            x_ref = x if kind == "full" else D.SkiparseRearrange(2, D.RearrangeType.Skiparse2DToken)(x, grid)
+            assert outs[0].shape == x_ref.shape
+            for o in outs:
+                assert bool(torch.isfinite(o).all())
+            nw, mx = block_errors(outs[0], outs[1], x_ref)
+            frac = float((outs[0].view(torch.int16) != outs[1].view(torch.int16)).float().mean())
+            print(f"[config5] block {i}: normwise {nw:.3e} max {mx:.3e}, {frac:.4%} of outputs differ", flush=True)
+            assert nw < TOL_HIF8[0] and mx < TOL_HIF8[1], (i, nw, mx)

@@ -55,15 +55,13 @@ def test_status_codes_without_gpu(pkg):
     assert L.hif8_fake_quant(fake, 0, 16, fake, odd, 0, None) == -3
     assert L.hif8_quant_bf16(None, fake, 16, 0, None) == -1
     assert L.hif8_decode(fake, -1, fake, 0, fake, None) == -1
-    # linear: bad format, missing state, K % 64, N % 8, alignment
-    args = dict(a=fake, fmt=0, ast=None, w=fake, wst=fake, b=None, y=fake, M=128, N=256, K=512)
+    # linear: missing pointers, K % 64, N % 8, alignment
+    args = dict(a=fake, w=fake, wst=fake, b=None, y=fake, M=128, N=256, K=512)
 
     def lin(**kw):
         a = {**args, **kw}
-        return L.hif8_linear_fwd(a["a"], a["fmt"], a["ast"], a["w"], a["wst"], a["b"], a["y"], a["M"], a["N"],
-                                 a["K"], None)
-    assert lin(fmt=3) == -1
-    assert lin(fmt=1) == -1
+        return L.hif8_linear_fwd(a["a"], a["w"], a["wst"], a["b"], a["y"], a["M"], a["N"], a["K"], None)
+    assert lin(a=None) == -1
     assert lin(wst=None) == -1
     assert lin(M=0) == -1
     assert lin(K=100) == -2
@@ -138,8 +136,8 @@ def test_device_encoder_matches_oracle_every_bf16(hostlib, R):
     xf = (b << 16).view(np.float32)
     fin = ~np.isnan(xf)
     got = _enc(hostlib, b << 16)
-    assert np.array_equal(got[fin], R.encode_npu(xf[fin]))
-    assert np.all(got[~fin] == 0x80)
+    assert np.array_equal(got, R.encode_npu(xf))        # NaN included
+    assert np.all(got[~fin] == 0xEF)                     # the -Inf code, as the Ascend kernel's NaN output
 
 
 def test_device_encoder_matches_oracle_random_fp32(hostlib, R):
@@ -150,8 +148,7 @@ def test_device_encoder_matches_oracle_random_fp32(hostlib, R):
     v = (np.ldexp(rng.random(500_000) + 1, e) * rng.choice([-1, 1], 500_000)).astype(np.float32)
     u = np.concatenate([u, v.view(np.uint32)])
     xf = u.view(np.float32)
-    fin = ~np.isnan(xf)
-    assert np.array_equal(_enc(hostlib, u)[fin], R.encode_npu(xf[fin]))
+    assert np.array_equal(_enc(hostlib, u), R.encode_npu(xf))
 
 
 def test_device_decode_matches_oracle(hostlib, R):
@@ -161,6 +158,20 @@ def test_device_decode_matches_oracle(hostlib, R):
     nan = np.isnan(d)
     assert np.array_equal(y[~nan], d[~nan].view(np.uint32))
     assert np.all(np.isnan(y.view(np.float32)[nan]))
+
+
+def test_device_code_layout_known_answers(hostlib):
+    """The kernels' decode of the published HiFloat8 layout's reference points (the same table
+    test_oracle.py pins the oracle with)."""
+    from test_oracle import HIF8_KNOWN
+    y = np.empty(256, np.uint32)
+    hostlib.chk_decode_bits(y.ctypes.data)
+    d = y.view(np.float32)
+    for c, v in HIF8_KNOWN.items():
+        assert d[c] == v, (hex(c), d[c], v)
+    assert np.isnan(d[0x80])
+    vals = np.array([HIF8_KNOWN[c] for c in sorted(HIF8_KNOWN)], np.float32)
+    assert np.array_equal(_enc(hostlib, vals.view(np.uint32)), np.array(sorted(HIF8_KNOWN), np.uint8))
 
 
 def test_lds_encode_table(hostlib, R):

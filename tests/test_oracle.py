@@ -196,6 +196,38 @@ def test_torch_literal_ops_match_numpy(R):
     assert np.array_equal(bits32(r[~nan]), bits32(got[~nan]))
 
 
+def test_torch_bf16_route_matches_torch_every_bf16(R):
+    """quant_dequant_float(bf16, force_py=True, force_fp32=False) runs QFuncs/hif8.py on the bf16
+    tensor itself: the reference's expression on torch's CPU bf16 kernels against the oracle's
+    bf16 restatement, every finite bf16 input bit for bit (non-finite inputs give NaN)."""
+    torch = pytest.importorskip("torch")
+    x = torch.from_numpy(ALL_BF16.view(np.int16)).view(torch.bfloat16)
+    got = R.quant_hif8_torch_cpu(x).view(torch.int16).numpy().view(np.uint16)
+    want = R.quant_hif8_torch_bf16(ALL_BF16)
+    fin = np.isfinite(R.bf16_to_f32(ALL_BF16))
+    assert np.array_equal(got[fin], want[fin])
+    assert np.all((got[~fin] & 0x7FFF) > 0x7F80) and np.all(want[~fin] == 0x7FC0)
+    # it differs from the fp32 route (force_fp32=True) only on 128 inputs, all below 2^-43
+    f32 = R.f32_to_bf16(R.quant_hif8_torch(R.bf16_to_f32(ALL_BF16)))
+    d = np.nonzero((want != f32) & fin)[0]
+    assert d.size == 128 and np.abs(R.bf16_to_f32(ALL_BF16[d])).max() < 2.0 ** -43
+
+
+def test_torch_bf16_log2_is_far_from_bf16_boundaries(R):
+    """The bf16 route rounds log2(bf16(|x| + 2^-45)) to bf16.  For every bf16 |x| the exact log2
+    lies at least 10 float32 ulps from a bf16 rounding boundary, so a float32 log2 that is off by
+    a few ulps (torch's on the CPU, log2f on the GPU) rounds to the same bf16 value."""
+    xu = R.bf16_to_f32(ALL_BF16[:0x7F80])                  # every non-negative finite bf16
+    t = R.bf16_to_f32(R.f32_to_bf16(xu + np.float32(2.0 ** -45))).astype(np.float64)
+    lg = np.log2(t)
+    m, e = np.frexp(lg)
+    nz = lg != 0
+    half = np.ldexp(1.0, e - 9)                             # half a bf16 unit of lg
+    dist = half - np.abs(lg - np.ldexp(np.round(m * 256.0), e - 8))
+    margin = dist[nz] / np.ldexp(1.0, e[nz] - 24)          # in float32 units of lg
+    assert margin.min() >= 10.0, margin.min()
+
+
 # ---------------------------------------------------------- invariants
 
 
@@ -249,6 +281,34 @@ def test_code_table_structure(R):
     xf = R.bf16_to_f32(ALL_BF16)
     qv = np.unique(R.quant_hif8_npu(xf[np.isfinite(xf)]))
     assert np.array_equal(np.sort(qv), np.sort(np.unique(d[~np.isnan(d)])))
+
+
+# Known answers from the published HiFloat8 layout (Luo et al., "Ascend HiFloat8 Format for Deep
+# Learning", 2024): sign | dot prefix (D exponent bits: 11 -> 4, 10 -> 3, 01 -> 2, 001 -> 1,
+# 0001 -> 0, 0000 -> denormal) | exponent in sign-magnitude with an implicit leading 1 |
+# mantissa (1, 2, 3, 3, 3 bits); denormal 0000 MMM = 2^(M - 23); 0x80 NaN; the 1.5 * 2^15 slot
+# of each sign is +-Inf, so 2^15 is the largest finite value.
+HIF8_KNOWN = {
+    0x00: 0.0, 0x01: 2.0 ** -22, 0x07: 2.0 ** -16,
+    0x08: 1.0, 0x09: 1.125, 0x0F: 1.875,                       # D = 0: e = 0
+    0x10: 2.0, 0x17: 3.75, 0x18: 0.5, 0x1C: 0.75,               # D = 1: e = +-1
+    0x20: 4.0, 0x28: 8.0, 0x2F: 15.0, 0x30: 0.25, 0x38: 0.125,  # D = 2: e = +-2, +-3
+    0x40: 16.0, 0x41: 20.0, 0x43: 28.0, 0x4C: 128.0, 0x50: 2.0 ** -4, 0x5F: 1.75 * 2.0 ** -7,  # D = 3
+    0x60: 256.0, 0x61: 384.0, 0x6E: 32768.0, 0x70: 2.0 ** -8, 0x7E: 2.0 ** -15, 0x7F: 1.5 * 2.0 ** -15,  # D = 4
+    0x6F: np.inf, 0xEF: -np.inf,
+    0x81: -(2.0 ** -22), 0x88: -1.0, 0x90: -2.0, 0xC0: -16.0, 0xEE: -32768.0,
+}
+
+
+def test_code_layout_known_answers(R):
+    d = R.decode_table()
+    for c, v in HIF8_KNOWN.items():
+        assert d[c] == v, (hex(c), d[c], v)
+    assert np.isnan(d[0x80])
+    # and the encoder maps each of these values back to its code
+    codes = np.array(sorted(HIF8_KNOWN), np.uint8)
+    vals = np.array([HIF8_KNOWN[c] for c in codes], np.float32)
+    assert np.array_equal(R.encode_npu(vals), codes)
 
 
 def test_codes_decode_to_npu_qdq_every_bf16(R):
@@ -371,8 +431,8 @@ def test_committed_fixtures_reproduce(R, golden):
     xf = R.bf16_to_f32(ALL_BF16)
     assert np.array_equal(R.f32_to_bf16(R.quant_hif8_npu(xf)), ex["npu_qdq"])
     assert np.array_equal(R.f32_to_bf16(R.quant_hif8_torch(xf)), ex["torch_qdq"])
-    fin = ~np.isnan(xf)
-    assert np.array_equal(R.encode_npu(xf[fin]), ex["codes"][fin])
+    assert np.array_equal(R.encode_npu(xf), ex["codes"])
+    assert np.all(ex["codes"][np.isnan(xf)] == 0xEF)
     sc = golden["scale"]
     sample = np.arange(0, 32768, 97)
     assert all(R.hif8_scale_bf16(int(a), 15.0) == int(sc["scale15"][a]) for a in sample)
