@@ -45,6 +45,7 @@ enum {
     HIF8_ERR_SHAPE = -2,     /* shape the kernel does not support (see each call) */
     HIF8_ERR_ALIGN = -3,     /* pointer alignment the kernel needs is not met */
     HIF8_ERR_HIP = -4,       /* a HIP runtime call or kernel launch failed */
+    HIF8_ERR_SCRATCH = -5,   /* input larger than an allocation-free entry point's static workspace */
 };
 
 enum { HIF8_DTYPE_BF16 = 0, HIF8_DTYPE_F32 = 1, HIF8_DTYPE_BF16_AS_F32 = 2 };
@@ -256,6 +257,21 @@ int hif8_modln_amax(const uint16_t *x, const uint16_t *shift, const uint16_t *sc
 int hif8_modln_fake_quant(const uint16_t *x, const uint16_t *shift, const uint16_t *scale, int64_t rows,
                           int64_t dim, int64_t rows_per_batch, const float *stats, const void *state,
                           int semantics, uint16_t *x_q, uint16_t *y, hif8_stream_t stream);
+
+/* Allocation-free form of hif8_modln_amax + hif8_modln_fake_quant: the same x_q, bit for bit,
+ * with the row statistics and the quantisation state held in a static device array of the
+ * library (1 MiB + hif8_state_size() bytes per GPU, kept until the process ends) instead of
+ * caller buffers: x, shift, scale and x_q as for those two entry points, no stats, no state, no
+ * y.  It calls no allocation routine, so it serves callers that cannot allocate: code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc.  rows <= 131072 (the 14B
+ * model at 768P has 84672), else HIF8_ERR_SCRATCH before any work is enqueued.  Every call on a
+ * GPU shares that GPU's array (the current device's; the stream must belong to it): calls that
+ * overlap on one GPU -- two streams, or two host threads -- race, and must be serialised by the
+ * caller.  The state's counters are cleared at the start of every call (a fill kernel, not a
+ * memset).  No counterpart in the reference. */
+int hif8_modln_quant_static(const uint16_t *x, const uint16_t *shift, const uint16_t *scale, int64_t rows,
+                            int64_t dim, int64_t rows_per_batch, float eps, float scale_max, int semantics,
+                            uint16_t *x_q, hif8_stream_t stream);
 
 /* ---------------------------------------------------------------------------
  * The block's residual updates (the harness around the path): x + y * e[2] and x + y * e[5]

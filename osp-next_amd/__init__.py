@@ -50,7 +50,7 @@ from .ffn import HIF8FFN  # noqa: F401
 from . import dit  # noqa: F401
 from .dit import OSPNextAttentionBlock, OSPNextBlocks  # noqa: F401
 from .norm import (WanLayerNorm, affine_norm_quant, grouped_weight, modulate, modulated_norm_quant,  # noqa: F401
-                   qkv_from_modulated_norm)
+                   modulated_norm_quant_static, qkv_from_modulated_norm)
 from .hif8_attention import (  # noqa: F401
     _HIF8QKVQuantFunction,
     attention_with_mask,
@@ -78,6 +78,6 @@ __all__ = [
     "scaled_dot_product_attention_with_mask", "LinearForward", "LinearForwardFast", "QLinear", "replace_linear",
     "save_packed", "load_packed", "pack_state_dict", "packed_from_codes", "fused_shape_ok", "linear_any",
     "linear_fwd_gelu_amax", "HIF8FFN", "WanLayerNorm", "modulate", "modulated_norm_quant", "affine_norm_quant",
-    "qkv_from_modulated_norm", "GroupedWeight", "grouped_ok", "linear_fwd_grouped", "grouped_weight",
+    "qkv_from_modulated_norm", "modulated_norm_quant_static", "GroupedWeight", "grouped_ok", "linear_fwd_grouped", "grouped_weight",
     "dit", "OSPNextAttentionBlock", "OSPNextBlocks", "linear_fwd_wq", "linear_wgrad", "transpose_bf16", "wgrad_ok",
 ]

@@ -533,6 +533,7 @@ const char *hif8_strerror(int status)
     case HIF8_ERR_SHAPE: return "unsupported shape";
     case HIF8_ERR_ALIGN: return "pointer not 16-byte aligned";
     case HIF8_ERR_HIP: return "HIP launch or runtime failure";
+    case HIF8_ERR_SCRATCH: return "input larger than the static workspace of an allocation-free entry point";
     default: return "unknown hif8 status";
     }
 }

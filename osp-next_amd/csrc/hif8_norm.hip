@@ -29,6 +29,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <mutex>
+
 #include "hif8_common.h"
 #include "hif8_internal.h"
 #include "hif8_state_dev.h"
@@ -664,6 +666,50 @@ template <int NCH, bool FULL> struct QdqAffL {
     template <typename... A> static void run(A... a) { launch_qdq_aff<NCH, FULL>(a...); }
 };
 
+// ---------------------------------------------------------------------------
+// Workspace of hif8_modln_quant_static: the per-row statistics and the quantisation state of the
+// modulated-LayerNorm producer in one file-scope device array instead of caller buffers, for
+// callers that cannot allocate.  Each GPU holds its own copy until the process ends.  Host code
+// never passes the array's name to a kernel (on the host it is only a stand-in for the symbol):
+// it uses the per-device address hipGetSymbolAddress returns.
+constexpr int64_t kStaticMaxRows = 131072;                                  // 14B at 768P: 84672 rows
+constexpr size_t kScratchStats = size_t(kStaticMaxRows) * 2 * sizeof(float);  // (mean, rstd) per row: 1 MiB
+constexpr size_t kScratchBytes = kScratchStats + sizeof(State);
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+// Clears the counters and scalars of the state in the workspace (the previous call leaves them
+// zero unless it was interrupted); a fill kernel, so a captured graph holds no memset node.
+__global__ void k_scratch_state_clear(State *st)
+{
+    if (threadIdx.x == 0) {
+        st->counter = 0;
+        st->amax_acc = 0;
+        st->amax_bits = 0;
+        st->scale = 0.0f;
+        st->fast = 0;
+        st->dtype = 0;
+        st->finite = 0;
+    }
+}
+
+static std::mutex g_scratch_mu;
+static uint8_t *g_scratch_dev[64];
+
+// The current device's address of the workspace, looked up once per device.
+static int scratch_base(uint8_t **base)
+{
+    int dev = -1;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return HIF8_ERR_HIP;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_dev[dev]) {
+        void *p = nullptr;
+        if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return HIF8_ERR_HIP;
+        g_scratch_dev[dev] = (uint8_t *)p;
+    }
+    *base = g_scratch_dev[dev];
+    return HIF8_OK;
+}
+
 }  // namespace norm
 }  // namespace hif8
 
@@ -698,6 +744,36 @@ int hif8_modln_fake_quant(const uint16_t *x, const uint16_t *shift, const uint16
                                       scale, rows, int(dim), rows_per_batch, stats, (const State *)state, semantics,
                                       x_q, y);
     if (st != HIF8_OK) return st;
+    return hipGetLastError() == hipSuccess ? HIF8_OK : HIF8_ERR_HIP;
+}
+
+int hif8_modln_quant_static(const uint16_t *x, const uint16_t *shift, const uint16_t *scale, int64_t rows,
+                            int64_t dim, int64_t rows_per_batch, float eps, float scale_max, int semantics,
+                            uint16_t *x_q, hif8_stream_t stream)
+{
+    if (!x || !x_q || rows <= 0 || dim <= 0 || rows_per_batch <= 0) return HIF8_ERR_ARG;
+    if (semantics != HIF8_SEM_NPU && semantics != HIF8_SEM_TORCH) return HIF8_ERR_ARG;
+    if (rows > kStaticMaxRows) return HIF8_ERR_SCRATCH;
+    if (dim % 8 != 0 || dim > 64 * 8 * kMaxChunks) return HIF8_ERR_SHAPE;
+    if (!aligned16(x) || !aligned16(x_q) || (shift && !aligned16(shift)) || (scale && !aligned16(scale)))
+        return HIF8_ERR_ALIGN;
+    uint8_t *base = nullptr;
+    int rc = scratch_base(&base);
+    if (rc != HIF8_OK) return rc;
+    float *stats = (float *)base;
+    State *st = (State *)(base + kScratchStats);
+    rc = check_args(x, shift, scale, rows, dim, rows_per_batch, stats, st);
+    if (rc != HIF8_OK) return rc;
+    hipStream_t s = (hipStream_t)stream;
+    hipLaunchKernelGGL(k_scratch_state_clear, dim3(1), dim3(64), 0, s, st);
+    const bool modl = use_lds_modulation(rows, dim, rows_per_batch);
+    rc = dispatch_dim<AmaxL>(dim, modl, grid_for_rows(rows, kWgPerCu), s, x, shift, scale, rows, int(dim),
+                             rows_per_batch, eps, stats, st, scale_max);
+    if (rc != HIF8_OK) return rc;
+    rc = dispatch_dim<QdqL>(dim, modl, grid_for_rows(rows, kQdqWgPerCu), s, x, shift, scale, rows, int(dim),
+                            rows_per_batch, (const float *)stats, (const State *)st, semantics, x_q,
+                            (uint16_t *)nullptr);
+    if (rc != HIF8_OK) return rc;
     return hipGetLastError() == hipSuccess ? HIF8_OK : HIF8_ERR_HIP;
 }
 

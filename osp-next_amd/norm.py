@@ -110,6 +110,37 @@ def modulated_norm_quant(x: Tensor, shift: Optional[Tensor] = None, scale: Optio
     return (xq, st, y) if return_y else (xq, st)
 
 
+STATIC_MAX_ROWS = 131072
+
+
+def modulated_norm_quant_static(x: Tensor, shift: Optional[Tensor] = None, scale: Optional[Tensor] = None,
+                                eps: float = 1e-6, scale_max: float = 15.0, semantics: int = _lib.SEM_NPU) -> Tensor:
+    """``modulated_norm_quant(x, shift, scale, eps, scale_max)[0]`` through the allocation-free entry
+    point ``hif8_modln_quant_static``: the row statistics and the state live in the library's static
+    device workspace (at most STATIC_MAX_ROWS rows), so the library allocates nothing; only x_q is
+    returned (it has no state object).  Calls overlapping on one GPU race on that workspace."""
+    if torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in (x, shift, scale)):
+        raise RuntimeError("modulated_norm_quant_static has no autograd")
+    if not fused_ok(x):
+        raise ValueError("modulated_norm_quant_static takes bf16 CUDA x with dim % 8 == 0 and dim <= 8192")
+    x = x.contiguous()
+    if x.data_ptr() % 16:
+        x = x.clone()
+    D = x.shape[-1]
+    rows = x.numel() // D
+    sh, rpb_s = _modulation_rows(shift, x, "shift")
+    sc, rpb_c = _modulation_rows(scale, x, "scale")
+    if sh is not None and sc is not None and rpb_s != rpb_c:
+        raise ValueError("shift and scale have different batch counts")
+    rpb = rpb_s or rpb_c or rows
+    xq = torch.empty_like(x)
+    _lib.check(_lib.load().hif8_modln_quant_static(x.data_ptr(), sh.data_ptr() if sh is not None else None,
+                                                   sc.data_ptr() if sc is not None else None, rows, D, rpb, float(eps),
+                                                   float(scale_max), int(semantics), xq.data_ptr(),
+                                                   _lib.stream_ptr(x.device)), "hif8_modln_quant_static")
+    return xq
+
+
 AFFINE_MAX_DIM = 6144
 
 

@@ -93,6 +93,12 @@ def test_status_codes_without_gpu(pkg):
     assert L.hif8_modln_amax(fake, None, None, 4, 5120, 0, 1e-6, fake, 15.0, fake, None) == -1
     assert L.hif8_modln_amax(fake, None, None, 4, 100, 4, 1e-6, fake, 15.0, fake, None) == -2
     assert L.hif8_modln_amax(fake, None, None, 4, 8200, 4, 1e-6, fake, 15.0, fake, None) == -2
+    # the allocation-free producer: its static workspace bounds the rows, checked before any work
+    assert L.hif8_modln_quant_static(fake, None, None, 131073, 5120, 131073, 1e-6, 15.0, 0, fake, None) == -5
+    assert L.hif8_modln_quant_static(fake, None, None, 4, 5120, 4, 1e-6, 15.0, 7, fake, None) == -1
+    assert L.hif8_modln_quant_static(fake, None, None, 4, 100, 4, 1e-6, 15.0, 0, fake, None) == -2
+    assert L.hif8_modln_quant_static(fake, None, None, 4, 5120, 4, 1e-6, 15.0, 0, odd, None) == -3
+    assert b"static workspace" in L.hif8_strerror(-5)
     assert L.hif8_modln_amax(odd, None, None, 4, 5120, 4, 1e-6, fake, 15.0, fake, None) == -3
     assert L.hif8_modln_amax(fake, odd, None, 4, 5120, 4, 1e-6, fake, 15.0, fake, None) == -3
     assert L.hif8_modln_amax(fake, None, None, 4, 5120, 4, 1e-6, fake + 4, 15.0, fake, None) == -3
