@@ -125,8 +125,12 @@ def measured_traffic(kernel: str):
 
 
 def time_ffn(pkg, torch, x, reps):
-    """The 14B FFN (osp_next.py:873-877) on x: HIF8FFN's fused route (GELU + amax in the
-    up-projection's epilogue) against the plain sequence HIF8Linear -> GELU -> HIF8Linear."""
+    """The 14B FFN (osp_next.py:873-877) on x: HIF8FFN's fused route (the up-projection's epilogue
+    folds the GELU statistic, the down-projection's quantisation applies GELU) against the plain
+    sequence HIF8Linear -> GELU -> HIF8Linear; and the up-projection's GEMM with and without the
+    GELU-statistic epilogue on the same operands (k_linear_w16<1> against <0>), with the down
+    input's quantisation with GELU (hif8_gelu_fake_quant) against the plain fake quant of the
+    same tensor."""
     dim, ffn = x.shape[1], 13824
     torch.manual_seed(3)
     mod = pkg.HIF8FFN(dim, ffn, device=x.device, dtype=torch.bfloat16)
@@ -136,21 +140,36 @@ def time_ffn(pkg, torch, x, reps):
     mod[0].prepack(drop_weight=False)
     mod[2].prepack(drop_weight=False)
     out = {}
+
+    def timed(fn, n):
+        for _ in range(2):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(n):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return round(e0.elapsed_time(e1) / n, 4)
+
     with torch.no_grad():
-        for label, fn in (("fused", lambda: mod(x)), ("sequence", lambda: torch.nn.Sequential.forward(mod, x))):
-            for _ in range(2):
-                fn()
-            torch.cuda.synchronize()
-            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            e0.record()
-            for _ in range(reps):
-                fn()
-            e1.record()
-            torch.cuda.synchronize()
-            out[f"{label}_ms"] = round(e0.elapsed_time(e1) / reps, 4)
+        out["fused_ms"] = timed(lambda: mod(x), reps)
+        out["sequence_ms"] = timed(lambda: torch.nn.Sequential.forward(mod, x), reps)
+        a, _, _ = pkg.quantize_activation(x, 15.0, "bf16")
+        w_q = mod[0]._packed_weight().dequantize()
+        st = pkg.QuantState(x.device)
+        out["up_gemm_plain_ms"] = timed(lambda: pkg.linear_fwd_wq(a, w_q, mod[0].bias), reps)
+        out["up_gemm_gelu_stat_ms"] = timed(lambda: pkg.linear_fwd_wq(a, w_q, mod[0].bias, st, 15.0), reps)
+        y = pkg.linear_fwd_wq(a, w_q, mod[0].bias, st, 15.0)
+        out["gelu_fake_quant_ms"] = timed(lambda: pkg.gelu_fake_quant(y, st, 15.0), reps)
+        st2 = pkg.absmax_scale(y, 15.0, pkg.QuantState(x.device))
+        out["plain_fake_quant_ms"] = timed(lambda: pkg.fake_quant(y, st2), reps)
+        del a, w_q, y
     flops = 2.0 * 2 * x.shape[0] * dim * ffn
     out["fused_TFLOPs"] = round(flops / (out["fused_ms"] * 1e-3) / 1e12, 1)
     out["speedup"] = round(out["sequence_ms"] / out["fused_ms"], 4)
+    out["up_epilogue_cost"] = round(out["up_gemm_gelu_stat_ms"] / out["up_gemm_plain_ms"] - 1.0, 4)
     out["what"] = "FFN 5120->13824->5120 on x[75600,5120] bf16, prepacked weights, no autograd"
     del mod
     return out
@@ -640,7 +659,7 @@ def main():
     ap.add_argument("--route", default="auto", choices=["auto", "fused", "decode_once"],
                     help="GEMM route for bf16 activations (auto: HIF8Linear's rule, decode_once at this M)")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--shapes", default="up,bwd,modln,qkv,block,step",
+    ap.add_argument("--shapes", default="up,bwd,ffn,modln,qkv,block,step",
                     help="comma list of up,bwd (the FFN-up backward),down,qkvo,ffn,modln,qkv,block (config 4),"
                          "step (config 5),"
                          "data (the GEMM with constant operands) to time in addition")
@@ -751,7 +770,11 @@ def main():
 
     extra_shapes = {}
     if "ffn" in args.shapes.split(","):
-        extra_shapes["ffn"] = time_ffn(pkg, torch, x, max(3, args.steps // 2))
+        log("[bench] timing the FFN (GELU route)")
+        try:
+            extra_shapes["ffn"] = time_ffn(pkg, torch, x, max(3, args.steps // 2))
+        except Exception as ex:
+            extra_shapes["ffn"] = {"error": repr(ex)}
     if "bwd" in args.shapes.split(","):
         log("[bench] timing the FFN-up backward (dgrad, wgrad)")
         try:

@@ -111,6 +111,20 @@ int hif8_fake_quant(const void *x, int dtype, int64_t n, const void *state, void
 int hif8_fake_quant_to_bf16(const void *x, int dtype, int64_t n, const void *state, uint16_t *y,
                             int semantics, hif8_stream_t stream);
 
+/* The FFN's GELU layer (nn.GELU(approximate="tanh") on a bf16 tensor, osp_next.py:875) folded
+ * into the next linear's _quant (hif8_linear.py:42-50), so its output is never written:
+ *   hif8_gelu_absmax_scale: amax|GELU(y)| and its scale for scale_max into state, as
+ *     hif8_absmax_scale of GELU(y) would (one read of y);
+ *   hif8_gelu_fake_quant: x_q = qdq(GELU(y) * s) / s in bf16 with state's scale -- first running
+ *     the amax of GELU(y) when state is pending (hif8_linear_fwd[_wq]_gelu_stat could not settle
+ *     it), otherwise reading y once.
+ * GELU(y) = bf16(0.5 y (1 + tanh(sqrt(2/pi) (y + 0.044715 y^3)))) in fp32, the same evaluation
+ * in every kernel.  y: n bf16, x_q: n bf16, 16-byte aligned.  No counterpart of its own in the
+ * reference, which runs GELU, amax and the fake quant as separate tensor ops. */
+int hif8_gelu_absmax_scale(const uint16_t *y, int64_t n, float scale_max, void *state, hif8_stream_t stream);
+int hif8_gelu_fake_quant(const uint16_t *y, int64_t n, void *state, float scale_max, uint16_t *x_q, int semantics,
+                         hif8_stream_t stream);
+
 /* Decode codes to x_q = decode(code) / scale in out_dtype (bf16 x_q of a bf16
  * tensor, or fp32 x_q of an fp32 tensor). */
 int hif8_decode(const uint8_t *codes, int64_t n, const void *state, int out_dtype, void *y,
@@ -158,15 +172,18 @@ int hif8_linear_fwd_grouped(const void *a, const uint8_t *w_codes, const void *c
                             const uint16_t *bias, uint16_t *const *ys, const int64_t *ns, int groups,
                             int64_t M, int64_t K, hif8_stream_t stream);
 
-/* Producer fusion for nn.Sequential(HIF8Linear, GELU(tanh), HIF8Linear)
- * (osp_next.py:873-877): hif8_linear_fwd with bf16 activations whose epilogue applies
- *   y = rnd_bf16(gelu_tanh(rnd_bf16(x_q @ w_q^T + bias)))
- * (nn.GELU(approximate="tanh") on the bf16 linear output, in fp32) and folds amax|y| into
- * y_state with the scale rule for scale_max, as hif8_absmax_scale(y) would: the next
- * linear's _quant (hif8_linear.py:45-48) then needs only hif8_fake_quant(y, y_state).
- * y_state must have been initialised (hif8_state_init); shapes as hif8_linear_fwd.
+/* Producer fusion for nn.Sequential(HIF8Linear, GELU(tanh), HIF8Linear) (osp_next.py:873-877),
+ * the up-projection's half: hif8_linear_fwd with bf16 activations, the same y, whose epilogue
+ * also folds the GELU statistic of y (its max, or a non-finite flag) into y_state.  When max y
+ * settles amax|GELU(y)| (GELU(max y) above 0.1699, the largest |GELU| of a non-positive input;
+ * GELU increases on y >= 0), y_state then holds that amax, its scale for scale_max and the
+ * decode tables, as hif8_absmax_scale(GELU(y)) would; otherwise it is marked pending.  The
+ * down-projection's _quant (hif8_linear.py:45-48) of the GELU layer's output is then
+ * hif8_gelu_fake_quant(y, y_state), which applies GELU itself: the GELU output is never
+ * written and no amax pass runs unless the state is pending.  y_state must have been
+ * initialised (hif8_state_init); shapes as hif8_linear_fwd.
  * No single reference function: it fuses three reference steps. */
-int hif8_linear_fwd_gelu_amax(const void *a, const uint8_t *w_codes, const void *w_state, const uint16_t *bias,
+int hif8_linear_fwd_gelu_stat(const void *a, const uint8_t *w_codes, const void *w_state, const uint16_t *bias,
                               uint16_t *y, int64_t M, int64_t N, int64_t K, float scale_max, void *y_state,
                               hif8_stream_t stream);
 
@@ -178,11 +195,11 @@ int hif8_linear_fwd_gelu_amax(const void *a, const uint8_t *w_codes, const void 
  * decodes each weight element once per 256-row tile of x (M/256 times); this route decodes it
  * once and streams bf16 W.  The same 16x16x32 MFMA products in the same k order: the outputs
  * equal hif8_linear_fwd's bit for bit.  Shapes, alignment and the GELU + amax and grouped variants
- * as for hif8_linear_fwd / _gelu_amax / _grouped (w_q concatenated along N for groups).
+ * as for hif8_linear_fwd / _gelu_stat / _grouped (w_q concatenated along N for groups).
  * No counterpart of its own in the reference: it is F.linear on the dequantised operands. */
 int hif8_linear_fwd_wq(const uint16_t *a, const uint16_t *w_q, const uint16_t *bias, uint16_t *y, int64_t M,
                        int64_t N, int64_t K, hif8_stream_t stream);
-int hif8_linear_fwd_wq_gelu_amax(const uint16_t *a, const uint16_t *w_q, const uint16_t *bias, uint16_t *y,
+int hif8_linear_fwd_wq_gelu_stat(const uint16_t *a, const uint16_t *w_q, const uint16_t *bias, uint16_t *y,
                                  int64_t M, int64_t N, int64_t K, float scale_max, void *y_state,
                                  hif8_stream_t stream);
 int hif8_linear_fwd_wq_grouped(const uint16_t *a, const uint16_t *w_q, const uint16_t *bias, uint16_t *const *ys,

@@ -19,6 +19,7 @@
 #include "hif8_internal.h"
 #include "hif8_state_dev.h"
 #include "hif8_qdq_dev.h"
+#include "hif8_gelu_dev.h"
 
 namespace hif8 {
 
@@ -36,6 +37,7 @@ __global__ void k_state_init(State *st)
         st->fast = 0;
         st->dtype = 0;
         st->finite = 0;
+        st->pending = 0;
     }
 }
 
@@ -48,6 +50,7 @@ __global__ __launch_bounds__(256) void k_set_scale(State *st, int dtype, float s
         st->fast = (__builtin_isfinite(s) && s > 0.0f) ? 1u : 0u;
         st->finite = 0;   // no amax pass: inputs may hold NaN
         st->amax_bits = 0;
+        st->pending = 0;
     }
     fill_luts(st, s, c);
 }
@@ -145,13 +148,14 @@ __global__ __launch_bounds__(kTPB) void k_absmax(const void *__restrict__ xv, in
     else fold_amax(st, m, gridDim.x, DT, smax, red + kTPB / 64);
 }
 
-// Element j of k_quant through the scalar reference route.
-template <int DT, int MODE>
+// Element j of k_quant through the scalar reference route (GELU: of the GELU of a bf16 element).
+template <int DT, int MODE, bool GELU = false>
 __device__ __forceinline__ void scalar_elem(const void *xv, void *outv, int64_t j, float s, int sem)
 {
     uint32_t xb, yb, code;
     if (DT == kBF16) {
         xb = ((const uint16_t *)xv)[j];
+        if (GELU) xb = gelu_bf16(xb);
         slow_elem<kBF16>(xb, s, sem, yb, code);
     } else {
         xb = DT == kF32 ? ((const uint32_t *)xv)[j] : uint32_t(((const uint16_t *)xv)[j]) << 16;
@@ -165,8 +169,10 @@ __device__ __forceinline__ void scalar_elem(const void *xv, void *outv, int64_t 
 
 // MODE 0: codes, MODE 1: qdq in the arithmetic dtype (bf16 for kBF16, fp32 otherwise),
 // MODE 2: decode codes -> x_q, MODE 3: qdq rounded to the bf16 GEMM operand.
-// DT kBF16F32 loads bf16 and computes as kF32 on the exact fp32 values.
-template <int DT, int MODE>
+// DT kBF16F32 loads bf16 and computes as kF32 on the exact fp32 values.  GELU (kBF16, MODE 1):
+// each element is first replaced by its GELU, rounded to bf16 (the FFN's GELU layer, applied in
+// the down-projection's quantisation instead of in a pass of its own).
+template <int DT, int MODE, bool GELU = false>
 __global__ __launch_bounds__(kTPB) void k_quant(const void *__restrict__ xv, int64_t n,
                                                  const State *__restrict__ st, void *__restrict__ outv,
                                                  int sem, int use_state)
@@ -266,6 +272,10 @@ __global__ __launch_bounds__(kTPB) void k_quant(const void *__restrict__ xv, int
                 u32x4 a = cur[0];
                 u32x4 b = cur[1];
                 uint32_t p[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+                if (GELU) {
+#pragma unroll
+                    for (int k = 0; k < 8; ++k) p[k] = gelu_bf16x2(p[k]);
+                }
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
                     uint32_t p0 = p[2 * j], p1 = p[2 * j + 1];
@@ -352,11 +362,11 @@ __global__ __launch_bounds__(kTPB) void k_quant(const void *__restrict__ xv, int
         }
     } else {
         // degenerate scale (amax Inf/NaN, scale 0/Inf/NaN): element-wise reference route
-        for (int64_t j = g; j < (ngrp << 4); j += stride) scalar_elem<DT, MODE>(xv, outv, j, s, sem);
+        for (int64_t j = g; j < (ngrp << 4); j += stride) scalar_elem<DT, MODE, GELU>(xv, outv, j, s, sem);
     }
     // tail (n % 16) through the scalar route
     for (int64_t j = (ngrp << 4) + int64_t(blockIdx.x) * kTPB + tid; j < n; j += stride)
-        scalar_elem<DT, MODE>(xv, outv, j, s, sem);
+        scalar_elem<DT, MODE, GELU>(xv, outv, j, s, sem);
 }
 
 // QFuncs/hif8.py:6-23 evaluated on a bf16 tensor without force_fp32 (quant_dequant_float with
@@ -380,6 +390,38 @@ static __device__ uint32_t qdq_torch_bf16(uint32_t xb)
     const float f = __builtin_floorf(bf2f(f2bf(m + 0.5f)));             // floor(. + 0.5)
     const float r = bf2f(f2bf(f * __builtin_ldexpf(1.0f, e - mb)));     // * 2**(e - mb)
     return f2bf(r * sign);                                              // * sign
+}
+
+// amax|GELU(y)| of a bf16 tensor folded into st with the scale rule for smax: hif8_absmax_scale
+// of the GELU layer's output, without writing it.  With only_pending, a state whose GELU
+// statistic settled the amax (pending == 0, written by the up-projection's GEMM) is left as it
+// is and every workgroup returns at once; all workgroups read the same flag before any of them
+// folds, so they all take the same branch.
+__global__ __launch_bounds__(kTPB) void k_gelu_absmax(const uint16_t *__restrict__ y, int64_t n,
+                                                      State *__restrict__ st, float smax, int only_pending)
+{
+    if (only_pending && st->pending == 0) return;
+    const int tid = threadIdx.x;
+    const int64_t stride = int64_t(gridDim.x) * kTPB;
+    const int64_t nvec = n >> 3;
+    const u32x4 *yq = (const u32x4 *)y;
+    uint32_t m = 0;
+    for (int64_t i = int64_t(blockIdx.x) * kTPB + tid; i < nvec; i += stride) {
+        const u32x4 v = ld_stream(&yq[i]);
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const uint32_t w = gelu_bf16x2(v[t]) & 0x7FFF7FFFu;
+            m = max(m, max(w & 0xFFFFu, w >> 16));
+        }
+    }
+    for (int64_t j = (nvec << 3) + int64_t(blockIdx.x) * kTPB + tid; j < n; j += stride)
+        m = max(m, gelu_bf16(y[j]) & 0x7FFFu);
+    for (int o = 32; o > 0; o >>= 1) m = max(m, (uint32_t)__shfl_xor((int)m, o, 64));
+    __shared__ uint32_t red[kTPB / 64 + 2];
+    if ((tid & 63) == 0) red[tid >> 6] = m;
+    __syncthreads();
+    m = max(max(red[0], red[1]), max(red[2], red[3]));
+    fold_amax(st, m, gridDim.x, kBF16, smax, red + kTPB / 64);
 }
 
 // Unscaled qdq of a bf16 tensor with QFuncs/hif8.py evaluated in bf16 arithmetic (the
@@ -494,6 +536,7 @@ __global__ __launch_bounds__(kTPB) void k_transpose_bf16(const uint16_t *__restr
 constexpr int kAmaxWgPerCu = 1;
 constexpr int kEncodeWgPerCu = 4;
 constexpr int kQdqWgPerCu = 8;
+constexpr int kGeluAmaxWgPerCu = 4;   // the GELU amax pass is VALU-bound: more waves per CU
 
 static int grid_for(int64_t units, int max_blocks)
 {
@@ -584,7 +627,7 @@ int hif8_set_scale(void *state, int dtype, float scale, hif8_stream_t stream)
 }
 
 static int launch_quant(const void *x, int dtype, int64_t n, const void *state, void *out, int mode,
-                        int sem, int use_state, hif8_stream_t stream)
+                        int sem, int use_state, hif8_stream_t stream, bool gelu = false)
 {
     if (!x || !out || n <= 0 || (use_state && !state)) return HIF8_ERR_ARG;
     if (dtype != HIF8_DTYPE_BF16 && dtype != HIF8_DTYPE_F32 && !(dtype == kBF16F32 && mode != 2)) return HIF8_ERR_ARG;
@@ -595,7 +638,10 @@ static int launch_quant(const void *x, int dtype, int64_t n, const void *state, 
     const State *st = (const State *)state;
 #define HIF8_LAUNCH(DT, MODE) \
     hipLaunchKernelGGL((k_quant<DT, MODE>), dim3(grid), dim3(kTPB), 0, s, x, n, st, out, sem, use_state)
-    if (dtype == HIF8_DTYPE_BF16) {
+    if (gelu) {
+        if (dtype != HIF8_DTYPE_BF16 || mode != 1) return HIF8_ERR_ARG;
+        hipLaunchKernelGGL((k_quant<kBF16, 1, true>), dim3(grid), dim3(kTPB), 0, s, x, n, st, out, sem, use_state);
+    } else if (dtype == HIF8_DTYPE_BF16) {
         if (mode == 0) HIF8_LAUNCH(kBF16, 0);
         else if (mode == 1 || mode == 3) HIF8_LAUNCH(kBF16, 1);
         else HIF8_LAUNCH(kBF16, 2);
@@ -649,6 +695,30 @@ int hif8_quant_bf16(const uint16_t *x, uint16_t *y, int64_t n, int semantics, hi
         return last_launch();
     }
     return launch_quant(x, HIF8_DTYPE_BF16, n, nullptr, y, 1, semantics, 0, stream);
+}
+
+int hif8_gelu_absmax_scale(const uint16_t *y, int64_t n, float scale_max, void *state, hif8_stream_t stream)
+{
+    if (!y || !state || n <= 0) return HIF8_ERR_ARG;
+    if (!aligned16(y)) return HIF8_ERR_ALIGN;
+    const int grid = grid_for((n + 7) / 8, cu_count() * kGeluAmaxWgPerCu);
+    hipLaunchKernelGGL(k_gelu_absmax, dim3(grid), dim3(kTPB), 0, (hipStream_t)stream, y, n, (State *)state,
+                       scale_max, 0);
+    return last_launch();
+}
+
+int hif8_gelu_fake_quant(const uint16_t *y, int64_t n, void *state, float scale_max, uint16_t *x_q, int semantics,
+                         hif8_stream_t stream)
+{
+    if (!y || !state || !x_q || n <= 0) return HIF8_ERR_ARG;
+    if (semantics != HIF8_SEM_NPU && semantics != HIF8_SEM_TORCH) return HIF8_ERR_ARG;
+    if (!aligned16(y) || !aligned16(x_q)) return HIF8_ERR_ALIGN;
+    const int grid = grid_for((n + 7) / 8, cu_count() * kGeluAmaxWgPerCu);
+    hipLaunchKernelGGL(k_gelu_absmax, dim3(grid), dim3(kTPB), 0, (hipStream_t)stream, y, n, (State *)state,
+                       scale_max, 1);
+    const int rc = last_launch();
+    if (rc != HIF8_OK) return rc;
+    return launch_quant(y, HIF8_DTYPE_BF16, n, state, x_q, 1, semantics, 1, stream, true);
 }
 
 int hif8_transpose_bf16(const uint16_t *x, int64_t rows, int64_t cols, int64_t rows_pad, uint16_t *out,

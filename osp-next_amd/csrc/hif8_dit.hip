@@ -128,9 +128,11 @@ __device__ __forceinline__ uint32_t bf_t(float f)
 }
 __device__ __forceinline__ uint32_t pack_t(float a, float b) { return bf_t(a) | (bf_t(b) << 16); }
 
+// out may be x (an in-place residual update): x, y and out are not restrict-qualified.  Each
+// element is loaded before its own store and no other element reads it.
 template <bool GATE>
-__global__ __launch_bounds__(kThreads) void k_gated_residual(const u32x4 *__restrict__ x, const u32x4 *__restrict__ y,
-                                                             const uint16_t *__restrict__ gate, u32x4 *__restrict__ out,
+__global__ __launch_bounds__(kThreads) void k_gated_residual(const u32x4 *x, const u32x4 *y,
+                                                             const uint16_t *__restrict__ gate, u32x4 *out,
                                                              int64_t nvec, int64_t dim, int64_t rows_per_batch)
 {
     const int64_t stride = int64_t(gridDim.x) * kThreads;

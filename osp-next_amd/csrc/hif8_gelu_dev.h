@@ -1,0 +1,122 @@
+// GELU (tanh approximation) of the DiT block's FFN -- nn.GELU(approximate="tanh") between the
+// up- and down-projections, osp_next.py:873-877 -- and the statistic that gives amax|GELU(y)| of
+// the up-projection's output without a pass over it.  Shared by the GEMM epilogues (which fold
+// the statistic) and the codec (which applies GELU in the down-projection's quantisation pass),
+// so both evaluate GELU with the same roundings.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "hif8_internal.h"
+#include "hif8_state_dev.h"
+
+namespace hif8 {
+
+// GELU in fp32 as the reference evaluates it on a bf16 tensor:
+//   u = sqrt(2/pi) (x + 0.044715 x^3),   y = 0.5 x (1 + tanh(u)).
+// tanh(u) = sign(u) (1 - d) with d = 2 / (1 + e^(2|u|)), from the hardware exp2 and reciprocal;
+// forming 1 - d in fp32 rounds it to the fp32 grid next to +-1 as an fp32 tanh does, so the
+// cancellation in 1 + tanh(u) for u << 0 (the result's tail) behaves as in the reference.  The
+// product-sum in u is one fused multiply-add and nothing else is contracted, whatever the
+// translation unit's contraction setting.
+__device__ __forceinline__ float gelu_tanh(float x)
+{
+#pragma clang fp contract(off)
+    const float u = 0.7978845608028654f * __builtin_fmaf(0.044715f, x * x * x, x);
+    const float e = __builtin_amdgcn_exp2f(__builtin_fabsf(u) * 2.8853900817779268f);  // e^(2|u|)
+    const float d = 2.0f * __builtin_amdgcn_rcpf(1.0f + e);
+    const float th = __builtin_copysignf(1.0f - d, u);
+    return 0.5f * x * (1.0f + th);
+}
+
+// Packed RNE conversion of two floats to bf16 (v_cvt_pk_bf16_f32).
+__device__ __forceinline__ uint32_t gelu_pk_cvt(float lo, float hi)
+{
+    typedef float f32x2 __attribute__((ext_vector_type(2)));
+    typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+    f32x2 v = {lo, hi};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
+}
+
+// GELU of the two bf16 values of a word, each rounded to bf16: the GELU layer's bf16 output.
+__device__ __forceinline__ uint32_t gelu_bf16x2(uint32_t w)
+{
+    return gelu_pk_cvt(gelu_tanh(bf2f(w & 0xFFFFu)), gelu_tanh(bf2f(w >> 16)));
+}
+__device__ __forceinline__ uint32_t gelu_bf16(uint32_t b) { return gelu_bf16x2(b & 0xFFFFu) & 0xFFFFu; }
+
+// The GELU statistic of a set of bf16 outputs: the largest non-negative value (bf16 bits, 0 when
+// there is none) or kGeluNonFinite when any output is Inf or NaN (GELU(-Inf) and GELU(NaN) are
+// NaN: the amax then needs the full pass).  Accumulated two outputs per 32-bit word:
+//   spos: packed signed 16-bit max of the raw bits -- a negative bf16 is a negative int16, a
+//         non-negative one keeps its numeric order;
+//   smag: packed unsigned 16-bit max of the magnitude bits, which reaches 0x7F80 for Inf or NaN.
+constexpr uint32_t kGeluNonFinite = 0x10000u;
+__device__ __forceinline__ void gelu_stat_pk(uint32_t &spos, uint32_t &smag, uint32_t w0, uint32_t w1)
+{
+    typedef short i16x2 __attribute__((ext_vector_type(2)));
+    typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+    const i16x2 p = __builtin_elementwise_max(__builtin_bit_cast(i16x2, w0), __builtin_bit_cast(i16x2, w1));
+    spos = __builtin_bit_cast(uint32_t, __builtin_elementwise_max(__builtin_bit_cast(i16x2, spos), p));
+    const u16x2 q = __builtin_elementwise_max(__builtin_bit_cast(u16x2, w0 & 0x7FFF7FFFu),
+                                              __builtin_bit_cast(u16x2, w1 & 0x7FFF7FFFu));
+    smag = __builtin_bit_cast(uint32_t, __builtin_elementwise_max(__builtin_bit_cast(u16x2, smag), q));
+}
+// One lane's statistic from its packed maxima (as an unsigned value: maxima of these over lanes and
+// workgroups are the statistic of the union).
+__device__ __forceinline__ uint32_t gelu_stat_final(uint32_t spos, uint32_t smag)
+{
+    const uint32_t mag = max(smag & 0xFFFFu, smag >> 16);
+    if (mag >= 0x7F80u) return kGeluNonFinite;
+    const int lo = int(short(spos & 0xFFFFu)), hi = int(short(spos >> 16));
+    const int p = lo > hi ? lo : hi;
+    return p > 0 ? uint32_t(p) : 0u;
+}
+
+// |GELU(y)| for y <= 0 is at most 0.16997 (near y = -0.7518): 0x3E2E (0.16992) once rounded to
+// bf16, with every y <= 0 mapping at or below it.  GELU increases on y >= 0, so when GELU(ymax)
+// rounds above 0x3E2E the largest |GELU(y)| over a tensor is GELU(ymax) itself.
+constexpr uint32_t kGeluNegAmaxBits = 0x3E2Eu;
+
+// Fold one workgroup's statistic (the max of gelu_stat_final over its lanes, thread 0's value) into
+// st.  The last of nwg workgroups resets the accumulators and, when max y settles the amax, writes
+// amax = GELU(max y), the scale for smax, the flags and the decode tables, as hif8_absmax_scale
+// of GELU(y) would; otherwise it marks the state pending (the down-projection's quantisation
+// then runs the amax pass first).  Called by all 256 threads; lds is three words of LDS.
+__device__ __forceinline__ void fold_gelu_stat(State *st, uint32_t m, uint32_t nwg, float smax, uint32_t *lds)
+{
+    const uint32_t tid = threadIdx.x;
+    if (tid == 0) {
+        __hip_atomic_fetch_max(&st->amax_acc, m, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const uint32_t prev = __hip_atomic_fetch_add(&st->counter, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+        lds[0] = (prev == nwg - 1) ? 1u : 0u;
+    }
+    __syncthreads();
+    if (!lds[0]) return;
+    if (tid == 0) {
+        const uint32_t a = __hip_atomic_exchange(&st->amax_acc, 0u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(&st->counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        uint32_t g = 0;
+        bool settled = false;
+        if (a < kGeluNonFinite) {
+            g = gelu_bf16(a);                                  // a: the largest output, non-negative
+            settled = g > kGeluNegAmaxBits && g < 0x7F80u;   // positive, finite, above every y <= 0
+        }
+        bool fast = false;
+        float s = 0.0f;
+        if (settled) s = scale_from_amax(g, kBF16, smax, fast);
+        st->amax_bits = settled ? g : 0u;
+        st->scale = s;
+        st->fast = fast ? 1u : 0u;
+        st->finite = fast ? 1u : 0u;
+        st->dtype = uint32_t(kBF16);
+        st->pending = settled ? 0u : 1u;
+        lds[1] = settled ? 1u : 0u;
+        lds[2] = f2u(s);
+    }
+    __syncthreads();
+    if (lds[1]) fill_luts(st, u2f(lds[2]), tid);
+}
+
+}  // namespace hif8

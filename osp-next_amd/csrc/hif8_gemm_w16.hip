@@ -25,7 +25,7 @@
 //   - The main loop is the fixed schedule in hif8_gemm_schedule_w16.inc (gen_gemm_schedule.py).
 //   - Epilogue: bias, RNE to bf16, staged through LDS into whole 512-byte row stores, non-temporal
 //     (the output is not read again here; it should not displace operand panels from L2); the
-//     GELU + amax variant and grouped outputs as in k_linear_dtl.
+//     GELU-statistic variant and grouped outputs as in k_linear_dtl.
 //   - Tile order: groups of group_m m-tiles, n-tiles outer within a group.  Workgroups go to the
 //     8 XCDs round robin, so each XCD runs (group_m / 8) m-tiles x (256 / group_m) n-tiles of
 //     every 256 consecutive tiles and its L2 fetches that many X and W panels.  Measured on the
@@ -35,6 +35,7 @@
 #include <stdint.h>
 
 #include "hif8_internal.h"
+#include "hif8_gelu_dev.h"
 #include "hif8_state_dev.h"
 
 namespace hif8 {
@@ -78,16 +79,6 @@ __device__ __forceinline__ void dtl_load(uint32_t m0v, uint32_t voff, const u32x
     ASMV("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(m0v), "v"(voff), "s"(rs) : "memory", "m0");
 }
 __device__ __forceinline__ void tie(u32x4 &a) { ASMV("" : "+v"(a)); }
-
-// GELU with the tanh approximation, as k_linear_dtl's epilogue evaluates it.
-__device__ __forceinline__ float gelu_tanh(float x)
-{
-    const float u = 0.7978845608028654f * (x + 0.044715f * (x * x * x));
-    const float e = __builtin_amdgcn_exp2f(__builtin_fabsf(u) * 2.8853900817779268f);  // e^(2|u|)
-    const float d = 2.0f * __builtin_amdgcn_rcpf(1.0f + e);
-    const float th = __builtin_copysignf(1.0f - d, u);
-    return 0.5f * x * (1.0f + th);
-}
 
 __device__ __forceinline__ uint32_t f2bf_pk(float lo, float hi)
 {
@@ -161,8 +152,10 @@ template <int SET> __device__ __forceinline__ void tie_set(Ctx &c)
 
 #include "hif8_gemm_schedule_w16.inc"
 
-// EPI 0: y = rnd(acc + bias).  EPI 1: y = rnd(gelu(rnd(acc + bias))) with amax|y| folded into
-// y_st (scale for y_smax).  The output features are G.n groups, each with its output buffer.
+// EPI 0: y = rnd(acc + bias).  EPI 1: the same y, and the GELU statistic of y (its max, or a
+// non-finite flag) folded into y_st, which then holds amax|GELU(y)| and its scale for y_smax
+// when max y settles it (hif8_gelu_dev.h).  The output features are G.n groups, each with its
+// output buffer.
 template <int EPI>
 __global__ __launch_bounds__(kThreads, 1) void k_linear_w16(const uint16_t *__restrict__ X, const uint16_t *__restrict__ Wq,
                                                             const Groups G, const uint16_t *__restrict__ bias,
@@ -282,7 +275,6 @@ __global__ __launch_bounds__(kThreads, 1) void k_linear_w16(const uint16_t *__re
     // m = wm + 16j + r.  Rows go to LDS (padded), then each wave stores 2 rows x 512 B per
     // instruction.
     __syncthreads();
-    uint32_t ymax = 0;  // EPI 1: largest magnitude bits of this lane's in-range outputs
     {
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
@@ -301,28 +293,16 @@ __global__ __launch_bounds__(kThreads, 1) void k_linear_w16(const uint16_t *__re
                 for (int j = 0; j < 8; ++j) {
                     const f32x4 &a = c.acc[i][j];
                     uint2 v;
-                    if (EPI == 0) {
-                        v.x = f2bf_pk(a[0] + b0, a[1] + b1);
-                        v.y = f2bf_pk(a[2] + b2, a[3] + b3);
-                    } else {
-                        const uint32_t p01 = f2bf_pk(a[0] + b0, a[1] + b1);
-                        const uint32_t p23 = f2bf_pk(a[2] + b2, a[3] + b3);
-                        v.x = f2bf_pk(gelu_tanh(bf2f(p01 & 0xFFFFu)), gelu_tanh(bf2f(p01 >> 16)));
-                        v.y = f2bf_pk(gelu_tanh(bf2f(p23 & 0xFFFFu)), gelu_tanh(bf2f(p23 >> 16)));
-                        const int m = m0 + int(wm) + j * 16 + int(r);
-                        if (n < N && m < M) {
-                            typedef uint16_t u16x2 __attribute__((ext_vector_type(2)));
-                            const u16x2 mg = __builtin_elementwise_max(__builtin_bit_cast(u16x2, v.x & 0x7FFF7FFFu),
-                                                                       __builtin_bit_cast(u16x2, v.y & 0x7FFF7FFFu));
-                            ymax = max(ymax, uint32_t(max(mg.x, mg.y)));
-                        }
-                    }
+                    v.x = f2bf_pk(a[0] + b0, a[1] + b1);
+                    v.y = f2bf_pk(a[2] + b2, a[3] + b3);
                     *(uint2 *)(smem + (wm + uint32_t(j * 16) + r) * kOutRow + nl * 2u) = v;
                 }
             }
         }
     }
     __syncthreads();
+    // EPI 1: packed running maxima of the in-range outputs this lane stores (the GELU statistic)
+    uint32_t spos = 0, smag = 0;
     {
         const uint32_t colb = (lane & 31u) * 16u, h = lane >> 5;
         const int n = n0 + int(colb / 2u);
@@ -337,26 +317,32 @@ __global__ __launch_bounds__(kThreads, 1) void k_linear_w16(const uint16_t *__re
 #pragma unroll
             for (int it = 0; it < 8; ++it) {
                 const int m = m0 + int(c.wave * 64u + uint32_t(blk * 8 + it) * 2u + h);
-                if (m < M && n - col0 < ycols)
+                if (m < M && n - col0 < ycols) {
                     __builtin_nontemporal_store(v[it], (u32x4 *)(Y + size_t(m) * size_t(ycols) + (n - col0)));
+                    if (EPI == 1) {
+                        gelu_stat_pk(spos, smag, v[it][0], v[it][1]);
+                        gelu_stat_pk(spos, smag, v[it][2], v[it][3]);
+                    }
+                }
             }
         }
     }
     if (EPI == 1) {
-        for (int o = 32; o > 0; o >>= 1) ymax = max(ymax, (uint32_t)__shfl_xor((int)ymax, o, 64));
+        uint32_t ystat = gelu_stat_final(spos, smag);
+        for (int o = 32; o > 0; o >>= 1) ystat = max(ystat, (uint32_t)__shfl_xor((int)ystat, o, 64));
         uint32_t *red = (uint32_t *)smem;  // the staging rows are read: reuse after the barrier
         __syncthreads();
-        if (lane == 0) red[c.wave] = ymax;
+        if (lane == 0) red[c.wave] = ystat;
         __syncthreads();
-        ymax = max(max(red[0], red[1]), max(red[2], red[3]));
-        fold_amax(y_st, ymax, gridDim.x, kBF16, y_smax, red + 4);
+        ystat = max(max(red[0], red[1]), max(red[2], red[3]));
+        fold_gelu_stat(y_st, ystat, gridDim.x, y_smax, red + 4);
     }
 }
 
 }  // namespace w16
 
 // Shapes: K % 64 == 0, N % 8 == 0, 16-byte aligned X, W_q and Y, 8-byte aligned bias (checked
-// by the caller).  M, N < 2^31, K < 2^22.  y_st != NULL selects the GELU + amax epilogue.
+// by the caller).  M, N < 2^31, K < 2^22.  y_st != NULL selects the GELU-statistic epilogue.
 static int launch_w16(const uint16_t *x, const uint16_t *w_q, const Groups &g, const uint16_t *bias, int64_t M,
                       int64_t N, int64_t K, hif8_stream_t stream, State *y_st, float y_smax)
 {
@@ -418,7 +404,7 @@ extern "C" int hif8_linear_fwd_wq(const uint16_t *a, const uint16_t *w_q, const 
     return rc != HIF8_OK ? rc : launch_linear_w16(a, w_q, bias, y, M, N, K, stream, nullptr, 0.0f);
 }
 
-extern "C" int hif8_linear_fwd_wq_gelu_amax(const uint16_t *a, const uint16_t *w_q, const uint16_t *bias,
+extern "C" int hif8_linear_fwd_wq_gelu_stat(const uint16_t *a, const uint16_t *w_q, const uint16_t *bias,
                                             uint16_t *y, int64_t M, int64_t N, int64_t K, float scale_max,
                                             void *y_state, hif8_stream_t stream)
 {

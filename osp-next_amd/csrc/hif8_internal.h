@@ -22,7 +22,7 @@ struct alignas(256) State {
     uint32_t fast;         // 1 when amax and scale are finite and scale > 0
     uint32_t dtype;        // HIF8_DTYPE_* the tables were built for
     uint32_t finite;       // 1 when an amax pass proved every input element finite
-    uint32_t pad;
+    uint32_t pending;      // 1 when a GEMM's GELU statistic left amax|GELU(y)| to an amax pass
     uint16_t lut_bf16[256];  // bf16 bits of x_q(code) = rnd(decode(code) / scale)
     float lut_f32[256];      // fp32 decode(code) / scale
 };
@@ -42,7 +42,8 @@ struct Groups {
 };
 
 // Fused GEMM for bf16 activations (hif8_gemm_dtl.hip); the caller has checked shapes and
-// alignment as hif8_linear_fwd documents.  With y_st, the GELU + amax epilogue.
+// alignment as hif8_linear_fwd documents.  With y_st, the epilogue also folds the GELU
+// statistic of its output (max y, hif8_gelu_dev.h) into y_st.
 int launch_linear_dtl(const uint16_t *x, const uint8_t *w_codes, const State *w_st, const uint16_t *bias,
                       uint16_t *y, int64_t M, int64_t N, int64_t K, hif8_stream_t stream, State *y_st = nullptr,
                       float y_smax = 0.0f);

@@ -1,7 +1,7 @@
 // C-ABI entry points of the fused HiF8 dequant-GEMM (k_linear_dtl, hif8_gemm_dtl.hip):
 //   Y[M,N] = X_q[M,K] . W_q[N,K]^T + bias[N]
 // the F.linear(x_q, w_q, bias) of ospnext/modules/hif8_linear.py:86 with bf16 activations x_q
-// and W held as packed 8-bit HiF8 codes, plus its GELU + amax epilogue and grouped forms.
+// and W held as packed 8-bit HiF8 codes, plus its GELU-statistic epilogue and grouped forms.
 // Shapes and alignment are checked here; the kernels assume them.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -18,7 +18,7 @@ constexpr int kBK = 64;
 
 using namespace hif8;
 
-extern "C" int hif8_linear_fwd_gelu_amax(const void *a, const uint8_t *w_codes, const void *w_state,
+extern "C" int hif8_linear_fwd_gelu_stat(const void *a, const uint8_t *w_codes, const void *w_state,
                                          const uint16_t *bias, uint16_t *y, int64_t M, int64_t N, int64_t K,
                                          float scale_max, void *y_state, hif8_stream_t stream)
 {

@@ -689,6 +689,7 @@ __global__ void k_scratch_state_clear(State *st)
         st->fast = 0;
         st->dtype = 0;
         st->finite = 0;
+        st->pending = 0;
     }
 }
 

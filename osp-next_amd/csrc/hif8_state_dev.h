@@ -80,6 +80,7 @@ __device__ __forceinline__ void fold_amax(State *st, uint32_t m, uint32_t nwg, i
         st->fast = fast ? 1u : 0u;
         st->finite = fast ? 1u : 0u;   // amax finite => every element finite
         st->dtype = uint32_t(dtype);
+        st->pending = 0u;
         lds[1] = f2u(s);
     }
     __syncthreads();

@@ -4,12 +4,16 @@
 HIF8Linear(ffn_dim, dim))`` -- ``ospnext/modules/osp_next.py:873-877`` -- with the same
 children and state-dict keys.  Without autograd, a bf16 input takes the fused route:
 
-    up:    hif8_linear_fwd_gelu_amax   y = gelu(x_q @ w_up^T + b_up), amax|y| and its scale
-    down:  hif8_fake_quant(y) with that scale (no amax pass), then the fused GEMM
+    up:    hif8_linear[_wq]_gelu_stat  y = x_q @ w_up^T + b_up, and max y, which settles
+                                        amax|GELU(y)| and its scale (GELU increases on y >= 0)
+    down:  hif8_gelu_fake_quant(y)      x_q = _quant(GELU(y)) with that scale, GELU applied on
+                                        the way in; then the GEMM
 
-which removes the standalone GELU pass and the down-projection's amax pass (the
-reference reads and writes y for GELU and reads it again for amax|y|).  With autograd,
-or for inputs and shapes the fused kernels do not take, it runs the plain sequence.
+which removes the GELU pass (read and write of y), the down-projection's amax pass and the GELU
+evaluation from the up-projection's epilogue, where the matrix cores would wait for it.  If max
+y does not settle the amax (no positive output large enough, or a non-finite one), the
+quantisation runs the amax pass of GELU(y) first.  With autograd, or for inputs and shapes the
+fused kernels do not take, it runs the plain sequence.
 """
 from __future__ import annotations
 
@@ -18,8 +22,8 @@ import torch.nn as nn
 from torch import Tensor
 
 from . import _lib
-from .hif8_linear import (HIF8Linear, QuantState, fake_quant, fused_shape_ok, linear_any,
-                          linear_fwd_gelu_amax, quantize_activation)
+from .hif8_linear import (HIF8Linear, QuantState, fused_shape_ok, gelu_fake_quant, linear_any,
+                          linear_fwd_gelu_stat, quantize_activation)
 
 
 class HIF8FFN(nn.Sequential):
@@ -59,9 +63,9 @@ class HIF8FFN(nn.Sequential):
         return self._fused_from_xq(x_q.reshape(-1, K).contiguous()).view(*x_q.shape[:-1], -1)
 
     def _fused_from_xq(self, a: Tensor) -> Tensor:
-        """up with the GELU + amax epilogue, fake quant of its output with that state, down."""
+        """up with the GELU-statistic epilogue, the fake quant of GELU of its output, down."""
         up, down = self[0], self[2]
         y_st = QuantState(a.device)
-        y = linear_fwd_gelu_amax(a, up._packed_weight(), up.bias, y_st, down.scale_max_forward)
-        yq = fake_quant(y, y_st)
+        y = linear_fwd_gelu_stat(a, up._packed_weight(), up.bias, y_st, down.scale_max_forward)
+        yq = gelu_fake_quant(y, y_st, down.scale_max_forward)
         return linear_any(yq, _lib.A_BF16, None, down._packed_weight(), down.bias)

@@ -259,8 +259,8 @@ def decode_once(M: int) -> bool:
 
 def linear_fwd_wq(a: Tensor, w_q: Tensor, bias: Optional[Tensor], y_state: Optional[QuantState] = None,
                   scale_max: float = 15.0) -> Tensor:
-    """hif8_linear_fwd_wq[_gelu_amax]: y = x_q @ w_q^T + bias with w_q the dequantised bf16 weight
-    [N, K] (``PackedWeight.dequantize()``); with ``y_state`` the GELU + amax epilogue."""
+    """hif8_linear_fwd_wq[_gelu_stat]: y = x_q @ w_q^T + bias with w_q the dequantised bf16 weight
+    [N, K] (``PackedWeight.dequantize()``); with ``y_state`` the GELU-statistic epilogue."""
     M, K = a.shape
     N = w_q.shape[0]
     if w_q.shape[1] != K or w_q.dtype != torch.bfloat16 or a.dtype != torch.bfloat16:
@@ -276,8 +276,8 @@ def linear_fwd_wq(a: Tensor, w_q: Tensor, bias: Optional[Tensor], y_state: Optio
         _lib.check(L.hif8_linear_fwd_wq(a.data_ptr(), w_q.data_ptr(), b_ptr, y.data_ptr(), M, N, K, s),
                    "hif8_linear_fwd_wq")
     else:
-        _lib.check(L.hif8_linear_fwd_wq_gelu_amax(a.data_ptr(), w_q.data_ptr(), b_ptr, y.data_ptr(), M, N, K,
-                                                  float(scale_max), y_state.ptr, s), "hif8_linear_fwd_wq_gelu_amax")
+        _lib.check(L.hif8_linear_fwd_wq_gelu_stat(a.data_ptr(), w_q.data_ptr(), b_ptr, y.data_ptr(), M, N, K,
+                                                  float(scale_max), y_state.ptr, s), "hif8_linear_fwd_wq_gelu_stat")
     return y
 
 
@@ -390,16 +390,18 @@ def linear_fwd_grouped(a: Tensor, gw: GroupedWeight) -> "List[Tensor]":
     return ys
 
 
-def linear_fwd_gelu_amax(a: Tensor, w: PackedWeight, bias: Optional[Tensor], y_state: QuantState,
+def linear_fwd_gelu_stat(a: Tensor, w: PackedWeight, bias: Optional[Tensor], y_state: QuantState,
                          scale_max: float) -> Tensor:
-    """hif8_linear_fwd_gelu_amax: y = gelu_tanh(x_q @ w_q^T + bias) in bf16 (bf16 x_q), with amax|y|
-    and its scale for ``scale_max`` left in ``y_state``."""
+    """hif8_linear_fwd[_wq]_gelu_stat: y = x_q @ w_q^T + bias in bf16 (bf16 x_q), with the GELU
+    statistic of y in ``y_state``: amax|GELU(y)| and its scale for ``scale_max`` when max y settles
+    it, else the state is pending.  ``gelu_fake_quant(y, y_state, scale_max)`` then gives the next
+    linear's x_q of GELU(y)."""
     M, K = a.shape
     N = w.shape[0]
     if w.shape[1] != K:
         raise ValueError(f"in_features mismatch: x has {K}, weight has {w.shape[1]}")
     if a.dtype != torch.bfloat16:
-        raise TypeError("the GELU + amax epilogue takes bf16 activations")
+        raise TypeError("the GELU-statistic epilogue takes bf16 activations")
     if decode_once(M):
         return linear_fwd_wq(a, w.dequantize(torch.bfloat16), bias, y_state, scale_max)
     y = torch.empty((M, N), dtype=torch.bfloat16, device=a.device)
@@ -407,10 +409,36 @@ def linear_fwd_gelu_amax(a: Tensor, w: PackedWeight, bias: Optional[Tensor], y_s
     if bias is not None:
         bias = bias.detach().to(torch.bfloat16).contiguous()
         b_ptr = bias.data_ptr()
-    _lib.check(_lib.load().hif8_linear_fwd_gelu_amax(a.data_ptr(), w.codes.data_ptr(), w.state.ptr, b_ptr,
+    _lib.check(_lib.load().hif8_linear_fwd_gelu_stat(a.data_ptr(), w.codes.data_ptr(), w.state.ptr, b_ptr,
                                                      y.data_ptr(), M, N, K, float(scale_max), y_state.ptr,
-                                                     _lib.stream_ptr(a.device)), "hif8_linear_fwd_gelu_amax")
+                                                     _lib.stream_ptr(a.device)), "hif8_linear_fwd_gelu_stat")
     return y
+
+
+def gelu_absmax_scale(y: Tensor, scale_max: float, state: QuantState) -> QuantState:
+    """amax|GELU(y)| and its scale into ``state`` (hif8_gelu_absmax_scale) for a bf16 y."""
+    _lib.require_gpu_tensor(y, "y")
+    if y.dtype != torch.bfloat16:
+        raise TypeError("gelu_absmax_scale takes a bfloat16 tensor")
+    y = _aligned(y)
+    _lib.check(_lib.load().hif8_gelu_absmax_scale(y.data_ptr(), y.numel(), float(scale_max), state.ptr,
+                                                  _lib.stream_ptr(y.device)), "hif8_gelu_absmax_scale")
+    return state
+
+
+def gelu_fake_quant(y: Tensor, state: QuantState, scale_max: float = 15.0, semantics: int = _lib.SEM_NPU) -> Tensor:
+    """``_quant(GELU(y))[0]`` in bf16 without writing GELU(y) (hif8_gelu_fake_quant), with the state
+    from ``linear_fwd_gelu_stat`` or ``gelu_absmax_scale`` (a pending state is completed first)."""
+    _lib.require_gpu_tensor(y, "y")
+    if y.dtype != torch.bfloat16:
+        raise TypeError("gelu_fake_quant takes a bfloat16 tensor")
+    y = _aligned(y)
+    out = torch.empty_like(y)
+    if y.numel():
+        _lib.check(_lib.load().hif8_gelu_fake_quant(y.data_ptr(), y.numel(), state.ptr, float(scale_max),
+                                                    out.data_ptr(), semantics, _lib.stream_ptr(y.device)),
+                   "hif8_gelu_fake_quant")
+    return out
 
 
 def quantize_activation(x2: Tensor, scale_max: float, a_format: str, as_f32: bool = False):

@@ -75,21 +75,26 @@ def _amax_bits(y):
 
 
 @pytest.mark.parametrize("M,K,N", [(300, 256, 264), (2048, 1536, 8960)])
-def test_wq_gelu_amax_matches_fused(pkg, M, K, N):
+def test_wq_gelu_stat_matches_fused(pkg, M, K, N):
+    """The GELU-statistic epilogue on both routes: the plain output, bit for bit, and the same
+    settled state (amax of GELU(y) and its scale)."""
     a, fmt, st, packed, b = operands(pkg, M, K, N, 7 * M + N)
     s_f, s_w = pkg.QuantState(DEV), pkg.QuantState(DEV)
     old = pkg.hif8_linear.GEMM_ROUTE
     try:
         pkg.hif8_linear.GEMM_ROUTE = "fused"
-        want = pkg.linear_fwd_gelu_amax(a, packed, b, s_f, 15.0)
+        want = pkg.linear_fwd_gelu_stat(a, packed, b, s_f, 15.0)
         pkg.hif8_linear.GEMM_ROUTE = "decode_once"
-        got = pkg.linear_fwd_gelu_amax(a, packed, b, s_w, 15.0)
+        got = pkg.linear_fwd_gelu_stat(a, packed, b, s_w, 15.0)
+        plain = pkg.linear_fwd(a, fmt, st, packed, b)
     finally:
         pkg.hif8_linear.GEMM_ROUTE = old
     assert torch.equal(got.view(torch.int16), want.view(torch.int16))
-    # each state holds the amax of its own output
-    assert s_f.read()[0] == _amax_bits(want)
+    assert torch.equal(got.view(torch.int16), plain.view(torch.int16))
     assert s_f.read() == s_w.read()
+    # the amax the statistic settled is the one a full pass over GELU(y) finds
+    s_p = pkg.gelu_absmax_scale(got, 15.0, pkg.QuantState(DEV))
+    assert s_f.read() == s_p.read()
 
 
 def test_wq_grouped_equals_single(pkg):
