@@ -181,7 +181,9 @@ int hif8_linear_fwd_grouped(const void *a, const uint8_t *w_codes, const void *c
  * down-projection's _quant (hif8_linear.py:45-48) of the GELU layer's output is then
  * hif8_gelu_fake_quant(y, y_state), which applies GELU itself: the GELU output is never
  * written and no amax pass runs unless the state is pending.  y_state must have been
- * initialised (hif8_state_init); shapes as hif8_linear_fwd.
+ * initialised (hif8_state_init); shapes as hif8_linear_fwd.  Two launches on the stream: the GEMM
+ * (each wave folds its maximum with one relaxed atomic) and a one-workgroup kernel that settles
+ * y_state from it.
  * No single reference function: it fuses three reference steps. */
 int hif8_linear_fwd_gelu_stat(const void *a, const uint8_t *w_codes, const void *w_state, const uint16_t *bias,
                               uint16_t *y, int64_t M, int64_t N, int64_t K, float scale_max, void *y_state,
@@ -194,7 +196,7 @@ int hif8_linear_fwd_gelu_stat(const void *a, const uint8_t *w_codes, const void 
  * packed codes with the weight's state, into a caller buffer, once per call.  The fused kernel
  * decodes each weight element once per 256-row tile of x (M/256 times); this route decodes it
  * once and streams bf16 W.  The same 16x16x32 MFMA products in the same k order: the outputs
- * equal hif8_linear_fwd's bit for bit.  Shapes, alignment and the GELU + amax and grouped variants
+ * equal hif8_linear_fwd's bit for bit.  Shapes, alignment and the GELU-statistic and grouped variants
  * as for hif8_linear_fwd / _gelu_stat / _grouped (w_q concatenated along N for groups).
  * No counterpart of its own in the reference: it is F.linear on the dequantised operands. */
 int hif8_linear_fwd_wq(const uint16_t *a, const uint16_t *w_q, const uint16_t *bias, uint16_t *y, int64_t M,

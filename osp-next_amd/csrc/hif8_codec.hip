@@ -424,6 +424,13 @@ __global__ __launch_bounds__(kTPB) void k_gelu_absmax(const uint16_t *__restrict
     fold_amax(st, m, gridDim.x, kBF16, smax, red + kTPB / 64);
 }
 
+// The state after a GELU-statistic GEMM: amax|GELU(y)| from max y, or pending.
+__global__ __launch_bounds__(kTPB) void k_gelu_stat_settle(State *__restrict__ st, float smax)
+{
+    __shared__ uint32_t lds[2];
+    gelu_stat_settle(st, smax, lds);
+}
+
 // Unscaled qdq of a bf16 tensor with QFuncs/hif8.py evaluated in bf16 arithmetic (the
 // HIF8_SEM_TORCH_BF16 route of hif8_quant_bf16): elementwise, off the linear's path.
 __global__ __launch_bounds__(kTPB) void k_qdq_torch_bf16(const uint16_t *__restrict__ x, uint16_t *__restrict__ y,
@@ -561,6 +568,12 @@ static int cu_count()
 static inline bool aligned16(const void *p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
 
 static int last_launch() { return hipGetLastError() == hipSuccess ? HIF8_OK : HIF8_ERR_HIP; }
+
+int launch_gelu_stat_settle(State *y_st, float y_smax, hif8_stream_t stream)
+{
+    hipLaunchKernelGGL(k_gelu_stat_settle, dim3(1), dim3(kTPB), 0, (hipStream_t)stream, y_st, y_smax);
+    return hipGetLastError() == hipSuccess ? HIF8_OK : HIF8_ERR_HIP;
+}
 
 }  // namespace hif8
 

@@ -48,29 +48,29 @@ __device__ __forceinline__ uint32_t gelu_bf16(uint32_t b) { return gelu_bf16x2(b
 
 // The GELU statistic of a set of bf16 outputs: the largest non-negative value (bf16 bits, 0 when
 // there is none) or kGeluNonFinite when any output is Inf or NaN (GELU(-Inf) and GELU(NaN) are
-// NaN: the amax then needs the full pass).  Accumulated two outputs per 32-bit word:
-//   spos: packed signed 16-bit max of the raw bits -- a negative bf16 is a negative int16, a
-//         non-negative one keeps its numeric order;
-//   smag: packed unsigned 16-bit max of the magnitude bits, which reaches 0x7F80 for Inf or NaN.
+// NaN: the amax then needs the full pass).  Accumulated two outputs per 32-bit word, one packed
+// max each, on the raw bits:
+//   smax_i: signed 16-bit max -- a negative bf16 is a negative int16 and a non-negative one keeps
+//           its numeric order, so this is the largest non-negative output, and +Inf / +NaN
+//           (0x7F80 .. 0x7FFF) are the largest int16 values of all;
+//   smax_u: unsigned 16-bit max -- -Inf / -NaN (0xFF80 .. 0xFFFF) are the largest uint16 values.
 constexpr uint32_t kGeluNonFinite = 0x10000u;
-__device__ __forceinline__ void gelu_stat_pk(uint32_t &spos, uint32_t &smag, uint32_t w0, uint32_t w1)
+__device__ __forceinline__ void gelu_stat_pk(uint32_t &smax_i, uint32_t &smax_u, uint32_t w0, uint32_t w1)
 {
     typedef short i16x2 __attribute__((ext_vector_type(2)));
     typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
     const i16x2 p = __builtin_elementwise_max(__builtin_bit_cast(i16x2, w0), __builtin_bit_cast(i16x2, w1));
-    spos = __builtin_bit_cast(uint32_t, __builtin_elementwise_max(__builtin_bit_cast(i16x2, spos), p));
-    const u16x2 q = __builtin_elementwise_max(__builtin_bit_cast(u16x2, w0 & 0x7FFF7FFFu),
-                                              __builtin_bit_cast(u16x2, w1 & 0x7FFF7FFFu));
-    smag = __builtin_bit_cast(uint32_t, __builtin_elementwise_max(__builtin_bit_cast(u16x2, smag), q));
+    smax_i = __builtin_bit_cast(uint32_t, __builtin_elementwise_max(__builtin_bit_cast(i16x2, smax_i), p));
+    const u16x2 q = __builtin_elementwise_max(__builtin_bit_cast(u16x2, w0), __builtin_bit_cast(u16x2, w1));
+    smax_u = __builtin_bit_cast(uint32_t, __builtin_elementwise_max(__builtin_bit_cast(u16x2, smax_u), q));
 }
-// One lane's statistic from its packed maxima (as an unsigned value: maxima of these over lanes and
-// workgroups are the statistic of the union).
-__device__ __forceinline__ uint32_t gelu_stat_final(uint32_t spos, uint32_t smag)
+// One lane's statistic from its packed maxima (both start at 0; as an unsigned value, maxima of
+// these over lanes and workgroups are the statistic of the union).
+__device__ __forceinline__ uint32_t gelu_stat_final(uint32_t smax_i, uint32_t smax_u)
 {
-    const uint32_t mag = max(smag & 0xFFFFu, smag >> 16);
-    if (mag >= 0x7F80u) return kGeluNonFinite;
-    const int lo = int(short(spos & 0xFFFFu)), hi = int(short(spos >> 16));
+    const int lo = int(short(smax_i & 0xFFFFu)), hi = int(short(smax_i >> 16));
     const int p = lo > hi ? lo : hi;
+    if (p >= 0x7F80 || max(smax_u & 0xFFFFu, smax_u >> 16) >= 0xFF80u) return kGeluNonFinite;
     return p > 0 ? uint32_t(p) : 0u;
 }
 
@@ -79,24 +79,27 @@ __device__ __forceinline__ uint32_t gelu_stat_final(uint32_t spos, uint32_t smag
 // rounds above 0x3E2E the largest |GELU(y)| over a tensor is GELU(ymax) itself.
 constexpr uint32_t kGeluNegAmaxBits = 0x3E2Eu;
 
-// Fold one workgroup's statistic (the max of gelu_stat_final over its lanes, thread 0's value) into
-// st.  The last of nwg workgroups resets the accumulators and, when max y settles the amax, writes
-// amax = GELU(max y), the scale for smax, the flags and the decode tables, as hif8_absmax_scale
-// of GELU(y) would; otherwise it marks the state pending (the down-projection's quantisation
-// then runs the amax pass first).  Called by all 256 threads; lds is three words of LDS.
-__device__ __forceinline__ void fold_gelu_stat(State *st, uint32_t m, uint32_t nwg, float smax, uint32_t *lds)
+// Fold one wave's statistic (the max of gelu_stat_final over its lanes) into st->amax_acc: a
+// relaxed atomic max with no return value and no fence, so the wave ends without waiting for its
+// output stores to complete (a release at agent scope would wait for them and write back the
+// XCD's L2 in every workgroup).  gelu_stat_settle reads the maximum in a kernel launched after the
+// GEMM on the same stream.
+__device__ __forceinline__ void fold_gelu_stat(State *st, uint32_t m)
+{
+    __hip_atomic_fetch_max(&st->amax_acc, m, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Settle the state after a GEMM that folded the statistic of its output y into st (one workgroup
+// of 256 threads): reset the accumulator and, when max y settles the amax, write
+// amax = GELU(max y), the scale for smax, the flags and the decode tables, as hif8_absmax_scale of
+// GELU(y) would; otherwise mark the state pending (the down-projection's quantisation then runs
+// the amax pass first).  lds is two words of LDS.
+__device__ __forceinline__ void gelu_stat_settle(State *st, float smax, uint32_t *lds)
 {
     const uint32_t tid = threadIdx.x;
     if (tid == 0) {
-        __hip_atomic_fetch_max(&st->amax_acc, m, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        const uint32_t prev = __hip_atomic_fetch_add(&st->counter, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-        lds[0] = (prev == nwg - 1) ? 1u : 0u;
-    }
-    __syncthreads();
-    if (!lds[0]) return;
-    if (tid == 0) {
-        const uint32_t a = __hip_atomic_exchange(&st->amax_acc, 0u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-        __hip_atomic_store(&st->counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        const uint32_t a = st->amax_acc;
+        st->amax_acc = 0u;
         uint32_t g = 0;
         bool settled = false;
         if (a < kGeluNonFinite) {
@@ -112,11 +115,11 @@ __device__ __forceinline__ void fold_gelu_stat(State *st, uint32_t m, uint32_t n
         st->finite = fast ? 1u : 0u;
         st->dtype = uint32_t(kBF16);
         st->pending = settled ? 0u : 1u;
-        lds[1] = settled ? 1u : 0u;
-        lds[2] = f2u(s);
+        lds[0] = settled ? 1u : 0u;
+        lds[1] = f2u(s);
     }
     __syncthreads();
-    if (lds[1]) fill_luts(st, u2f(lds[2]), tid);
+    if (lds[0]) fill_luts(st, u2f(lds[1]), tid);
 }
 
 }  // namespace hif8

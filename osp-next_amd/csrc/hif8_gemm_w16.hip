@@ -153,14 +153,14 @@ template <int SET> __device__ __forceinline__ void tie_set(Ctx &c)
 #include "hif8_gemm_schedule_w16.inc"
 
 // EPI 0: y = rnd(acc + bias).  EPI 1: the same y, and the GELU statistic of y (its max, or a
-// non-finite flag) folded into y_st, which then holds amax|GELU(y)| and its scale for y_smax
-// when max y settles it (hif8_gelu_dev.h).  The output features are G.n groups, each with its
-// output buffer.
+// non-finite flag) folded into y_st's accumulator; the settle kernel launched after it turns that
+// into amax|GELU(y)| and its scale when max y settles it (hif8_gelu_dev.h).  The output features
+// are G.n groups, each with its output buffer.
 template <int EPI>
 __global__ __launch_bounds__(kThreads, 1) void k_linear_w16(const uint16_t *__restrict__ X, const uint16_t *__restrict__ Wq,
                                                             const Groups G, const uint16_t *__restrict__ bias,
                                                             int M, int N, int K, int tiles_m, int tiles_n,
-                                                            int group_m, State *__restrict__ y_st, float y_smax)
+                                                            int group_m, State *__restrict__ y_st)
 {
     __shared__ __attribute__((aligned(1024))) uint8_t smem[kLds];
     ASMV("; lds base %0" ::"v"(uint32_t(uintptr_t(smem))) : "memory");
@@ -302,7 +302,7 @@ __global__ __launch_bounds__(kThreads, 1) void k_linear_w16(const uint16_t *__re
     }
     __syncthreads();
     // EPI 1: packed running maxima of the in-range outputs this lane stores (the GELU statistic)
-    uint32_t spos = 0, smag = 0;
+    uint32_t smax_i = 0, smax_u = 0;
     {
         const uint32_t colb = (lane & 31u) * 16u, h = lane >> 5;
         const int n = n0 + int(colb / 2u);
@@ -320,29 +320,25 @@ __global__ __launch_bounds__(kThreads, 1) void k_linear_w16(const uint16_t *__re
                 if (m < M && n - col0 < ycols) {
                     __builtin_nontemporal_store(v[it], (u32x4 *)(Y + size_t(m) * size_t(ycols) + (n - col0)));
                     if (EPI == 1) {
-                        gelu_stat_pk(spos, smag, v[it][0], v[it][1]);
-                        gelu_stat_pk(spos, smag, v[it][2], v[it][3]);
+                        gelu_stat_pk(smax_i, smax_u, v[it][0], v[it][1]);
+                        gelu_stat_pk(smax_i, smax_u, v[it][2], v[it][3]);
                     }
                 }
             }
         }
     }
     if (EPI == 1) {
-        uint32_t ystat = gelu_stat_final(spos, smag);
+        uint32_t ystat = gelu_stat_final(smax_i, smax_u);
         for (int o = 32; o > 0; o >>= 1) ystat = max(ystat, (uint32_t)__shfl_xor((int)ystat, o, 64));
-        uint32_t *red = (uint32_t *)smem;  // the staging rows are read: reuse after the barrier
-        __syncthreads();
-        if (lane == 0) red[c.wave] = ystat;
-        __syncthreads();
-        ystat = max(max(red[0], red[1]), max(red[2], red[3]));
-        fold_gelu_stat(y_st, ystat, gridDim.x, y_smax, red + 4);
+        if (lane == 0) fold_gelu_stat(y_st, ystat);
     }
 }
 
 }  // namespace w16
 
 // Shapes: K % 64 == 0, N % 8 == 0, 16-byte aligned X, W_q and Y, 8-byte aligned bias (checked
-// by the caller).  M, N < 2^31, K < 2^22.  y_st != NULL selects the GELU-statistic epilogue.
+// by the caller).  M, N < 2^31, K < 2^22.  y_st != NULL selects the GELU-statistic epilogue and the
+// settle kernel (scale for y_smax).
 static int launch_w16(const uint16_t *x, const uint16_t *w_q, const Groups &g, const uint16_t *bias, int64_t M,
                       int64_t N, int64_t K, hif8_stream_t stream, State *y_st, float y_smax)
 {
@@ -355,11 +351,12 @@ static int launch_w16(const uint16_t *x, const uint16_t *w_q, const Groups &g, c
     if (tiles >= (int64_t(1) << 31)) return HIF8_ERR_SHAPE;
     if (y_st)
         hipLaunchKernelGGL(w16::k_linear_w16<1>, dim3(unsigned(tiles)), dim3(w16::kThreads), 0, s, x, w_q, g, bias,
-                           int(M), int(N), int(K), tiles_m, tiles_n, group_m, y_st, y_smax);
+                           int(M), int(N), int(K), tiles_m, tiles_n, group_m, y_st);
     else
         hipLaunchKernelGGL(w16::k_linear_w16<0>, dim3(unsigned(tiles)), dim3(w16::kThreads), 0, s, x, w_q, g, bias,
-                           int(M), int(N), int(K), tiles_m, tiles_n, group_m, (State *)nullptr, 0.0f);
-    return hipGetLastError() == hipSuccess ? HIF8_OK : HIF8_ERR_HIP;
+                           int(M), int(N), int(K), tiles_m, tiles_n, group_m, (State *)nullptr);
+    if (hipGetLastError() != hipSuccess) return HIF8_ERR_HIP;
+    return y_st ? launch_gelu_stat_settle(y_st, y_smax, stream) : HIF8_OK;
 }
 
 int launch_linear_w16(const uint16_t *x, const uint16_t *w_q, const uint16_t *bias, uint16_t *y, int64_t M,

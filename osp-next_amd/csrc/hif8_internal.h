@@ -43,7 +43,8 @@ struct Groups {
 
 // Fused GEMM for bf16 activations (hif8_gemm_dtl.hip); the caller has checked shapes and
 // alignment as hif8_linear_fwd documents.  With y_st, the epilogue also folds the GELU
-// statistic of its output (max y, hif8_gelu_dev.h) into y_st.
+// statistic of its output (max y, hif8_gelu_dev.h) into y_st, and the settle kernel
+// (launch_gelu_stat_settle) follows it on the stream.
 int launch_linear_dtl(const uint16_t *x, const uint8_t *w_codes, const State *w_st, const uint16_t *bias,
                       uint16_t *y, int64_t M, int64_t N, int64_t K, hif8_stream_t stream, State *y_st = nullptr,
                       float y_smax = 0.0f);
@@ -55,5 +56,8 @@ int launch_linear_w16_groups(const uint16_t *x, const uint16_t *w_q, const Group
 // The grouped form: N is the total of the groups' features.
 int launch_linear_dtl_groups(const uint16_t *x, const uint8_t *w_codes, const Groups &g, const uint16_t *bias,
                              int64_t M, int64_t N, int64_t K, hif8_stream_t stream);
+
+// One workgroup that settles y_st after a GELU-statistic GEMM (gelu_stat_settle, hif8_codec.hip).
+int launch_gelu_stat_settle(State *y_st, float y_smax, hif8_stream_t stream);
 
 }  // namespace hif8
