@@ -201,6 +201,21 @@ int hif8_linear_fwd_gelu_stat(const void *a, const uint8_t *w_codes, const void 
  * No counterpart of its own in the reference: it is F.linear on the dequantised operands. */
 int hif8_linear_fwd_wq(const uint16_t *a, const uint16_t *w_q, const uint16_t *bias, uint16_t *y, int64_t M,
                        int64_t N, int64_t K, hif8_stream_t stream);
+
+/* hif8_linear_fwd_wq with a split tail, for the backward's GEMMs (dgrad on the decode-once
+ * route, wgrad): when a grid of fewer than 8 waves of 256 x 256 output tiles (one workgroup per
+ * CU) ends in a partial wave that would leave over half the CUs idle, each of those tail tiles
+ * is computed as 2-8 workgroups over
+ * consecutive k ranges (at least 8 k-steps each), whose fp32 sums a second kernel adds in a fixed
+ * order and rounds once: deterministic, and within fp32 rounding of the unsplit sums (the tail
+ * tiles' outputs may differ from hif8_linear_fwd_wq's in the last bf16 bit).  The workspace is
+ * hif8_linear_split_workspace_bytes(M, N, K) bytes of device memory, 16-byte aligned (at most
+ * 64 MiB on 256 CUs; 0 when no split applies, e.g. whole waves); with workspace NULL every tile
+ * is computed whole.  Shapes and alignment as hif8_linear_fwd_wq.  No counterpart of its own in
+ * the reference: F.linear's and the backward matmuls' tiling is the library's choice. */
+int64_t hif8_linear_split_workspace_bytes(int64_t M, int64_t N, int64_t K);
+int hif8_linear_fwd_wq_split(const uint16_t *a, const uint16_t *w_q, const uint16_t *bias, uint16_t *y, int64_t M,
+                             int64_t N, int64_t K, void *workspace, int64_t workspace_bytes, hif8_stream_t stream);
 int hif8_linear_fwd_wq_gelu_stat(const uint16_t *a, const uint16_t *w_q, const uint16_t *bias, uint16_t *y,
                                  int64_t M, int64_t N, int64_t K, float scale_max, void *y_state,
                                  hif8_stream_t stream);
@@ -238,13 +253,24 @@ int hif8_transpose_codes(const uint8_t *codes, int64_t rows, int64_t cols, uint8
 /* wgrad support.  The reference's weight gradient is grad_q^T @ x_q over the flattened tokens
  * (hif8_linear.py:100-105), a product whose reduction runs over the rows of both operands.  The
  * decode-free GEMM reduces over its operands' rows of contiguous k, so wgrad runs
- * hif8_linear_fwd_wq(grad_q^T, x_q^T) on the two operands transposed, with the token dimension
+ * hif8_linear_wgrad(grad_q^T, x_q^T) on the two operands transposed, with the token dimension
  * padded with zeros to a multiple of 64 (zeros add nothing to the sums).  This entry point writes
  * out[c][r] = x[r][c] for r < rows and 0 for rows <= r < rows_pad: x bf16 [rows, cols],
  * out bf16 [cols, rows_pad].  Any shape and alignment; 16-byte aligned pointers, cols % 8 == 0
  * and rows_pad % 8 == 0 take the vector path.  No counterpart of its own in the reference. */
 int hif8_transpose_bf16(const uint16_t *x, int64_t rows, int64_t cols, int64_t rows_pad, uint16_t *out,
                         hif8_stream_t stream);
+
+/* The weight gradient of _HIF8LinearFunction.backward, grad_W = grad_q^T @ x_q
+ * (hif8_linear.py:100-105), on the transposed operands hif8_transpose_bf16 writes:
+ *   dw[n_out, k_in] = g_t[n_out, tokens_pad] . x_t[k_in, tokens_pad]^T     (fp32 sums, bf16 out)
+ * with tokens_pad % 64 == 0 (zero-padded tokens), k_in % 8 == 0, 16-byte aligned pointers,
+ * tokens_pad < 2^22: hif8_linear_fwd_wq_split(g_t, x_t, NULL, dw, n_out, k_in, tokens_pad, ...),
+ * whose split tail matters most here (1080 tiles over 75648 tokens for the 14B FFN-up weight).
+ * The sums' order differs from the reference's bf16 matmul (it does in any case).  No
+ * counterpart of its own in the reference. */
+int hif8_linear_wgrad(const uint16_t *g_t, const uint16_t *x_t, uint16_t *dw, int64_t n_out, int64_t k_in,
+                      int64_t tokens_pad, void *workspace, int64_t workspace_bytes, hif8_stream_t stream);
 
 /* ---------------------------------------------------------------------------
  * Producer fusion for the modulated LayerNorm in front of the self-attention q/k/v

@@ -45,6 +45,7 @@ from .hif8_linear import (  # noqa: F401
     linear_fwd_grouped,
     linear_fwd_wq,
     linear_wgrad,
+    linear_fwd_wq_split,
     transpose_bf16,
     wgrad_ok,
 )
@@ -81,5 +82,5 @@ __all__ = [
     "save_packed", "load_packed", "pack_state_dict", "packed_from_codes", "fused_shape_ok", "linear_any",
     "linear_fwd_gelu_stat", "gelu_absmax_scale", "gelu_fake_quant", "HIF8FFN", "WanLayerNorm", "modulate", "modulated_norm_quant", "affine_norm_quant",
     "qkv_from_modulated_norm", "modulated_norm_quant_static", "GroupedWeight", "grouped_ok", "linear_fwd_grouped", "grouped_weight",
-    "dit", "OSPNextAttentionBlock", "OSPNextBlocks", "linear_fwd_wq", "linear_wgrad", "transpose_bf16", "wgrad_ok",
+    "dit", "OSPNextAttentionBlock", "OSPNextBlocks", "linear_fwd_wq", "linear_fwd_wq_split", "linear_wgrad", "transpose_bf16", "wgrad_ok",
 ]

@@ -38,6 +38,9 @@ SIGNATURES = {
     "hif8_linear_fwd": (_i, [_p, _p, _p, _p, _p, _i64, _i64, _i64, _p]),
     "hif8_transpose_codes": (_i, [_p, _i64, _i64, _p, _p]),
     "hif8_transpose_bf16": (_i, [_p, _i64, _i64, _i64, _p, _p]),
+    "hif8_linear_split_workspace_bytes": (_i64, [_i64, _i64, _i64]),
+    "hif8_linear_fwd_wq_split": (_i, [_p, _p, _p, _p, _i64, _i64, _i64, _p, _i64, _p]),
+    "hif8_linear_wgrad": (_i, [_p, _p, _p, _i64, _i64, _i64, _p, _i64, _p]),
     "hif8_linear_fwd_gelu_stat": (_i, [_p, _p, _p, _p, _p, _i64, _i64, _i64, _f, _p, _p]),
     "hif8_gelu_absmax_scale": (_i, [_p, _i64, _f, _p, _p]),
     "hif8_gelu_fake_quant": (_i, [_p, _i64, _p, _f, _p, _i, _p]),

@@ -156,11 +156,28 @@ template <int SET> __device__ __forceinline__ void tie_set(Ctx &c)
 // non-finite flag) folded into y_st's accumulator; the settle kernel launched after it turns that
 // into amax|GELU(y)| and its scale when max y settles it (hif8_gelu_dev.h).  The output features
 // are G.n groups, each with its output buffer.
+// Tile t of the order: groups of group_m m-tiles, n-tiles outer within a group.
+__device__ __forceinline__ void tile_origin(int t, int tiles_m, int tiles_n, int group_m, int &m0, int &n0)
+{
+    const int group = t / (group_m * tiles_n);
+    const int first_m = group * group_m;
+    const int gm = (tiles_m - first_m) < group_m ? (tiles_m - first_m) : group_m;
+    const int within = t - group * group_m * tiles_n;
+    m0 = (first_m + within % gm) * kTile;
+    n0 = (within / gm) * kTile;
+}
+
+// EPI 2, the split tail: workgroup w computes k range w % splits (consecutive k-steps) of tile
+// tile0 + w / splits and writes its fp32 sums to part (256 KB per workgroup, in the accumulators'
+// lane order) for k_split_reduce.  (A separate instantiation: in the same kernel as the bf16
+// epilogue, the register allocator moved all accumulators to VGPRs ahead of the branch and
+// spilled.)
 template <int EPI>
 __global__ __launch_bounds__(kThreads, 1) void k_linear_w16(const uint16_t *__restrict__ X, const uint16_t *__restrict__ Wq,
                                                             const Groups G, const uint16_t *__restrict__ bias,
                                                             int M, int N, int K, int tiles_m, int tiles_n,
-                                                            int group_m, State *__restrict__ y_st)
+                                                            int group_m, State *__restrict__ y_st, int tile0,
+                                                            int splits, float *__restrict__ part)
 {
     __shared__ __attribute__((aligned(1024))) uint8_t smem[kLds];
     ASMV("; lds base %0" ::"v"(uint32_t(uintptr_t(smem))) : "memory");
@@ -169,14 +186,16 @@ __global__ __launch_bounds__(kThreads, 1) void k_linear_w16(const uint16_t *__re
     c.wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t r = lane & 15u, g = lane >> 4;
 
-    // tile order: groups of group_m m-tiles, n-tiles outer within a group
-    const int t = blockIdx.x;
-    const int group = t / (group_m * tiles_n);
-    const int first_m = group * group_m;
-    const int gm = (tiles_m - first_m) < group_m ? (tiles_m - first_m) : group_m;
-    const int within = t - group * group_m * tiles_n;
-    const int m0 = (first_m + within % gm) * kTile;
-    const int n0 = (within / gm) * kTile;
+    int t = blockIdx.x;
+    int nk = K / kBK, kb = 0;
+    if (EPI == 2) {
+        t = tile0 + int(blockIdx.x) / splits;
+        const int per = (nk + splits - 1) / splits;
+        kb = (int(blockIdx.x) % splits) * per;
+        nk = (nk - kb < per ? nk - kb : per);
+    }
+    int m0, n0;
+    tile_origin(t, tiles_m, tiles_n, group_m, m0, n0);
     int gi = 0;
     while (gi + 1 < G.n && n0 / kTile >= G.tile_end[gi]) ++gi;
     uint16_t *__restrict__ Y = G.y[gi];
@@ -184,12 +203,14 @@ __global__ __launch_bounds__(kThreads, 1) void k_linear_w16(const uint16_t *__re
     const int ycols = G.cols[gi];
 
     {
-        const uint64_t xa = uint64_t(X) + uint64_t(m0) * uint64_t(K) * 2u;
+        // the buffers start at k-step kb of row 0; rows past M or N lie past the range
+        const uint32_t kofs = uint32_t(kb) * uint32_t(kBK) * 2u;
+        const uint64_t xa = uint64_t(X) + uint64_t(m0) * uint64_t(K) * 2u + kofs;
         const uint32_t xrows = uint32_t(M - m0 < kTile ? M - m0 : kTile);
-        c.rx = u32x4{uint32_t(xa), uint32_t(xa >> 32), xrows * uint32_t(K) * 2u, 0x00020000u};
-        const uint64_t wa = uint64_t(Wq) + uint64_t(n0) * uint64_t(K) * 2u;
+        c.rx = u32x4{uint32_t(xa), uint32_t(xa >> 32), xrows * uint32_t(K) * 2u - kofs, 0x00020000u};
+        const uint64_t wa = uint64_t(Wq) + uint64_t(n0) * uint64_t(K) * 2u + kofs;
         const uint32_t wrows = uint32_t(N - n0 < kTile ? N - n0 : kTile);
-        c.rw = u32x4{uint32_t(wa), uint32_t(wa >> 32), wrows * uint32_t(K) * 2u, 0x00020000u};
+        c.rw = u32x4{uint32_t(wa), uint32_t(wa >> 32), wrows * uint32_t(K) * 2u - kofs, 0x00020000u};
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             c.rx[i] = __builtin_amdgcn_readfirstlane(c.rx[i]);
@@ -218,7 +239,6 @@ __global__ __launch_bounds__(kThreads, 1) void k_linear_w16(const uint16_t *__re
         c.wb[p] = (wn + r) * 128u + ch;
     }
 
-    const int nk = K / kBK;
     // Prologue: X and W of k-steps 0 and 1 into stages 0..3; wait for k-step 0.
     c.ex = c.rx;
     c.ew = c.rw;
@@ -270,6 +290,16 @@ __global__ __launch_bounds__(kThreads, 1) void k_linear_w16(const uint16_t *__re
     for (int i = 0; i < 8; ++i)
 #pragma unroll
         for (int j = 0; j < 8; ++j) ASMV("" : "+a"(c.acc[i][j]));
+
+    if (EPI == 2) {
+        // a k range of a split tile: the fp32 sums, 1 KB per store instruction
+        f32x4 *P = (f32x4 *)part + size_t(blockIdx.x) * 16384u + c.wave * 4096u + lane;
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+#pragma unroll
+            for (int j = 0; j < 8; ++j) P[(i * 8 + j) * 64] = c.acc[i][j];
+        return;
+    }
 
     // Epilogue.  acc[i][j] lane (r, g), element e: D[n][m] with n = wn + 16i + 4g + e,
     // m = wm + 16j + r.  Rows go to LDS (padded), then each wave stores 2 rows x 512 B per
@@ -334,13 +364,96 @@ __global__ __launch_bounds__(kThreads, 1) void k_linear_w16(const uint16_t *__re
     }
 }
 
+// The split tiles' outputs: workgroup b sums the splits fp32 partials of tile full_tiles + b in
+// split order (a fixed order: the result does not depend on timing), adds the bias, rounds to
+// bf16 and stores the in-range outputs.  One lane per 4 consecutive outputs of a row.
+__global__ __launch_bounds__(kThreads) void k_split_reduce(const float *__restrict__ part, int splits, int full_tiles,
+                                                            int tiles_m, int tiles_n, int group_m, int M, int N,
+                                                            const uint16_t *__restrict__ bias, uint16_t *__restrict__ Y)
+{
+    const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
+    const uint32_t r = lane & 15u, g = lane >> 4;
+    int m0, n0;
+    tile_origin(full_tiles + int(blockIdx.x), tiles_m, tiles_n, group_m, m0, n0);
+    const uint32_t wm = (wave & 1u) * 128u, wn = (wave >> 1) * 128u;
+    const f32x4 *P = (const f32x4 *)part + size_t(blockIdx.x) * size_t(splits) * 16384u + wave * 4096u + lane;
+    for (int i = 0; i < 8; ++i) {
+        const int n = n0 + int(wn) + i * 16 + int(4u * g);
+        if (n >= N) continue;
+        float b0 = 0.f, b1 = 0.f, b2 = 0.f, b3 = 0.f;
+        if (bias) {
+            const uint2 bb = *(const uint2 *)(bias + n);
+            b0 = __builtin_bit_cast(float, bb.x << 16);
+            b1 = __builtin_bit_cast(float, bb.x & 0xFFFF0000u);
+            b2 = __builtin_bit_cast(float, bb.y << 16);
+            b3 = __builtin_bit_cast(float, bb.y & 0xFFFF0000u);
+        }
+        for (int j = 0; j < 8; ++j) {
+            const int m = m0 + int(wm) + j * 16 + int(r);
+            if (m >= M) continue;
+            f32x4 a = P[(i * 8 + j) * 64];
+            for (int sp = 1; sp < splits; ++sp) {
+                const f32x4 q = P[size_t(sp) * 16384u + (i * 8 + j) * 64];
+                a[0] = a[0] + q[0];
+                a[1] = a[1] + q[1];
+                a[2] = a[2] + q[2];
+                a[3] = a[3] + q[3];
+            }
+            uint2 v;
+            v.x = f2bf_pk(a[0] + b0, a[1] + b1);
+            v.y = f2bf_pk(a[2] + b2, a[3] + b3);
+            *(uint2 *)(Y + size_t(m) * size_t(N) + n) = v;
+        }
+    }
+}
+
 }  // namespace w16
+
+static int cu_count()
+{
+    static int cus[64] = {0};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (cus[dev] == 0) {
+        int c = 0;
+        if (hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || c <= 0) c = 256;
+        cus[dev] = c;
+    }
+    return cus[dev];
+}
+
+// Split of the last, partial wave of tiles (one workgroup per CU): for grids of fewer than 8
+// waves whose tail (tiles % CUs) fills at most half the CUs, each tail tile runs as `splits`
+// workgroups over consecutive k ranges (at least 8 k-steps each), so the last wave takes about
+// 1/splits of a tile's time.  Measured on MI355X: the 14B FFN-up wgrad (1080 tiles, 4.2 waves)
+// 8.08-8.19 -> 7.22-7.26 ms; its dgrad (5920 tiles, 23.1 waves) 7.35 ms either way -- after
+// many waves the CUs' tile boundaries have drifted apart and the tail tiles start as CUs free up.
+struct SplitPlan {
+    int full;     // tiles computed whole
+    int tail;     // tiles computed in k ranges
+    int splits;   // k ranges per tail tile (1: no split)
+    int64_t bytes() const { return splits > 1 ? int64_t(tail) * splits * w16::kTile * w16::kTile * 4 : 0; }
+};
+static SplitPlan plan_split(int64_t tiles, int64_t K)
+{
+    const int cus = cu_count();
+    const int tail = int(tiles % cus);
+    const int64_t nk = K / w16::kBK;
+    SplitPlan p{int(tiles), 0, 1};
+    if (tiles < cus || tiles >= 8 * int64_t(cus) || tail == 0 || tail > cus / 2) return p;
+    int sp = cus / tail;
+    if (sp > 8) sp = 8;
+    while (sp > 1 && nk < 8 * int64_t(sp)) --sp;
+    if (sp < 2) return p;
+    return SplitPlan{int(tiles) - tail, tail, sp};
+}
 
 // Shapes: K % 64 == 0, N % 8 == 0, 16-byte aligned X, W_q and Y, 8-byte aligned bias (checked
 // by the caller).  M, N < 2^31, K < 2^22.  y_st != NULL selects the GELU-statistic epilogue and the
-// settle kernel (scale for y_smax).
+// settle kernel (scale for y_smax).  part != NULL (one output group, no y_st) splits the tail as
+// plan_split says, with part holding plan_split(...).bytes() bytes.
 static int launch_w16(const uint16_t *x, const uint16_t *w_q, const Groups &g, const uint16_t *bias, int64_t M,
-                      int64_t N, int64_t K, hif8_stream_t stream, State *y_st, float y_smax)
+                      int64_t N, int64_t K, hif8_stream_t stream, State *y_st, float y_smax, float *part = nullptr)
 {
     hipStream_t s = (hipStream_t)stream;
     if (K >= (int64_t(1) << 22)) return HIF8_ERR_SHAPE;
@@ -349,13 +462,30 @@ static int launch_w16(const uint16_t *x, const uint16_t *w_q, const Groups &g, c
     const int64_t tiles = int64_t(tiles_m) * tiles_n;
     const int group_m = tiles_n >= 32 ? w16::kGroupWide : w16::kGroupNarrow;
     if (tiles >= (int64_t(1) << 31)) return HIF8_ERR_SHAPE;
+    SplitPlan sp{int(tiles), 0, 1};
+    if (part) {
+        if (y_st || g.n != 1) return HIF8_ERR_ARG;
+        sp = plan_split(tiles, K);
+    }
     if (y_st)
-        hipLaunchKernelGGL(w16::k_linear_w16<1>, dim3(unsigned(tiles)), dim3(w16::kThreads), 0, s, x, w_q, g, bias,
-                           int(M), int(N), int(K), tiles_m, tiles_n, group_m, y_st);
-    else
-        hipLaunchKernelGGL(w16::k_linear_w16<0>, dim3(unsigned(tiles)), dim3(w16::kThreads), 0, s, x, w_q, g, bias,
-                           int(M), int(N), int(K), tiles_m, tiles_n, group_m, (State *)nullptr);
+        hipLaunchKernelGGL(w16::k_linear_w16<1>, dim3(unsigned(sp.full)), dim3(w16::kThreads), 0, s, x, w_q, g, bias,
+                           int(M), int(N), int(K), tiles_m, tiles_n, group_m, y_st, 0, 1, (float *)nullptr);
+    else if (sp.full > 0)
+        hipLaunchKernelGGL(w16::k_linear_w16<0>, dim3(unsigned(sp.full)), dim3(w16::kThreads), 0, s, x, w_q, g, bias,
+                           int(M), int(N), int(K), tiles_m, tiles_n, group_m, (State *)nullptr, 0, 1,
+                           (float *)nullptr);
     if (hipGetLastError() != hipSuccess) return HIF8_ERR_HIP;
+    if (sp.splits > 1) {
+        // after the whole tiles on the stream: they fill whole waves, so the split workgroups
+        // start as the last of them end
+        hipLaunchKernelGGL(w16::k_linear_w16<2>, dim3(unsigned(sp.tail * sp.splits)), dim3(w16::kThreads), 0, s, x,
+                           w_q, g, bias, int(M), int(N), int(K), tiles_m, tiles_n, group_m, (State *)nullptr,
+                           sp.full, sp.splits, part);
+        if (hipGetLastError() != hipSuccess) return HIF8_ERR_HIP;
+        hipLaunchKernelGGL(w16::k_split_reduce, dim3(unsigned(sp.tail)), dim3(w16::kThreads), 0, s, part, sp.splits,
+                           sp.full, tiles_m, tiles_n, group_m, int(M), int(N), bias, g.y[0]);
+        if (hipGetLastError() != hipSuccess) return HIF8_ERR_HIP;
+    }
     return y_st ? launch_gelu_stat_settle(y_st, y_smax, stream) : HIF8_OK;
 }
 
@@ -399,6 +529,47 @@ extern "C" int hif8_linear_fwd_wq(const uint16_t *a, const uint16_t *w_q, const 
 {
     const int rc = check_w16(a, w_q, bias, y, M, N, K);
     return rc != HIF8_OK ? rc : launch_linear_w16(a, w_q, bias, y, M, N, K, stream, nullptr, 0.0f);
+}
+
+extern "C" int64_t hif8_linear_split_workspace_bytes(int64_t M, int64_t N, int64_t K)
+{
+    if (M <= 0 || N <= 0 || K <= 0) return 0;
+    const int64_t tiles = ((M + w16::kTile - 1) / w16::kTile) * ((N + w16::kTile - 1) / w16::kTile);
+    return plan_split(tiles, K).bytes();
+}
+
+static int split_part(void *workspace, int64_t workspace_bytes, int64_t M, int64_t N, int64_t K, float **part)
+{
+    *part = nullptr;
+    const int64_t need = hif8_linear_split_workspace_bytes(M, N, K);
+    if (!workspace || need == 0) return HIF8_OK;
+    if (workspace_bytes < need) return HIF8_ERR_ARG;
+    if ((uintptr_t)workspace & 15u) return HIF8_ERR_ALIGN;
+    *part = (float *)workspace;
+    return HIF8_OK;
+}
+
+extern "C" int hif8_linear_fwd_wq_split(const uint16_t *a, const uint16_t *w_q, const uint16_t *bias, uint16_t *y,
+                                        int64_t M, int64_t N, int64_t K, void *workspace, int64_t workspace_bytes,
+                                        hif8_stream_t stream)
+{
+    int rc = check_w16(a, w_q, bias, y, M, N, K);
+    if (rc != HIF8_OK) return rc;
+    float *part = nullptr;
+    rc = split_part(workspace, workspace_bytes, M, N, K, &part);
+    if (rc != HIF8_OK) return rc;
+    Groups g{};
+    g.n = 1;
+    g.tile_end[0] = int((N + w16::kTile - 1) / w16::kTile);
+    g.cols[0] = int(N);
+    g.y[0] = y;
+    return launch_w16(a, w_q, g, bias, M, N, K, stream, nullptr, 0.0f, part);
+}
+
+extern "C" int hif8_linear_wgrad(const uint16_t *g_t, const uint16_t *x_t, uint16_t *dw, int64_t n_out, int64_t k_in,
+                                 int64_t tokens_pad, void *workspace, int64_t workspace_bytes, hif8_stream_t stream)
+{
+    return hif8_linear_fwd_wq_split(g_t, x_t, nullptr, dw, n_out, k_in, tokens_pad, workspace, workspace_bytes, stream);
 }
 
 extern "C" int hif8_linear_fwd_wq_gelu_stat(const uint16_t *a, const uint16_t *w_q, const uint16_t *bias,

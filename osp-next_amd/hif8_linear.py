@@ -201,12 +201,13 @@ def dgrad_fused_ok(grad_q: Tensor, w: "PackedWeight") -> bool:
 def linear_dgrad(grad_q2: Tensor, w: "PackedWeight") -> Tensor:
     """grad_q [M, N] @ w_q [N, K] -> [M, K] bf16 (hif8_linear.py:97): the forward GEMM with the
     transposed weight codes [K, N] as its weight, on the route the forward takes at this M (the
-    fused GEMM, or the transposed codes decoded once and the decode-free GEMM)."""
+    fused GEMM, or the transposed codes decoded once and the decode-free GEMM with its last
+    partial wave of tiles split over k ranges)."""
     M, N = grad_q2.shape
     K = w.shape[1]
     g = _aligned(grad_q2.contiguous())
     if decode_once(M):
-        return linear_fwd_wq(g, decode(w.codes_t(), w.state, torch.bfloat16), None)
+        return linear_fwd_wq_split(g, decode(w.codes_t(), w.state, torch.bfloat16))
     y = torch.empty((M, K), dtype=torch.bfloat16, device=g.device)
     _lib.check(_lib.load().hif8_linear_fwd(g.data_ptr(), w.codes_t().data_ptr(), w.state.ptr, None, y.data_ptr(),
                                            M, K, N, _lib.stream_ptr(g.device)), "hif8_linear_fwd (dgrad)")
@@ -232,15 +233,39 @@ def wgrad_ok(grad_q2: Tensor, x_q2: Tensor) -> bool:
             and grad_q2.shape[0] == x_q2.shape[0] and grad_q2.shape[0] > 0)
 
 
-def linear_wgrad(grad_q2: Tensor, x_q2: Tensor) -> Tensor:
+def linear_wgrad(grad_q2: Tensor, x_q2: Tensor, split_tail: bool = True) -> Tensor:
     """grad_weight = grad_q^T [N, M] @ x_q [M, K] -> [N, K] bf16 (hif8_linear.py:100-105, fp32
     accumulation): both operands transposed with the token dimension padded to a multiple of 64,
-    then the decode-free GEMM, which reduces over the padded tokens (the zeros add nothing)."""
+    then hif8_linear_wgrad, the decode-free GEMM reducing over the padded tokens (the zeros add
+    nothing), with the last partial wave of tiles split over token ranges unless ``split_tail``
+    is False."""
     M = grad_q2.shape[0]
     Mp = (M + 63) // 64 * 64
     g_t = transpose_bf16(grad_q2.contiguous(), Mp)
     x_t = transpose_bf16(x_q2.contiguous(), Mp)
-    return linear_fwd_wq(g_t, x_t, None)
+    return linear_fwd_wq_split(g_t, x_t, split_tail=split_tail)
+
+
+def linear_fwd_wq_split(a: Tensor, w_q: Tensor, bias: Optional[Tensor] = None, split_tail: bool = True) -> Tensor:
+    """hif8_linear_fwd_wq_split: y = a @ w_q^T (+ bias), bf16, with the tail of the tile grid split
+    over k ranges into a transient fp32 workspace (hif8_linear_split_workspace_bytes) unless
+    ``split_tail`` is False."""
+    M, K = a.shape
+    N = w_q.shape[0]
+    if w_q.shape[1] != K or w_q.dtype != torch.bfloat16 or a.dtype != torch.bfloat16:
+        raise ValueError("linear_fwd_wq_split takes bf16 a [M, K] and bf16 w_q [N, K]")
+    L = _lib.load()
+    y = torch.empty((M, N), dtype=torch.bfloat16, device=a.device)
+    b_ptr = None
+    if bias is not None:
+        bias = bias.detach().to(torch.bfloat16).contiguous()
+        b_ptr = bias.data_ptr()
+    nbytes = int(L.hif8_linear_split_workspace_bytes(M, N, K)) if split_tail else 0
+    ws = torch.empty((nbytes + 3) // 4, dtype=torch.float32, device=a.device) if nbytes > 0 else None
+    _lib.check(L.hif8_linear_fwd_wq_split(a.data_ptr(), w_q.data_ptr(), b_ptr, y.data_ptr(), M, N, K,
+                                          ws.data_ptr() if ws is not None else None, nbytes,
+                                          _lib.stream_ptr(a.device)), "hif8_linear_fwd_wq_split")
+    return y
 
 
 # GEMM route for bf16 activations: "fused" decodes the packed weight inside the GEMM (each

@@ -169,3 +169,76 @@ def test_wgrad_config3_full_size_rows(pkg):
     gw = pkg.linear_wgrad(gq, xq)
     rows = torch.cat([torch.randint(0, N, (48,), generator=g, device=DEV), torch.arange(N - 16, N, device=DEV)])
     wgrad_bound(gq[:, rows], xq, gw[rows])
+
+
+def test_wgrad_split_tail(pkg):
+    """A shape whose last wave of tiles is split: 17 x 16 = 272 tiles of 256 x 256 on 256 CUs
+    leave 16 tail tiles, each computed as 8 token ranges whose fp32 sums the reduce kernel adds.
+    The split result is bounded against fp64 like the rest, agrees with the unsplit GEMM to
+    rounding (the sums only change order), and is the same on a second call."""
+    M, N, K = 4100, 4352, 4096
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    L = pkg._lib.load()
+    Mp = (M + 63) // 64 * 64
+    tiles = (N // 256) * (K // 256)
+    nbytes = int(L.hif8_linear_split_workspace_bytes(N, K, Mp))
+    tail = tiles % cus
+    if cus == 256:
+        assert nbytes == tail * 8 * 256 * 256 * 4, nbytes
+    print(f"[wgrad] split tail M={M} N={N} K={K} cus={cus} workspace={nbytes}", flush=True)
+    g = torch.Generator(device=DEV).manual_seed(11)
+    gq, _ = pkg._quant(torch.randn(M, N, generator=g, device=DEV).to(torch.bfloat16), 224.0)
+    xq, _ = pkg._quant(torch.randn(M, K, generator=g, device=DEV).to(torch.bfloat16), 15.0)
+    split = pkg.linear_wgrad(gq, xq)
+    whole = pkg.linear_wgrad(gq, xq, split_tail=False)
+    again = pkg.linear_wgrad(gq, xq)
+    assert torch.equal(split.view(torch.int16), again.view(torch.int16))
+    wgrad_bound(gq, xq, split)
+    wgrad_bound(gq, xq, whole)
+    # only the tail tiles' sums change order: about one bf16 rounding step apart at most
+    a, b = split.double(), whole.double()
+    diff = (a - b).abs()
+    floor = b.square().mean().sqrt() * 2.0 ** -12
+    assert bool((diff <= torch.maximum(a.abs(), b.abs()) * 2.0 ** -7 + floor).all())
+    frac = float((diff > 0).double().mean())
+    print(f"[wgrad] split vs whole: {frac:.4%} of outputs differ", flush=True)
+    assert frac < 0.1
+
+
+def test_wgrad_workspace_sizes(pkg):
+    """No split for a grid that fills whole waves, runs 8 waves or more, or whose tail is over half
+    the CUs, or whose reduction is too short to divide; the 14B FFN-up weight splits 56 tail tiles
+    4 ways on 256 CUs."""
+    L = pkg._lib.load()
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    assert L.hif8_linear_split_workspace_bytes(4096, 4096, 75648) == 0     # 256 tiles: whole waves
+    assert L.hif8_linear_split_workspace_bytes(256, 256, 75648) == 0       # fewer tiles than CUs
+    assert L.hif8_linear_split_workspace_bytes(4352, 4096, 128) == 0       # 2 k-steps: nothing to split
+    if cus == 256:
+        assert L.hif8_linear_split_workspace_bytes(13824, 5120, 75648) == 56 * 4 * 256 * 256 * 4
+        assert L.hif8_linear_split_workspace_bytes(75600, 5120, 13824) == 0     # 5920 tiles: 23 waves
+
+
+def test_dgrad_full_size_rows(pkg):
+    """Wan-14B 720P FFN-up dgrad on the decode-once route: grad_q [75600, 13824] @ w_q [13824, 5120]
+    (216 k-steps).  Its 296 x 20 = 5920 tiles are 23 whole waves on 256 CUs, more than the split
+    tail takes (no workspace).  Sampled rows, the last 40 included, against fp32 torch on the same
+    operands; the plain decode-free GEMM agrees within one bf16 step."""
+    M, N, K = 75600, 13824, 5120
+    print(f"[dgrad] full size M={M} N={N} K={K}", flush=True)
+    if torch.cuda.get_device_properties(0).multi_processor_count == 256:
+        assert pkg._lib.load().hif8_linear_split_workspace_bytes(M, K, N) == 0
+    g = torch.Generator(device=DEV).manual_seed(12)
+    w = (torch.randn(N, K, generator=g, device=DEV) * 0.02).to(torch.bfloat16)
+    packed = pkg.PackedWeight(w, 15.0)
+    gq, _ = pkg._quant(torch.randn(M, N, generator=g, device=DEV).to(torch.bfloat16), 224.0)
+    gx = pkg.linear_dgrad(gq, packed)
+    w_qt = pkg.decode(packed.codes_t(), packed.state, torch.bfloat16)
+    whole = pkg.linear_fwd_wq(gq, w_qt, None)
+    rows = torch.cat([torch.randint(0, M, (256,), generator=g, device=DEV), torch.arange(M - 40, M, device=DEV)])
+    ref = gq[rows].float() @ packed.dequantize().float()
+    elem, norm = rel_errors(gx[rows], ref)
+    assert elem <= TOL_ELEM and norm <= TOL_NORM, (elem, norm)
+    a, b = gx[rows].double(), whole[rows].double()
+    floor = b.square().mean().sqrt() * 2.0 ** -12
+    assert bool(((a - b).abs() <= torch.maximum(a.abs(), b.abs()) * 2.0 ** -7 + floor).all())

@@ -318,6 +318,32 @@ def test_codes_decode_to_npu_qdq_every_bf16(R):
     assert np.array_equal(bits32(R.decode(c)), bits32(R.quant_hif8_npu(xf[fin])))
 
 
+@pytest.mark.parametrize("amax", [1.0, 3.75, 0.013, 200.0, 40000.0])
+def test_decode_lut_bf16_is_the_quant_chain_of_its_code(R, amax):
+    """x_q as a function of the code: for every finite bf16 x with |x| <= amax (amax itself
+    included, so it sets the scale), decode_lut_bf16(scale)[code(x * scale)] equals the whole
+    _quant chain's x_q, which test_quant_chain_matches_torch_expression pins against torch.  A
+    table built without the division by the scale, or with the fp32 instead of the bf16 rounding
+    of decode(c) / scale, fails it."""
+    xf = R.bf16_to_f32(ALL_BF16)
+    a_bits = int(R.f32_to_bf16(np.array([amax], np.float32))[0])
+    amax_b = float(R.bf16_to_f32(np.array([a_bits], np.uint16))[0])
+    x = ALL_BF16[np.isfinite(xf) & (np.abs(xf) <= amax_b)]
+    x = np.concatenate([x, np.array([a_bits], np.uint16)])
+    xq, s_bits = R.quant_bf16(x, 15.0, "npu")
+    codes, s2 = R.codes_bf16(x, 15.0)
+    assert s2 == s_bits
+    lut = R.decode_lut_bf16(s_bits)
+    assert np.array_equal(lut[codes], xq)
+    s = float(R.bf16_to_f32(np.array([s_bits], np.uint16))[0])
+    wrong = R.f32_to_bf16(R.decode_table())                     # no division by the scale
+    assert not np.array_equal(wrong[codes], xq)
+    if math.frexp(s)[0] != 0.5:                                  # a power-of-two scale divides exactly
+        with np.errstate(all="ignore"):
+            f32_only = (R.decode_table() / np.float32(s)).astype(np.float32)
+        assert not np.array_equal(bits32(f32_only[codes]), bits32(R.bf16_to_f32(xq)))
+
+
 # ------------------------------------------------- scale and bf16 ops vs torch
 
 
