@@ -553,18 +553,26 @@ def median(v):
 
 
 def _cpu_info():
-    """The host CPU as ``lscpu`` names it, and the instruction-set flags that decide its bf16 GEMM
-    rate (AMX, AVX-512 BF16): ``(model, {flag: present})``.  /proc/cpuinfo when lscpu is absent."""
-    model, flags = None, set()
+    """The host CPU as ``lscpu`` names it, the identifying fields it prints beside the model name
+    (which a virtual machine may shorten, e.g. to "AMD EPYC"), and the instruction-set flags that
+    decide its bf16 GEMM rate (AMX, AVX-512 BF16): ``(model, details, {flag: present})``.
+    /proc/cpuinfo when lscpu is absent."""
+    model, flags, details = None, set(), {}
+    keep = {"Vendor ID": "vendor", "CPU family": "family", "Model": "model_number", "Stepping": "stepping",
+            "Hypervisor vendor": "hypervisor", "Socket(s)": "sockets", "Core(s) per socket": "cores_per_socket",
+            "Thread(s) per core": "threads_per_core", "L3": "l3"}
     try:
         import subprocess
         out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=20).stdout
         for line in out.splitlines():
             key, _, val = line.partition(":")
-            if key.strip() == "Model name" and model is None:
+            key = key.strip()
+            if key == "Model name" and model is None:
                 model = val.strip()
-            elif key.strip() == "Flags":
+            elif key == "Flags":
                 flags = set(val.split())
+            elif key in keep and keep[key] not in details:
+                details[keep[key]] = val.strip()
     except Exception:
         pass
     if model is None or not flags:
@@ -579,7 +587,7 @@ def _cpu_info():
         except OSError:
             pass
     names = ("amx_bf16", "amx_tile", "amx_int8", "avx512_bf16", "avx512f", "avx512_vnni", "avx2")
-    return model or platform.machine(), {n: n in flags for n in names}
+    return model or platform.machine(), details, {n: n in flags for n in names}
 
 
 def _cpu_threads():
@@ -675,14 +683,14 @@ def cpu_baseline(torch, M, K, N, sample_rows=4096, target_s=10.0):
         c2[name] = {"M": Mc, "N": n_, "K": k_, "s": round(t_c, 4), "runs": n_c,
                     "TFLOPs": round(2.0 * Mc * n_ * k_ / t_c / 1e12, 4)}
         del xc, wc, bc
-    model, flags = _cpu_info()
+    model, details, flags = _cpu_info()
     return {
         "value": round(value, 4), "unit": "TFLOP/s", "cores": threads, "kind": "port",
         "sample": (f"reference CPU path (torch ops, bf16 F.linear) on the FFN-up shape: W[{N},{K}] qdq x2 "
                    f"(median {tw:.2f}s) and {len(t_slice)} reps of an x[{sample_rows},{K}] slice, qdq + GEMM "
                    f"(median {ts:.3f}s), {total:.1f}s of CPU work; one step at M={M} = W qdq + "
                    f"{M / sample_rows:.2f} slices = {t_full:.2f}s"),
-        "cpu_model": model, "cpu_flags": flags, "os_cpu_count": os.cpu_count(),
+        "cpu_model": model, "cpu_lscpu": details, "cpu_flags": flags, "os_cpu_count": os.cpu_count(),
         "affinity_cpus": len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else None,
         "omp_num_threads": os.environ.get("OMP_NUM_THREADS"),
         "c1": c1_out, "c2": c2,

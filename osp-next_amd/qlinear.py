@@ -106,7 +106,7 @@ class QLinear(nn.Linear):
         self._quant_grad = value
 
     def forward(self, x: Tensor) -> Tensor:
-        assert self.qparams is not None, "Linear: Must assign quant params (QType) to this layer"
+        assert self.qparams is not None, "QLinear has no weight QType: call assign_qparams() before forward"
         qp = self.qparams.dim(-1)
         qp_in = self.qparams.dim(-1) if self.in_qparams is None else self.in_qparams.dim(-1)
         if not x.is_contiguous():
@@ -117,9 +117,10 @@ class QLinear(nn.Linear):
     def transfer(self, layer: Union["QLinear", nn.Linear]):
         self.to(layer.weight.device)
         self.to(layer.weight.dtype)
-        self.weight.data.view(-1)[:] = layer.weight.data.view(-1)[:]
-        if self.bias is not None:
-            self.bias.data[:] = layer.bias.data[:]
+        with torch.no_grad():
+            self.weight.copy_(layer.weight.reshape(self.weight.shape))
+            if self.bias is not None:
+                self.bias.copy_(layer.bias)
 
     def assign_qparams(self, Q: Union[QType, str]):
         self.qparams = QType(Q) if isinstance(Q, str) else Q.copy()
@@ -130,7 +131,7 @@ class QLinear(nn.Linear):
     def __deepcopy__(self, memo):
         layer = QLinear(self.weight.shape[1], self.weight.shape[0], self.bias is not None)
         layer.transfer(self)
-        assert self.qparams is not None, "Must assign quant params before deepcopy"
+        assert self.qparams is not None, "a QLinear is copied only once its weight QType is assigned"
         layer.assign_qparams(self.qparams)
         if self.in_qparams is not None:
             layer.assign_input_qparams(self.in_qparams)
@@ -143,7 +144,7 @@ def replace_linear(module: nn.Module, w_Q: Union[QType, str], in_Q: Union[QType,
     """utils.py:16-37: swap every nn.Linear below ``module`` (not ``exclude_layers``) for a QLinear.
     As in the reference, subclasses of nn.Linear (QLinear, HIF8Linear) are replaced too."""
     exclude_layers = [] if exclude_layers is None else exclude_layers
-    assert isinstance(exclude_layers, list), "Exclude layers must be list of string"
+    assert isinstance(exclude_layers, list), "exclude_layers takes a list of module names"
     mods = dict(module.named_modules())
     for name, m in list(module.named_modules()):
         if name in exclude_layers or not isinstance(m, nn.Linear):
