@@ -203,10 +203,11 @@ def time_ffn(pkg, torch, x, reps):
 def time_backward(pkg, torch, x, packed, reps):
     """The backward of the FFN-up HIF8Linear (hif8_linear.py:88-111) at the 14B 720P shape: the
     gradient's _quant with scale_max 224, dgrad grad_q [M, N] @ w_q [N, K] (the transposed codes
-    decoded once, then the decode-free GEMM) and wgrad grad_q^T @ x_q (both operands transposed
-    with the tokens padded to the k-step, then hif8_linear_wgrad: the decode-free GEMM with its
-    last partial wave split over token ranges, and without the split for comparison); each phase
-    timed with HIP events on the launch stream.  hipBLASLt on the same operands for context."""
+    decoded once, then the decode-free GEMM) and wgrad grad_q^T @ x_q (hif8_linear_wgrad: the
+    decode-free GEMM reading both operands token-major with transposing LDS loads, its last
+    partial wave split over token ranges); for comparison the GEMMs without the split and wgrad's
+    transposed route (both operands transposed, then the row-major GEMM); each phase timed with HIP
+    events on the launch stream.  hipBLASLt on the same operands for context."""
     dev = x.device
     M, K = x.shape
     N = packed.shape[0]
@@ -224,7 +225,7 @@ def time_backward(pkg, torch, x, packed, reps):
     x_t = torch.empty((K, Mp), dtype=torch.bfloat16, device=dev)
     gx = torch.empty((M, K), dtype=torch.bfloat16, device=dev)
     gw = torch.empty((N, K), dtype=torch.bfloat16, device=dev)
-    ws_bytes = int(L.hif8_linear_split_workspace_bytes(N, K, Mp))
+    ws_bytes = int(L.hif8_linear_split_workspace_bytes(N, K, M))
     ws = torch.empty(max(ws_bytes // 4, 1), dtype=torch.float32, device=dev)
     ws_d_bytes = int(L.hif8_linear_split_workspace_bytes(M, K, N))
     ws_d = torch.empty(max(ws_d_bytes // 4, 1), dtype=torch.float32, device=dev)
@@ -239,14 +240,20 @@ def time_backward(pkg, torch, x, packed, reps):
                                                             K, N, ws_d.data_ptr(), ws_d_bytes, stream), "dgrad"),
         "dgrad_gemm_unsplit": lambda: ck(L.hif8_linear_fwd_wq(gq.data_ptr(), w_qt.data_ptr(), None, gx.data_ptr(), M,
                                                               K, N, stream), "dgrad whole"),
-        "wgrad_transposes": lambda: (ck(L.hif8_transpose_bf16(gq.data_ptr(), M, N, Mp, g_t.data_ptr(), stream), "tg"),
-                                     ck(L.hif8_transpose_bf16(xq.data_ptr(), M, K, Mp, x_t.data_ptr(), stream), "tx")),
-        "wgrad_gemm": lambda: ck(L.hif8_linear_wgrad(g_t.data_ptr(), x_t.data_ptr(), gw.data_ptr(), N, K, Mp,
+        "wgrad_gemm": lambda: ck(L.hif8_linear_wgrad(gq.data_ptr(), xq.data_ptr(), gw.data_ptr(), M, N, K,
                                                      ws.data_ptr(), ws_bytes, stream), "wgrad"),
-        # the same GEMM with every tile computed whole (no split tail), for comparison
-        "wgrad_gemm_unsplit": lambda: ck(L.hif8_linear_wgrad(g_t.data_ptr(), x_t.data_ptr(), gw.data_ptr(), N, K, Mp,
+        # for comparison: every tile computed whole (no split tail) ...
+        "wgrad_gemm_unsplit": lambda: ck(L.hif8_linear_wgrad(gq.data_ptr(), xq.data_ptr(), gw.data_ptr(), M, N, K,
                                                              None, 0, stream), "wgrad whole"),
+        # ... and the transposed route: both operands transposed, then the row-major GEMM
+        "wgrad_transposed_transposes": lambda: (
+            ck(L.hif8_transpose_bf16(gq.data_ptr(), M, N, Mp, g_t.data_ptr(), stream), "tg"),
+            ck(L.hif8_transpose_bf16(xq.data_ptr(), M, K, Mp, x_t.data_ptr(), stream), "tx")),
+        "wgrad_transposed_gemm": lambda: ck(L.hif8_linear_fwd_wq_split(g_t.data_ptr(), x_t.data_ptr(), None,
+                                                                       gw.data_ptr(), N, K, Mp, ws.data_ptr(), ws_bytes,
+                                                                       stream), "wgrad transposed"),
     }
+    comparison = ("dgrad_gemm_unsplit", "wgrad_gemm_unsplit", "wgrad_transposed_transposes", "wgrad_transposed_gemm")
     for _ in range(2):
         for fn in phases.values():
             fn()
@@ -268,11 +275,12 @@ def time_backward(pkg, torch, x, packed, reps):
            "dgrad_frac": round(flops / (ms["dgrad_gemm"] * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
            "wgrad_TFLOPs": round(flops / (ms["wgrad_gemm"] * 1e-3) / 1e12, 1),
            "wgrad_frac": round(flops / (ms["wgrad_gemm"] * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
-           "wgrad_with_transposes_TFLOPs": round(flops / ((ms["wgrad_gemm"] + ms["wgrad_transposes"]) * 1e-3) / 1e12, 1),
+           "wgrad_transposed_route_TFLOPs": round(
+               flops / ((ms["wgrad_transposed_gemm"] + ms["wgrad_transposed_transposes"]) * 1e-3) / 1e12, 1),
            "dgrad_unsplit_frac": round(flops / (ms["dgrad_gemm_unsplit"] * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
            "wgrad_unsplit_frac": round(flops / (ms["wgrad_gemm_unsplit"] * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
            "split_workspace_bytes": {"dgrad": ws_d_bytes, "wgrad": ws_bytes},
-           "backward_ms": round(sum(v for k, v in ms.items() if not k.endswith("_unsplit")), 4)}
+           "backward_ms": round(sum(v for k, v in ms.items() if k not in comparison), 4)}
     # hipBLASLt on the same operands (context only): grad_q @ w_q and grad_q^T @ x_q
     try:
         w_q = packed.dequantize()

@@ -252,8 +252,8 @@ int hif8_transpose_codes(const uint8_t *codes, int64_t rows, int64_t cols, uint8
 
 /* wgrad support.  The reference's weight gradient is grad_q^T @ x_q over the flattened tokens
  * (hif8_linear.py:100-105), a product whose reduction runs over the rows of both operands.  The
- * decode-free GEMM reduces over its operands' rows of contiguous k, so wgrad runs
- * hif8_linear_wgrad(grad_q^T, x_q^T) on the two operands transposed, with the token dimension
+ * row-major decode-free GEMM reduces over its operands' rows of contiguous k, so the fallback
+ * of hif8_linear_wgrad runs it on the two operands transposed, with the token dimension
  * padded with zeros to a multiple of 64 (zeros add nothing to the sums).  This entry point writes
  * out[c][r] = x[r][c] for r < rows and 0 for rows <= r < rows_pad: x bf16 [rows, cols],
  * out bf16 [cols, rows_pad].  Any shape and alignment; 16-byte aligned pointers, cols % 8 == 0
@@ -262,15 +262,21 @@ int hif8_transpose_bf16(const uint16_t *x, int64_t rows, int64_t cols, int64_t r
                         hif8_stream_t stream);
 
 /* The weight gradient of _HIF8LinearFunction.backward, grad_W = grad_q^T @ x_q
- * (hif8_linear.py:100-105), on the transposed operands hif8_transpose_bf16 writes:
- *   dw[n_out, k_in] = g_t[n_out, tokens_pad] . x_t[k_in, tokens_pad]^T     (fp32 sums, bf16 out)
- * with tokens_pad % 64 == 0 (zero-padded tokens), k_in % 8 == 0, 16-byte aligned pointers,
- * tokens_pad < 2^22: hif8_linear_fwd_wq_split(g_t, x_t, NULL, dw, n_out, k_in, tokens_pad, ...),
- * whose split tail matters most here (1080 tiles over 75648 tokens for the 14B FFN-up weight).
- * The sums' order differs from the reference's bf16 matmul (it does in any case).  No
- * counterpart of its own in the reference. */
-int hif8_linear_wgrad(const uint16_t *g_t, const uint16_t *x_t, uint16_t *dw, int64_t n_out, int64_t k_in,
-                      int64_t tokens_pad, void *workspace, int64_t workspace_bytes, hif8_stream_t stream);
+ * (hif8_linear.py:100-105), on the operands as the forward and the gradient quantisation leave
+ * them, token-major:
+ *   dw[n_out, k_in] = g[tokens, n_out]^T . x[tokens, k_in]     (fp32 sums, bf16 out)
+ * The decode-free GEMM's tiles with both operands staged k-major in LDS and read with transposing
+ * loads (ds_read_b64_tr_b16), so neither operand is transposed in memory; tokens need not be a
+ * multiple of 64.  n_out % 8 == 0, k_in % 8 == 0, 16-byte aligned pointers, and
+ * (tokens + 128) * n_out * 2 and (tokens + 128) * k_in * 2 below 2^32 (HIF8_ERR_SHAPE otherwise: the caller then
+ * transposes both operands with hif8_transpose_bf16 and runs hif8_linear_fwd_wq_split).  The
+ * split tail as for hif8_linear_fwd_wq_split, with
+ * hif8_linear_split_workspace_bytes(n_out, k_in, tokens) bytes of workspace (or NULL): the
+ * 1080 tiles over 75600 tokens of the 14B FFN-up weight split 56 tail tiles 4 ways.  The sums'
+ * order differs from the reference's bf16 matmul (it does in any case).  No counterpart of its
+ * own in the reference. */
+int hif8_linear_wgrad(const uint16_t *g, const uint16_t *x, uint16_t *dw, int64_t tokens, int64_t n_out,
+                      int64_t k_in, void *workspace, int64_t workspace_bytes, hif8_stream_t stream);
 
 /* ---------------------------------------------------------------------------
  * Producer fusion for the modulated LayerNorm in front of the self-attention q/k/v

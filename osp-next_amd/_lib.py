@@ -15,6 +15,7 @@ _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libhif8_mi355x.so")
 
 HIF8_OK = 0
+ERR_SHAPE = -2    # HIF8_ERR_SHAPE: a shape the entry point does not take
 DTYPE_BF16, DTYPE_F32, DTYPE_BF16_AS_F32 = 0, 1, 2
 SEM_NPU, SEM_TORCH, SEM_TORCH_BF16 = 0, 1, 2
 # formats of a quantised activation held by the Python layer: bf16 x_q, or its 8-bit codes

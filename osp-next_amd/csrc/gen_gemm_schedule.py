@@ -205,7 +205,7 @@ def schedule_w16(phase):
 
 def emit_w16(phase):
     ops = schedule_w16(phase)
-    lines = [f"__device__ __forceinline__ void phase{phase}(Ctx &c)", "{"]
+    lines = ["template <bool TR>", f"__device__ __forceinline__ void phase{phase}(Ctx<TR> &c)", "{"]
     for m in range(W16_MFMAS):
         lines += ["    " + op for op in ops.get(("pre", m), [])]
         lines.append(f"    mm<{phase}, {m}>(c);")

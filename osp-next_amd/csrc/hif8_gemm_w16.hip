@@ -90,11 +90,15 @@ __device__ __forceinline__ uint32_t f2bf_pk(float lo, float hi)
 
 // Per-wave loop state.  Fragment sets alternate between phases: set 0 is consumed in the even
 // phase (first 32 k of a k-step) and filled in the odd one, set 1 the other way round.
-struct Ctx {
+// TR: the operands are k-major (token-major) in memory and in LDS, read with transposing loads
+// (the K-major layout below).
+template <bool TR> struct Ctx {
     u32x4 B[2][8];    // [set][j]  X fragments (m-tile j)
     u32x4 A[2][8];    // [set][i]  W fragments (n-tile i)
-    uint32_t xb[2], wb[2];  // fragment read bases in stage 0 [phase p]
-    uint32_t xr, wr;        // the same in the stages read this phase
+    uint32_t xb[2], wb[2];  // fragment read bases in stage 0: [phase p]; TR: [parity of the tile]
+    uint32_t xr, wr;        // the same in the stages read this phase (TR: even tiles)
+    uint32_t xr1, wr1;      // TR: odd tiles
+    uint32_t xstep, wstep;  // TR: source bytes per k-step of X and W (uniform)
     f32x4 acc[8][8];
     u32x4 rx, rw, ex, ew;  // buffer resources: X, W, and the effective ones (size 0 past the end)
     uint32_t xoff[8], woff[8];  // DTL source offsets of the next X and W stage to load
@@ -102,46 +106,88 @@ struct Ctx {
     uint32_t wave;
 };
 
+// K-major stage (TR): 64 k-rows x 256 columns of one operand in 128-byte blocks of 4 k-rows x
+// 16 columns (the width of an MFMA tile); block (q, P) -- k-rows 4q .. 4q + 3, columns
+// 16P .. 16P + 15 -- at (16 q + (P ^ ((q >> 1) & 1))) * 128, k-row 4q + e at +32 e.  A
+// ds_read_b64_tr_b16 gives lane l of each 16-lane group element j of the 4 loaded by lane
+// 4 j + (l % 16) / 4 of the group, at position (l % 4): with lane 4 j + u of group g loading
+// columns 4u .. 4u + 3 of k-row 8 g + j (+ 4 for the second read), lane (r, g) receives k-rows
+// 8 g .. 8 g + 7 of column r -- the operand layout of v_mfma_f32_16x16x32_bf16.  The XOR puts
+// the k-rows 8 g + 0..3 of groups g and g + 1, read in the same cycle, in opposite halves of the
+// 64 banks; within a block the 4 k-rows cover 32 distinct banks.  A DTL item (1 KB) is the 8
+// blocks of one 4-k-row group and one half of the columns.
+
 __device__ __forceinline__ uint32_t ring(uint32_t off, uint32_t n) { return off + n * kSlot >= kLds ? off + n * kSlot - kLds : off + n * kSlot; }
 // before the reads of phase P: the even phase reads the second half of its own k-step, the odd
 // phase the first half of the next one, whose stages are two further along the ring
-template <int P> __device__ __forceinline__ void read_bases(Ctx &c)
+template <int P, bool TR> __device__ __forceinline__ void read_bases(Ctx<TR> &c)
 {
     if (P == 1) {
         c.xs = ring(c.xs, 2);
         c.ws = ring(c.ws, 2);
     }
     constexpr int p = 1 - P;
-    c.xr = c.xb[p] + c.xs;
-    c.wr = c.wb[p] + c.ws;
+    if (TR) {
+        // k-rows 32 p .. of the stage: 8 blocks of 4 k-rows further
+        c.xr = c.xb[0] + c.xs + uint32_t(p) * 16384u;
+        c.xr1 = c.xb[1] + c.xs + uint32_t(p) * 16384u;
+        c.wr = c.wb[0] + c.ws + uint32_t(p) * 16384u;
+        c.wr1 = c.wb[1] + c.ws + uint32_t(p) * 16384u;
+    } else {
+        c.xr = c.xb[p] + c.xs;
+        c.wr = c.wb[p] + c.ws;
+    }
 }
-__device__ __forceinline__ void rotate(Ctx &c) { c.ls = ring(c.ls, 1); }
-template <int I> __device__ __forceinline__ void adv(Ctx &c)
+template <bool TR> __device__ __forceinline__ void rotate(Ctx<TR> &c) { c.ls = ring(c.ls, 1); }
+// a k-step further in the source: 64 k (128 bytes) along a row, or 64 k-rows (TR)
+template <int I, bool TR> __device__ __forceinline__ void adv(Ctx<TR> &c)
 {
-    if (I < 8) ASMV("v_add_u32 %0, 0x80, %0" : "+v"(c.xoff[I]));
-    else ASMV("v_add_u32 %0, 0x80, %0" : "+v"(c.woff[I - 8]));
+    if (TR) {
+        if (I < 8) ASMV("v_add_u32 %0, %1, %0" : "+v"(c.xoff[I]) : "s"(c.xstep));
+        else ASMV("v_add_u32 %0, %1, %0" : "+v"(c.woff[I - 8]) : "s"(c.wstep));
+    } else {
+        if (I < 8) ASMV("v_add_u32 %0, 0x80, %0" : "+v"(c.xoff[I]));
+        else ASMV("v_add_u32 %0, 0x80, %0" : "+v"(c.woff[I - 8]));
+    }
 }
 
 // DTL item i (8 rows x 128 B, rows (8 wave + i) * 8 ..) of the X (OP 0) or W (OP 1) stage at
 // the current source offsets, into the stage at `stage`.
-template <int OP> __device__ __forceinline__ void issue_dtl(Ctx &c, uint32_t stage, int i)
+template <int OP, bool TR> __device__ __forceinline__ void issue_dtl(Ctx<TR> &c, uint32_t stage, int i)
 {
     const uint32_t m0v = __builtin_amdgcn_readfirstlane(stage + (c.wave * 8u + uint32_t(i)) * 1024u);
     if (OP == 0) dtl_load(m0v, c.xoff[i], c.ex);
     else dtl_load(m0v, c.woff[i], c.ew);
 }
-template <int OP> __device__ __forceinline__ void issue_dtl(Ctx &c, int i) { issue_dtl<OP>(c, c.ls, i); }
+template <int OP, bool TR> __device__ __forceinline__ void issue_dtl(Ctx<TR> &c, int i) { issue_dtl<OP>(c, c.ls, i); }
 
-// fragment reads: 16 rows x 128 B per m- or n-tile
-template <int NXT, int J> __device__ __forceinline__ void rd_x(Ctx &c) { ldsb128<J * 2048>(c.B[NXT][J], c.xr); }
-template <int NXT, int I> __device__ __forceinline__ void rd_w(Ctx &c) { ldsb128<I * 2048>(c.A[NXT][I], c.wr); }
-template <int CUR, int MI> __device__ __forceinline__ void mm(Ctx &c)
+// two transposing reads (TR): k-rows 8 g + 0..3 and 8 g + 4..7 of a 16-column tile
+template <int OFF> __device__ __forceinline__ void ldstr(u32x4 &d, uint32_t a)
+{
+    typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+    u32x2 lo, hi;
+    ASMV("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(lo) : "v"(a), "i"(OFF));
+    ASMV("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(hi) : "v"(a), "i"(OFF + 2048));
+    d = u32x4{lo.x, lo.y, hi.x, hi.y};
+}
+// fragment reads: 16 rows x 128 B per m- or n-tile, or (TR) a 16-column block column
+template <int NXT, int J, bool TR> __device__ __forceinline__ void rd_x(Ctx<TR> &c)
+{
+    if (TR) ldstr<(J & ~1) * 128>(c.B[NXT][J], (J & 1) ? c.xr1 : c.xr);
+    else ldsb128<J * 2048>(c.B[NXT][J], c.xr);
+}
+template <int NXT, int I, bool TR> __device__ __forceinline__ void rd_w(Ctx<TR> &c)
+{
+    if (TR) ldstr<(I & ~1) * 128>(c.A[NXT][I], (I & 1) ? c.wr1 : c.wr);
+    else ldsb128<I * 2048>(c.A[NXT][I], c.wr);
+}
+template <int CUR, int MI, bool TR> __device__ __forceinline__ void mm(Ctx<TR> &c)
 {
     constexpr int i = MI / 8, j = MI % 8;
     mfma(c.acc[i][j], c.A[CUR][i], c.B[CUR][j]);
 }
 // after the wait covering the fragments of set SET
-template <int SET> __device__ __forceinline__ void tie_set(Ctx &c)
+template <int SET, bool TR> __device__ __forceinline__ void tie_set(Ctx<TR> &c)
 {
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
@@ -152,10 +198,6 @@ template <int SET> __device__ __forceinline__ void tie_set(Ctx &c)
 
 #include "hif8_gemm_schedule_w16.inc"
 
-// EPI 0: y = rnd(acc + bias).  EPI 1: the same y, and the GELU statistic of y (its max, or a
-// non-finite flag) folded into y_st's accumulator; the settle kernel launched after it turns that
-// into amax|GELU(y)| and its scale when max y settles it (hif8_gelu_dev.h).  The output features
-// are G.n groups, each with its output buffer.
 // Tile t of the order: groups of group_m m-tiles, n-tiles outer within a group.
 __device__ __forceinline__ void tile_origin(int t, int tiles_m, int tiles_n, int group_m, int &m0, int &n0)
 {
@@ -167,12 +209,20 @@ __device__ __forceinline__ void tile_origin(int t, int tiles_m, int tiles_n, int
     n0 = (within / gm) * kTile;
 }
 
+// EPI 0: y = rnd(acc + bias).  EPI 1: the same y, and the GELU statistic of y (its max, or a
+// non-finite flag) folded into y_st's accumulator; the settle kernel launched after it turns that
+// into amax|GELU(y)| and its scale when max y settles it (hif8_gelu_dev.h).  The output features
+// are G.n groups, each with its output buffer.
 // EPI 2, the split tail: workgroup w computes k range w % splits (consecutive k-steps) of tile
 // tile0 + w / splits and writes its fp32 sums to part (256 KB per workgroup, in the accumulators'
 // lane order) for k_split_reduce.  (A separate instantiation: in the same kernel as the bf16
 // epilogue, the register allocator moved all accumulators to VGPRs ahead of the branch and
 // spilled.)
-template <int EPI>
+// TR: X and Wq are k-major, X^T [K][M] and Wq^T [K][N] (contiguous rows of M and N elements):
+// the weight gradient's grad_q [tokens][out] and x_q [tokens][in] as they are, K = tokens.  Rows
+// past K read as zero through the buffers' ranges; columns past M or N read other data, which
+// only reaches outputs that are not stored.
+template <int EPI, bool TR = false>
 __global__ __launch_bounds__(kThreads, 1) void k_linear_w16(const uint16_t *__restrict__ X, const uint16_t *__restrict__ Wq,
                                                             const Groups G, const uint16_t *__restrict__ bias,
                                                             int M, int N, int K, int tiles_m, int tiles_n,
@@ -181,13 +231,13 @@ __global__ __launch_bounds__(kThreads, 1) void k_linear_w16(const uint16_t *__re
 {
     __shared__ __attribute__((aligned(1024))) uint8_t smem[kLds];
     ASMV("; lds base %0" ::"v"(uint32_t(uintptr_t(smem))) : "memory");
-    Ctx c;
+    Ctx<TR> c;
     const uint32_t tid = threadIdx.x, lane = tid & 63u;
     c.wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const uint32_t r = lane & 15u, g = lane >> 4;
 
     int t = blockIdx.x;
-    int nk = K / kBK, kb = 0;
+    int nk = TR ? (K + kBK - 1) / kBK : K / kBK, kb = 0;
     if (EPI == 2) {
         t = tile0 + int(blockIdx.x) / splits;
         const int per = (nk + splits - 1) / splits;
@@ -202,7 +252,7 @@ __global__ __launch_bounds__(kThreads, 1) void k_linear_w16(const uint16_t *__re
     const int col0 = gi == 0 ? 0 : G.tile_end[gi - 1] * kTile;
     const int ycols = G.cols[gi];
 
-    {
+    if (!TR) {
         // the buffers start at k-step kb of row 0; rows past M or N lie past the range
         const uint32_t kofs = uint32_t(kb) * uint32_t(kBK) * 2u;
         const uint64_t xa = uint64_t(X) + uint64_t(m0) * uint64_t(K) * 2u + kofs;
@@ -211,32 +261,68 @@ __global__ __launch_bounds__(kThreads, 1) void k_linear_w16(const uint16_t *__re
         const uint64_t wa = uint64_t(Wq) + uint64_t(n0) * uint64_t(K) * 2u + kofs;
         const uint32_t wrows = uint32_t(N - n0 < kTile ? N - n0 : kTile);
         c.rw = u32x4{uint32_t(wa), uint32_t(wa >> 32), wrows * uint32_t(K) * 2u - kofs, 0x00020000u};
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            c.rx[i] = __builtin_amdgcn_readfirstlane(c.rx[i]);
-            c.rw[i] = __builtin_amdgcn_readfirstlane(c.rw[i]);
-        }
+    } else {
+        // the buffers start at column m0 (n0) of k-row 64 kb and end with the matrix: k-rows past
+        // K lie past the range (the caller keeps K * M * 2 and K * N * 2 below 2^32)
+        const uint64_t xofs = uint64_t(kb) * uint64_t(kBK) * uint64_t(M) * 2u + uint64_t(m0) * 2u;
+        const uint64_t xa = uint64_t(X) + xofs;
+        c.rx = u32x4{uint32_t(xa), uint32_t(xa >> 32), uint32_t(uint64_t(K) * uint64_t(M) * 2u - xofs), 0x00020000u};
+        const uint64_t wofs = uint64_t(kb) * uint64_t(kBK) * uint64_t(N) * 2u + uint64_t(n0) * 2u;
+        const uint64_t wa = uint64_t(Wq) + wofs;
+        c.rw = u32x4{uint32_t(wa), uint32_t(wa >> 32), uint32_t(uint64_t(K) * uint64_t(N) * 2u - wofs), 0x00020000u};
+        c.xstep = __builtin_amdgcn_readfirstlane(uint32_t(kBK) * uint32_t(M) * 2u);
+        c.wstep = __builtin_amdgcn_readfirstlane(uint32_t(kBK) * uint32_t(N) * 2u);
     }
-    // DTL source offsets of k-step 0.  LDS 16-B slot s of a stage is written by lane s%64 of
-    // load s/64; its source chunk is the slot's chunk un-swizzled (the XOR is an involution).
-    // X and W rows share the layout.
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-        const uint32_t row = (c.wave * 8u + i) * 8u + (lane >> 3);
-        const uint32_t ch = (lane & 7u) ^ (lane >> 3) ^ uint32_t(i & 1);
-        c.xoff[i] = row * uint32_t(K) * 2u + ch * 16u;
-        c.woff[i] = c.xoff[i];
+    for (int i = 0; i < 4; ++i) {
+        c.rx[i] = __builtin_amdgcn_readfirstlane(c.rx[i]);
+        c.rw[i] = __builtin_amdgcn_readfirstlane(c.rw[i]);
     }
-    // Fragment read bases.  Lane (r, g) = (lane & 15, lane >> 4) holds k = 32p + 8g .. +7 of
-    // phase p for row r of its 16-row tile, for both operands: chunk 4p + g of rows wm + 16j + r
-    // (X) and wn + 16i + r (W); f(row) = f(r).
-    const uint32_t fr = (r & 7u) ^ ((r >> 3) & 1u);
     const uint32_t wm = (c.wave & 1u) * 128u, wn = (c.wave >> 1) * 128u;
+    if (!TR) {
+        // DTL source offsets of k-step 0.  LDS 16-B slot s of a stage is written by lane s%64 of
+        // load s/64; its source chunk is the slot's chunk un-swizzled (the XOR is an involution).
+        // X and W rows share the layout.
 #pragma unroll
-    for (int p = 0; p < 2; ++p) {
-        const uint32_t ch = ((4u * p + g) ^ fr) << 4;
-        c.xb[p] = (wm + r) * 128u + ch;
-        c.wb[p] = (wn + r) * 128u + ch;
+        for (int i = 0; i < 8; ++i) {
+            const uint32_t row = (c.wave * 8u + i) * 8u + (lane >> 3);
+            const uint32_t ch = (lane & 7u) ^ (lane >> 3) ^ uint32_t(i & 1);
+            c.xoff[i] = row * uint32_t(K) * 2u + ch * 16u;
+            c.woff[i] = c.xoff[i];
+        }
+        // Fragment read bases.  Lane (r, g) = (lane & 15, lane >> 4) holds k = 32p + 8g .. +7 of
+        // phase p for row r of its 16-row tile, for both operands: chunk 4p + g of rows wm + 16j + r
+        // (X) and wn + 16i + r (W); f(row) = f(r).
+        const uint32_t fr = (r & 7u) ^ ((r >> 3) & 1u);
+#pragma unroll
+        for (int p = 0; p < 2; ++p) {
+            const uint32_t ch = ((4u * p + g) ^ fr) << 4;
+            c.xb[p] = (wm + r) * 128u + ch;
+            c.wb[p] = (wn + r) * 128u + ch;
+        }
+    } else {
+        // DTL item it = 8 wave + i: 4-k-row group q = it / 2, column half it % 2; lane s writes
+        // block P' = 8 (it % 2) + s / 8, k-row e = (s % 8) / 2, bytes 16 (s % 2) .. of its 32; the
+        // source is column block P = P' ^ ((q >> 1) & 1) of k-row 4 q + e.
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const uint32_t it = c.wave * 8u + uint32_t(i), q = it >> 1;
+            const uint32_t pb = ((it & 1u) * 8u + (lane >> 3)) ^ ((q >> 1) & 1u);
+            const uint32_t krow = 4u * q + ((lane & 7u) >> 1);
+            const uint32_t col = pb * 32u + (lane & 1u) * 16u;
+            c.xoff[i] = krow * uint32_t(M) * 2u + col;
+            c.woff[i] = krow * uint32_t(N) * 2u + col;
+        }
+        // Fragment read bases: lane (L, g) = (lane & 15, lane >> 4) reads k-rows 8 g + L / 4 (and
+        // + 4) of the stage, columns 4 (L % 4) .. of a 16-column block: block group q = 2 g (+ 1),
+        // XOR bit s = g & 1.  Even tiles J sit at J * 128 + s * 128, odd ones at (J - 1) * 128 +
+        // 128 - s * 128 from the quadrant's first block (wm / 16 or wn / 16).
+        const uint32_t sx = g & 1u;
+        const uint32_t common = g * 4096u + (r >> 2) * 32u + (r & 3u) * 8u;
+        c.xb[0] = common + (wm / 16u) * 128u + sx * 128u;
+        c.xb[1] = common + (wm / 16u) * 128u + 128u - sx * 128u;
+        c.wb[0] = common + (wn / 16u) * 128u + sx * 128u;
+        c.wb[1] = common + (wn / 16u) * 128u + 128u - sx * 128u;
     }
 
     // Prologue: X and W of k-steps 0 and 1 into stages 0..3; wait for k-step 0.
@@ -263,6 +349,8 @@ __global__ __launch_bounds__(kThreads, 1) void k_linear_w16(const uint16_t *__re
     c.ws = kSlot;
     c.xr = c.xb[0];
     c.wr = c.wb[0] + kSlot;
+    c.xr1 = c.xb[1];  // TR: the odd tiles' bases
+    c.wr1 = c.wb[1] + kSlot;
     rd_w<0, 0>(c); rd_x<0, 0>(c); rd_x<0, 1>(c); rd_x<0, 2>(c); rd_x<0, 3>(c);
     rd_x<0, 4>(c); rd_x<0, 5>(c); rd_x<0, 6>(c); rd_x<0, 7>(c);
     rd_w<0, 1>(c); rd_w<0, 2>(c); rd_w<0, 3>(c); rd_w<0, 4>(c); rd_w<0, 5>(c); rd_w<0, 6>(c); rd_w<0, 7>(c);
@@ -438,7 +526,7 @@ static SplitPlan plan_split(int64_t tiles, int64_t K)
 {
     const int cus = cu_count();
     const int tail = int(tiles % cus);
-    const int64_t nk = K / w16::kBK;
+    const int64_t nk = (K + w16::kBK - 1) / w16::kBK;
     SplitPlan p{int(tiles), 0, 1};
     if (tiles < cus || tiles >= 8 * int64_t(cus) || tail == 0 || tail > cus / 2) return p;
     int sp = cus / tail;
@@ -451,9 +539,11 @@ static SplitPlan plan_split(int64_t tiles, int64_t K)
 // Shapes: K % 64 == 0, N % 8 == 0, 16-byte aligned X, W_q and Y, 8-byte aligned bias (checked
 // by the caller).  M, N < 2^31, K < 2^22.  y_st != NULL selects the GELU-statistic epilogue and the
 // settle kernel (scale for y_smax).  part != NULL (one output group, no y_st) splits the tail as
-// plan_split says, with part holding plan_split(...).bytes() bytes.
+// plan_split says, with part holding plan_split(...).bytes() bytes.  tr: x and w_q are k-major
+// (one output group, no y_st).
 static int launch_w16(const uint16_t *x, const uint16_t *w_q, const Groups &g, const uint16_t *bias, int64_t M,
-                      int64_t N, int64_t K, hif8_stream_t stream, State *y_st, float y_smax, float *part = nullptr)
+                      int64_t N, int64_t K, hif8_stream_t stream, State *y_st, float y_smax, float *part = nullptr,
+                      bool tr = false)
 {
     hipStream_t s = (hipStream_t)stream;
     if (K >= (int64_t(1) << 22)) return HIF8_ERR_SHAPE;
@@ -463,6 +553,7 @@ static int launch_w16(const uint16_t *x, const uint16_t *w_q, const Groups &g, c
     const int group_m = tiles_n >= 32 ? w16::kGroupWide : w16::kGroupNarrow;
     if (tiles >= (int64_t(1) << 31)) return HIF8_ERR_SHAPE;
     SplitPlan sp{int(tiles), 0, 1};
+    if (tr && (y_st || g.n != 1)) return HIF8_ERR_ARG;
     if (part) {
         if (y_st || g.n != 1) return HIF8_ERR_ARG;
         sp = plan_split(tiles, K);
@@ -470,6 +561,10 @@ static int launch_w16(const uint16_t *x, const uint16_t *w_q, const Groups &g, c
     if (y_st)
         hipLaunchKernelGGL(w16::k_linear_w16<1>, dim3(unsigned(sp.full)), dim3(w16::kThreads), 0, s, x, w_q, g, bias,
                            int(M), int(N), int(K), tiles_m, tiles_n, group_m, y_st, 0, 1, (float *)nullptr);
+    else if (sp.full > 0 && tr)
+        hipLaunchKernelGGL((w16::k_linear_w16<0, true>), dim3(unsigned(sp.full)), dim3(w16::kThreads), 0, s, x, w_q, g,
+                           bias, int(M), int(N), int(K), tiles_m, tiles_n, group_m, (State *)nullptr, 0, 1,
+                           (float *)nullptr);
     else if (sp.full > 0)
         hipLaunchKernelGGL(w16::k_linear_w16<0>, dim3(unsigned(sp.full)), dim3(w16::kThreads), 0, s, x, w_q, g, bias,
                            int(M), int(N), int(K), tiles_m, tiles_n, group_m, (State *)nullptr, 0, 1,
@@ -478,9 +573,14 @@ static int launch_w16(const uint16_t *x, const uint16_t *w_q, const Groups &g, c
     if (sp.splits > 1) {
         // after the whole tiles on the stream: they fill whole waves, so the split workgroups
         // start as the last of them end
-        hipLaunchKernelGGL(w16::k_linear_w16<2>, dim3(unsigned(sp.tail * sp.splits)), dim3(w16::kThreads), 0, s, x,
-                           w_q, g, bias, int(M), int(N), int(K), tiles_m, tiles_n, group_m, (State *)nullptr,
-                           sp.full, sp.splits, part);
+        if (tr)
+            hipLaunchKernelGGL((w16::k_linear_w16<2, true>), dim3(unsigned(sp.tail * sp.splits)), dim3(w16::kThreads), 0,
+                               s, x, w_q, g, bias, int(M), int(N), int(K), tiles_m, tiles_n, group_m, (State *)nullptr,
+                               sp.full, sp.splits, part);
+        else
+            hipLaunchKernelGGL(w16::k_linear_w16<2>, dim3(unsigned(sp.tail * sp.splits)), dim3(w16::kThreads), 0, s, x,
+                               w_q, g, bias, int(M), int(N), int(K), tiles_m, tiles_n, group_m, (State *)nullptr,
+                               sp.full, sp.splits, part);
         if (hipGetLastError() != hipSuccess) return HIF8_ERR_HIP;
         hipLaunchKernelGGL(w16::k_split_reduce, dim3(unsigned(sp.tail)), dim3(w16::kThreads), 0, s, part, sp.splits,
                            sp.full, tiles_m, tiles_n, group_m, int(M), int(N), bias, g.y[0]);
@@ -566,10 +666,29 @@ extern "C" int hif8_linear_fwd_wq_split(const uint16_t *a, const uint16_t *w_q, 
     return launch_w16(a, w_q, g, bias, M, N, K, stream, nullptr, 0.0f, part);
 }
 
-extern "C" int hif8_linear_wgrad(const uint16_t *g_t, const uint16_t *x_t, uint16_t *dw, int64_t n_out, int64_t k_in,
-                                 int64_t tokens_pad, void *workspace, int64_t workspace_bytes, hif8_stream_t stream)
+extern "C" int hif8_linear_wgrad(const uint16_t *g, const uint16_t *x, uint16_t *dw, int64_t tokens, int64_t n_out,
+                                 int64_t k_in, void *workspace, int64_t workspace_bytes, hif8_stream_t stream)
 {
-    return hif8_linear_fwd_wq_split(g_t, x_t, nullptr, dw, n_out, k_in, tokens_pad, workspace, workspace_bytes, stream);
+    if (!g || !x || !dw) return HIF8_ERR_ARG;
+    if (tokens <= 0 || n_out <= 0 || k_in <= 0) return HIF8_ERR_ARG;
+    if (n_out % 8 != 0 || k_in % 8 != 0) return HIF8_ERR_SHAPE;
+    if (n_out >= (int64_t(1) << 31) || k_in >= (int64_t(1) << 31) || tokens >= (int64_t(1) << 31)) return HIF8_ERR_SHAPE;
+    // the k-major buffers address g and x with 32-bit offsets, including the k-rows of the last
+    // k-step past the tokens (which must fall past the buffers' ranges, not wrap into them)
+    if ((tokens + 128) * n_out * 2 >= (int64_t(1) << 32) || (tokens + 128) * k_in * 2 >= (int64_t(1) << 32))
+        return HIF8_ERR_SHAPE;
+    if (((uintptr_t)g | (uintptr_t)x | (uintptr_t)dw) & 15u) return HIF8_ERR_ALIGN;
+    const int64_t tiles = ((n_out + w16::kTile - 1) / w16::kTile) * ((k_in + w16::kTile - 1) / w16::kTile);
+    if (tiles >= (int64_t(1) << 31)) return HIF8_ERR_SHAPE;
+    float *part = nullptr;
+    const int rc = split_part(workspace, workspace_bytes, n_out, k_in, tokens, &part);
+    if (rc != HIF8_OK) return rc;
+    Groups gr{};
+    gr.n = 1;
+    gr.tile_end[0] = int((k_in + w16::kTile - 1) / w16::kTile);
+    gr.cols[0] = int(k_in);
+    gr.y[0] = dw;
+    return launch_w16(g, x, gr, nullptr, n_out, k_in, tokens, stream, nullptr, 0.0f, part, true);
 }
 
 extern "C" int hif8_linear_fwd_wq_gelu_stat(const uint16_t *a, const uint16_t *w_q, const uint16_t *bias,

@@ -233,16 +233,30 @@ def wgrad_ok(grad_q2: Tensor, x_q2: Tensor) -> bool:
             and grad_q2.shape[0] == x_q2.shape[0] and grad_q2.shape[0] > 0)
 
 
-def linear_wgrad(grad_q2: Tensor, x_q2: Tensor, split_tail: bool = True) -> Tensor:
+def linear_wgrad(grad_q2: Tensor, x_q2: Tensor, split_tail: bool = True, transposed: bool = False) -> Tensor:
     """grad_weight = grad_q^T [N, M] @ x_q [M, K] -> [N, K] bf16 (hif8_linear.py:100-105, fp32
-    accumulation): both operands transposed with the token dimension padded to a multiple of 64,
-    then hif8_linear_wgrad, the decode-free GEMM reducing over the padded tokens (the zeros add
-    nothing), with the last partial wave of tiles split over token ranges unless ``split_tail``
-    is False."""
-    M = grad_q2.shape[0]
+    accumulation): hif8_linear_wgrad, the decode-free GEMM reading both operands token-major as
+    they are, with the last partial wave of tiles split over token ranges unless ``split_tail`` is
+    False.  Operands too large for its 32-bit offsets (or ``transposed=True``) take the transposed
+    route: both operands transposed with the tokens zero-padded to a multiple of 64, then the
+    row-major GEMM over the padded tokens (the zeros add nothing)."""
+    M, N = grad_q2.shape
+    K = x_q2.shape[1]
+    g = grad_q2.contiguous()
+    x = x_q2.contiguous()
+    L = _lib.load()
+    if not transposed:
+        dw = torch.empty((N, K), dtype=torch.bfloat16, device=g.device)
+        nbytes = int(L.hif8_linear_split_workspace_bytes(N, K, M)) if split_tail else 0
+        ws = torch.empty((nbytes + 3) // 4, dtype=torch.float32, device=g.device) if nbytes > 0 else None
+        rc = L.hif8_linear_wgrad(g.data_ptr(), x.data_ptr(), dw.data_ptr(), M, N, K,
+                                 ws.data_ptr() if ws is not None else None, nbytes, _lib.stream_ptr(g.device))
+        if rc != _lib.ERR_SHAPE:
+            _lib.check(rc, "hif8_linear_wgrad")
+            return dw
     Mp = (M + 63) // 64 * 64
-    g_t = transpose_bf16(grad_q2.contiguous(), Mp)
-    x_t = transpose_bf16(x_q2.contiguous(), Mp)
+    g_t = transpose_bf16(g, Mp)
+    x_t = transpose_bf16(x, Mp)
     return linear_fwd_wq_split(g_t, x_t, split_tail=split_tail)
 
 

@@ -112,24 +112,31 @@ def w16_asm(tmp_path_factory):
 
 
 def test_w16_resources(w16_asm):
-    """The decode-free twin: its three instantiations (bf16 epilogue, GELU statistic, fp32 split
-    partials) with the 160 KB LDS ring, the split-tail reduce kernel without LDS, no spills."""
+    """The decode-free twin: its five instantiations (bf16 epilogue, GELU statistic, fp32 split
+    partials; the last and the first also with token-major operands) with the 160 KB LDS ring, the
+    split-tail reduce kernel without LDS, no spills."""
     _, remarks = w16_asm
     spills = re.findall(r"(?:VGPRs|SGPRs) Spill: (\d+)", remarks)
     lds = re.findall(r"LDS Size \[bytes/block\]: (\d+)", remarks)
     scratch = re.findall(r"ScratchSize \[bytes/lane\]: (\d+)", remarks)
-    assert sorted(lds) == ["0", "163840", "163840", "163840"], lds
+    assert sorted(lds) == ["0"] + ["163840"] * 5, lds
     assert spills and set(spills) == {"0"}, spills
     assert scratch and set(scratch) == {"0"}, scratch
 
 
 def test_w16_main_loop_hazards(w16_asm):
-    """Per k-step: 128 MFMAs (16x16x32), 32 fragment reads (16 per phase), 16 global->LDS loads."""
+    """Per k-step: 128 MFMAs (16x16x32), 16 global->LDS loads, and 32 fragment reads (16 per
+    phase), or 64 transposing reads for token-major operands (two per fragment), with no register
+    copies of the fragments (each pair of reads lands in its fragment's registers)."""
     import isa_check
     loops = isa_check.mfma_loops(w16_asm[0])
-    assert len(loops) == 3
+    assert len(loops) == 5
+    reads = []
     for body in loops:
         kinds = isa_check.census(body)
-        assert kinds.get("mfma") == 128 and kinds.get("lds_load") == 32 and kinds.get("lds_dma") == 16, kinds
+        assert kinds.get("mfma") == 128 and kinds.get("lds_dma") == 16, kinds
+        reads.append(kinds.get("lds_load"))
+        assert not any(ins[0].startswith("v_mov") for ins in body), "fragment copies in the loop"
         errors = isa_check.check_body(body)
         assert not errors, "\n".join(errors[:20])
+    assert sorted(reads) == [32, 32, 32, 64, 64], reads

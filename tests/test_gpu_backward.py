@@ -143,9 +143,12 @@ def wgrad_bound(gq, xq, got):
 
 
 @pytest.mark.parametrize("M,N,K", [(64, 256, 256), (300, 320, 264), (1000, 1536, 1536), (4100, 520, 8),
-                                   (65, 8, 64), (2049, 5120, 1024)])
+                                   (65, 8, 64), (2049, 5120, 1024), (1, 16, 8), (130, 264, 1032)])
 def test_wgrad_vs_fp64(pkg, M, N, K):
-    """grad_q^T [N, M] @ x_q [M, K] with M padded to the k-step inside (M % 64 != 0 included)."""
+    """grad_q^T [N, M] @ x_q [M, K] read token-major (a last partial k-step of tokens, columns past
+    a tile's end), bounded against fp64, and bit-identical to the transposed route (both operands
+    transposed and zero-padded, then the row-major GEMM): the same MFMA products in the same
+    order."""
     print(f"[wgrad] M={M} N={N} K={K}", flush=True)
     g = torch.Generator(device="cpu").manual_seed(M * 3 + N + K)
     gy = torch.randn(M, N, generator=g).to(torch.bfloat16).to(DEV)
@@ -156,6 +159,8 @@ def test_wgrad_vs_fp64(pkg, M, N, K):
     gw = pkg.linear_wgrad(gq, xq)
     assert gw.shape == (N, K) and gw.dtype == torch.bfloat16
     wgrad_bound(gq, xq, gw)
+    gw_t = pkg.linear_wgrad(gq, xq, transposed=True)
+    assert torch.equal(gw.view(torch.int16), gw_t.view(torch.int16))
 
 
 def test_wgrad_config3_full_size_rows(pkg):
@@ -169,6 +174,8 @@ def test_wgrad_config3_full_size_rows(pkg):
     gw = pkg.linear_wgrad(gq, xq)
     rows = torch.cat([torch.randint(0, N, (48,), generator=g, device=DEV), torch.arange(N - 16, N, device=DEV)])
     wgrad_bound(gq[:, rows], xq, gw[rows])
+    gw_t = pkg.linear_wgrad(gq, xq, transposed=True)
+    assert torch.equal(gw.view(torch.int16), gw_t.view(torch.int16))
 
 
 def test_wgrad_split_tail(pkg):
@@ -193,6 +200,9 @@ def test_wgrad_split_tail(pkg):
     whole = pkg.linear_wgrad(gq, xq, split_tail=False)
     again = pkg.linear_wgrad(gq, xq)
     assert torch.equal(split.view(torch.int16), again.view(torch.int16))
+    # the transposed route splits the same tail the same way
+    split_t = pkg.linear_wgrad(gq, xq, transposed=True)
+    assert torch.equal(split.view(torch.int16), split_t.view(torch.int16))
     wgrad_bound(gq, xq, split)
     wgrad_bound(gq, xq, whole)
     # only the tail tiles' sums change order: about one bf16 rounding step apart at most
