@@ -181,7 +181,10 @@ W16_DTL_GAPS = {0: tuple(range(1, 32, 4)), 1: tuple(range(1, 32, 4))}
 W16_ADV_GAPS = tuple(range(40, 48))
 
 
-def schedule_w16(phase):
+def schedule_w16(phase, tr=False):
+    """tr: token-major operands, each fragment two transposing reads (its k-rows 0..3 and 4..7 of
+    the lane group); the first goes in the even gap of the plain schedule, the second in the odd
+    gap after it, so that no two reads issue back to back."""
     ops = {}
 
     def at(pos, *items):
@@ -194,7 +197,11 @@ def schedule_w16(phase):
         at(("pre", 0), "wait_lgkm<0>();")
     at(("pre", 0), f"tie_set<{cur}>(c);")
     for gap, (op, n) in zip(W16_READ_GAPS, W16_READ_ORDER):
-        at(gap, f"rd_{op}<{nxt}, {n}>(c);")
+        if tr:
+            at(gap, f"rd_{op}_half<{nxt}, {n}, 0>(c);")
+            at(gap + 1, f"rd_{op}_half<{nxt}, {n}, 1>(c);")
+        else:
+            at(gap, f"rd_{op}<{nxt}, {n}>(c);")
     for n, g in enumerate(W16_DTL_GAPS[phase]):
         at(g, f"issue_dtl<{phase}>(c, {n});")
     for n, g in enumerate(W16_ADV_GAPS):
@@ -203,9 +210,10 @@ def schedule_w16(phase):
     return ops
 
 
-def emit_w16(phase):
-    ops = schedule_w16(phase)
-    lines = ["template <bool TR>", f"__device__ __forceinline__ void phase{phase}(Ctx<TR> &c)", "{"]
+def emit_w16(phase, tr=False):
+    ops = schedule_w16(phase, tr)
+    name = f"phase{phase}_tr" if tr else f"phase{phase}"
+    lines = ["template <bool TR>", f"__device__ __forceinline__ void {name}(Ctx<TR> &c)", "{"]
     for m in range(W16_MFMAS):
         lines += ["    " + op for op in ops.get(("pre", m), [])]
         lines.append(f"    mm<{phase}, {m}>(c);")
@@ -217,8 +225,9 @@ def emit_w16(phase):
 
 def generate_w16():
     return ("// Generated by gen_gemm_schedule.py -- do not edit.\n"
-            "// Main-loop phase bodies of k_linear_w16 (hif8_gemm_w16.hip).\n\n"
-            + emit_w16(0) + "\n\n" + emit_w16(1) + "\n")
+            "// Main-loop phase bodies of k_linear_w16 (hif8_gemm_w16.hip): row-major operands\n"
+            "// (phase0, phase1) and token-major ones (phase0_tr, phase1_tr).\n\n"
+            + emit_w16(0) + "\n\n" + emit_w16(1) + "\n\n" + emit_w16(0, True) + "\n\n" + emit_w16(1, True) + "\n")
 
 
 if __name__ == "__main__":

@@ -170,6 +170,24 @@ template <int OFF> __device__ __forceinline__ void ldstr(u32x4 &d, uint32_t a)
     ASMV("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(hi) : "v"(a), "i"(OFF + 2048));
     d = u32x4{lo.x, lo.y, hi.x, hi.y};
 }
+// one of the two transposing reads of a fragment (TR): H = 0 its k-rows 8 g + 0..3, H = 1 the
+// next four, into the fragment's low or high half
+template <int OFF, int H> __device__ __forceinline__ void ldstr_half(u32x4 &d, uint32_t a)
+{
+    typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+    u32x2 v;
+    ASMV("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(v) : "v"(a), "i"(OFF + H * 2048));
+    if (H == 0) d = u32x4{v.x, v.y, d.z, d.w};
+    else d = u32x4{d.x, d.y, v.x, v.y};
+}
+template <int NXT, int J, int H, bool TR> __device__ __forceinline__ void rd_x_half(Ctx<TR> &c)
+{
+    ldstr_half<(J & ~1) * 128, H>(c.B[NXT][J], (J & 1) ? c.xr1 : c.xr);
+}
+template <int NXT, int I, int H, bool TR> __device__ __forceinline__ void rd_w_half(Ctx<TR> &c)
+{
+    ldstr_half<(I & ~1) * 128, H>(c.A[NXT][I], (I & 1) ? c.wr1 : c.wr);
+}
 // fragment reads: 16 rows x 128 B per m- or n-tile, or (TR) a 16-column block column
 template <int NXT, int J, bool TR> __device__ __forceinline__ void rd_x(Ctx<TR> &c)
 {
@@ -366,8 +384,13 @@ __global__ __launch_bounds__(kThreads, 1) void k_linear_w16(const uint16_t *__re
     for (int kk = 0; kk < nk; ++kk) {
         c.ex[2] = kk + 2 < nk ? c.rx[2] : 0u;
         c.ew[2] = kk + 2 < nk ? c.rw[2] : 0u;
-        phase0(c);
-        phase1(c);
+        if (TR) {
+            phase0_tr(c);
+            phase1_tr(c);
+        } else {
+            phase0(c);
+            phase1(c);
+        }
     }
     // no load may still target LDS when it is reused or released
     wait_vm<0>();
