@@ -87,6 +87,20 @@ def test_status_codes_without_gpu(pkg):
     assert grp([256, 256], sts=[fake, None]) == -1
     assert grp([256, 256], ys=[fake, odd]) == -3
     assert grp([256, 256], b=fake + 2) == -3
+    # token-major wgrad: pointers, sizes, n_out and k_in % 8, the 32-bit offset limit, alignment
+    # (all checked before any device call)
+    assert L.hif8_linear_wgrad(None, fake, fake, 1024, 256, 256, None, 0, None) == -1
+    assert L.hif8_linear_wgrad(fake, fake, fake, 0, 256, 256, None, 0, None) == -1
+    assert L.hif8_linear_wgrad(fake, fake, fake, 1024, 260, 256, None, 0, None) == -2
+    assert L.hif8_linear_wgrad(fake, fake, fake, 1024, 256, 100, None, 0, None) == -2
+    assert L.hif8_linear_wgrad(fake, fake, fake, 1 << 23, 256, 256, None, 0, None) == -2   # 4 GB of grad_q
+    assert L.hif8_linear_wgrad(fake, fake, fake, 1 << 20, 2048, 16, None, 0, None) == -2   # (2^20 + 128) * 4 KB
+    assert L.hif8_linear_wgrad(fake, odd, fake, 1024, 256, 256, None, 0, None) == -3
+    # split-tail GEMM: pointers and the shapes of hif8_linear_fwd_wq
+    assert L.hif8_linear_fwd_wq_split(None, fake, None, fake, 128, 256, 512, None, 0, None) == -1
+    assert L.hif8_linear_fwd_wq_split(fake, fake, None, fake, 128, 256, 100, None, 0, None) == -2
+    assert L.hif8_linear_fwd_wq_split(fake, fake, None, odd, 128, 256, 512, None, 0, None) == -3
+    assert L.hif8_linear_split_workspace_bytes(0, 256, 512) == 0
     # modulated LayerNorm: dim % 8, dim <= 8192, alignment of x and of the row statistics
     assert L.hif8_modln_amax(None, None, None, 4, 5120, 4, 1e-6, fake, 15.0, fake, None) == -1
     assert L.hif8_modln_amax(fake, None, None, 0, 5120, 4, 1e-6, fake, 15.0, fake, None) == -1
