@@ -475,9 +475,10 @@ __global__ __launch_bounds__(kThreads, 1) void k_linear_w16(const uint16_t *__re
     }
 }
 
-// The split tiles' outputs: workgroup b sums the splits fp32 partials of tile full_tiles + b in
-// split order (a fixed order: the result does not depend on timing), adds the bias, rounds to
-// bf16 and stores the in-range outputs.  One lane per 4 consecutive outputs of a row.
+// The split tiles' outputs: workgroup b sums the splits fp32 partials of tile full_tiles + b / 8,
+// MFMA tile row i = b % 8 of each wave quadrant, in split order (a fixed order: the result does
+// not depend on timing), adds the bias, rounds to bf16 and stores the in-range outputs.  One lane
+// per 4 consecutive outputs of a row; 8 workgroups per tile so that the reads fill the chip.
 __global__ __launch_bounds__(kThreads) void k_split_reduce(const float *__restrict__ part, int splits, int full_tiles,
                                                             int tiles_m, int tiles_n, int group_m, int M, int N,
                                                             const uint16_t *__restrict__ bias, uint16_t *__restrict__ Y)
@@ -485,12 +486,14 @@ __global__ __launch_bounds__(kThreads) void k_split_reduce(const float *__restri
     const uint32_t tid = threadIdx.x, lane = tid & 63u, wave = tid >> 6;
     const uint32_t r = lane & 15u, g = lane >> 4;
     int m0, n0;
-    tile_origin(full_tiles + int(blockIdx.x), tiles_m, tiles_n, group_m, m0, n0);
+    const uint32_t tile = blockIdx.x >> 3;
+    const int i = int(blockIdx.x & 7u);
+    tile_origin(full_tiles + int(tile), tiles_m, tiles_n, group_m, m0, n0);
     const uint32_t wm = (wave & 1u) * 128u, wn = (wave >> 1) * 128u;
-    const f32x4 *P = (const f32x4 *)part + size_t(blockIdx.x) * size_t(splits) * 16384u + wave * 4096u + lane;
-    for (int i = 0; i < 8; ++i) {
+    const f32x4 *P = (const f32x4 *)part + size_t(tile) * size_t(splits) * 16384u + wave * 4096u + lane;
+    {
         const int n = n0 + int(wn) + i * 16 + int(4u * g);
-        if (n >= N) continue;
+        if (n >= N) return;
         float b0 = 0.f, b1 = 0.f, b2 = 0.f, b3 = 0.f;
         if (bias) {
             const uint2 bb = *(const uint2 *)(bias + n);
@@ -605,7 +608,7 @@ static int launch_w16(const uint16_t *x, const uint16_t *w_q, const Groups &g, c
                                w_q, g, bias, int(M), int(N), int(K), tiles_m, tiles_n, group_m, (State *)nullptr,
                                sp.full, sp.splits, part);
         if (hipGetLastError() != hipSuccess) return HIF8_ERR_HIP;
-        hipLaunchKernelGGL(w16::k_split_reduce, dim3(unsigned(sp.tail)), dim3(w16::kThreads), 0, s, part, sp.splits,
+        hipLaunchKernelGGL(w16::k_split_reduce, dim3(unsigned(sp.tail) * 8u), dim3(w16::kThreads), 0, s, part, sp.splits,
                            sp.full, tiles_m, tiles_n, group_m, int(M), int(N), bias, g.y[0]);
         if (hipGetLastError() != hipSuccess) return HIF8_ERR_HIP;
     }
