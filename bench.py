@@ -34,10 +34,10 @@ def log(msg):
     print(msg, file=sys.stderr, flush=True)
 
 
-def make_inputs(torch, M, K, N, seed=0, dev="cuda:0"):
+def make_inputs(torch, M, K, N, seed=0, dev="cuda:0", outlier_channels=16):
     g = torch.Generator(device=dev).manual_seed(seed)
     x = torch.randn(M, K, generator=g, device=dev, dtype=torch.float32)
-    ch = torch.randperm(K, generator=g, device=dev)[:16]
+    ch = torch.randperm(K, generator=g, device=dev)[:outlier_channels]
     x[:, ch] *= 20
     x = x.to(torch.bfloat16)
     w = (torch.randn(N, K, generator=g, device=dev, dtype=torch.float32) * 0.02).to(torch.bfloat16)
@@ -713,8 +713,9 @@ def main():
     ap.add_argument("--route", default="auto", choices=["auto", "fused", "decode_once"],
                     help="GEMM route for bf16 activations (auto: HIF8Linear's rule, decode_once at this M)")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--shapes", default="up,bwd,ffn,modln,qkv,block,step",
-                    help="comma list of up,bwd (the FFN-up backward),down,qkvo,ffn,modln,qkv,block (config 4),"
+    ap.add_argument("--shapes", default="up,bwd,ffn,down,qkvo,c2,modln,qkv,block,step",
+                    help="comma list of up,bwd (the FFN-up backward),down,qkvo (the other 14B linears),"
+                         "c2 (the three 1.3B 480P linears, config 2),ffn,modln,qkv,block (config 4),"
                          "step (config 5),"
                          "data (the GEMM with constant operands) to time in addition")
     ap.add_argument("--block-routes", default="fused,reference",
@@ -856,17 +857,32 @@ def main():
             extra_shapes["step"] = time_step(pkg, torch, 2)
         except Exception as ex:
             extra_shapes["step"] = {"error": repr(ex)}
-    for name in [s for s in args.shapes.split(",")
-                 if s and s not in ("up", "bwd", "ffn", "modln", "qkv", "block", "step", "data")]:
-        n_, k_ = {"down": (5120, 13824), "qkvo": (5120, 5120)}[name]
-        xs, ws, bs = make_inputs(torch, M, k_, n_, seed=1)
+    def linear_line(m_, n_, k_, seed, outliers):
+        xs, ws, bs = make_inputs(torch, m_, k_, n_, seed=seed, outlier_channels=outliers)
         ps = pkg.PackedWeight(ws, 15.0)
-        rr = time_linear(pkg, torch, xs, ps, bs, max(3, args.steps // 2), 2, route)
+        r_ = route if args.route != "auto" else ("decode_once" if pkg.hif8_linear.decode_once(m_) else "fused")
+        rr = time_linear(pkg, torch, xs, ps, bs, max(3, args.steps // 2), 2, r_)
         gm = sum(rr["gemm"]) / len(rr["gemm"])
-        extra_shapes[name] = {"M": M, "N": n_, "K": k_, "gemm_ms": round(gm, 4),
-                              "gemm_TFLOPs": round(2.0 * M * n_ * k_ / (gm * 1e-3) / 1e12, 1),
-                              "step_ms": round(rr["wall_ms"] / max(3, args.steps // 2), 4)}
+        st_ms = rr["wall_ms"] / max(3, args.steps // 2)
+        line = {"M": m_, "N": n_, "K": k_, "route": r_, "gemm_ms": round(gm, 4),
+                "gemm_TFLOPs": round(2.0 * m_ * n_ * k_ / (gm * 1e-3) / 1e12, 1),
+                "gemm_frac": round(2.0 * m_ * n_ * k_ / (gm * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+                "step_ms": round(st_ms, 4),
+                "step_TFLOPs": round(2.0 * m_ * n_ * k_ / (st_ms * 1e-3) / 1e12, 1)}
         del xs, ws, bs, ps, rr
+        return line
+
+    for name in [s for s in args.shapes.split(",")
+                 if s and s not in ("up", "bwd", "ffn", "modln", "qkv", "block", "step", "data", "c2")]:
+        n_, k_ = {"down": (5120, 13824), "qkvo": (5120, 5120)}[name]
+        print(f"[bench] timing the 14B {name} linear", file=sys.stderr, flush=True)
+        extra_shapes[name] = linear_line(M, n_, k_, 1, 16)
+    if "c2" in args.shapes.split(","):
+        # config 2: the 1.3B 480P linears on x [32760, 1536] with 8 outlier channels
+        print("[bench] timing the 1.3B 480P linears (config 2)", file=sys.stderr, flush=True)
+        extra_shapes["c2"] = {name: linear_line(32760, n_, k_, seed, 8)
+                              for name, n_, k_, seed in (("qkvo", 1536, 1536, 2), ("ffn_up", 8960, 1536, 3),
+                                                         ("ffn_down", 1536, 8960, 4))}
 
     # the vendor bf16 GEMM on the same shape, for context (not part of the product)
     vendor = None
