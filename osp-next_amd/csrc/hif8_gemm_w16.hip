@@ -343,6 +343,16 @@ __global__ __launch_bounds__(kThreads, 1) void k_linear_w16(const uint16_t *__re
         c.wb[1] = common + (wn / 16u) * 128u + 128u - sx * 128u;
     }
 
+    // The bias words of this lane's output features (4 per MFMA tile row i), loaded ahead of the
+    // operand loads: they land during the main loop (in-order completion puts them before every
+    // operand wait), where in the epilogue each was a global load waited for on its own.
+    uint2 bw[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int n = n0 + int(wn + uint32_t(i * 16) + 4u * (lane >> 4));
+        bw[i] = (bias && n < N) ? *(const uint2 *)(bias + n) : uint2{0u, 0u};
+    }
+
     // Prologue: X and W of k-steps 0 and 1 into stages 0..3; wait for k-step 0.
     c.ex = c.rx;
     c.ew = c.rw;
@@ -421,15 +431,11 @@ __global__ __launch_bounds__(kThreads, 1) void k_linear_w16(const uint16_t *__re
         for (int i = 0; i < 8; ++i) {
             {
                 const uint32_t nl = wn + uint32_t(i * 16) + 4u * g;
-                const int n = n0 + int(nl);
-                float b0 = 0.f, b1 = 0.f, b2 = 0.f, b3 = 0.f;
-                if (bias && n < N) {
-                    const uint2 bb = *(const uint2 *)(bias + n);
-                    b0 = __builtin_bit_cast(float, bb.x << 16);
-                    b1 = __builtin_bit_cast(float, bb.x & 0xFFFF0000u);
-                    b2 = __builtin_bit_cast(float, bb.y << 16);
-                    b3 = __builtin_bit_cast(float, bb.y & 0xFFFF0000u);
-                }
+                const uint2 bb = bw[i];
+                const float b0 = __builtin_bit_cast(float, bb.x << 16);
+                const float b1 = __builtin_bit_cast(float, bb.x & 0xFFFF0000u);
+                const float b2 = __builtin_bit_cast(float, bb.y << 16);
+                const float b3 = __builtin_bit_cast(float, bb.y & 0xFFFF0000u);
 #pragma unroll
                 for (int j = 0; j < 8; ++j) {
                     const f32x4 &a = c.acc[i][j];
