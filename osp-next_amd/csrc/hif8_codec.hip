@@ -579,6 +579,30 @@ int launch_gelu_stat_settle(State *y_st, float y_smax, hif8_stream_t stream)
 
 using namespace hif8;
 
+// Workgroups of one k_quant instantiation that fit on a CU at once (its registers decide: 65 or
+// more VGPRs allow 7 or fewer waves per SIMD), read once from the runtime.  A grid of more
+// workgroups per CU than fit would run the excess as a second, partial wave.
+template <int DT, int MODE, bool GELU> static int resident_wgs()
+{
+    static int wgs = 0;
+    if (wgs == 0) {
+        int b = 0;
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&b, k_quant<DT, MODE, GELU>, kTPB, 0) != hipSuccess || b <= 0)
+            b = 1;
+        wgs = b;
+    }
+    return wgs;
+}
+
+template <int DT, int MODE, bool GELU = false>
+static void launch_k_quant(const void *x, int64_t n, const State *st, void *out, int sem, int use_state, int wg_per_cu,
+                           hipStream_t s)
+{
+    const int fit = resident_wgs<DT, MODE, GELU>();
+    const int grid = grid_for((n + 15) / 16, cu_count() * (wg_per_cu < fit ? wg_per_cu : fit));
+    hipLaunchKernelGGL((k_quant<DT, MODE, GELU>), dim3(grid), dim3(kTPB), 0, s, x, n, st, out, sem, use_state);
+}
+
 extern "C" {
 
 const char *hif8_strerror(int status)
@@ -646,14 +670,13 @@ static int launch_quant(const void *x, int dtype, int64_t n, const void *state, 
     if (dtype != HIF8_DTYPE_BF16 && dtype != HIF8_DTYPE_F32 && !(dtype == kBF16F32 && mode != 2)) return HIF8_ERR_ARG;
     if (sem != HIF8_SEM_NPU && sem != HIF8_SEM_TORCH) return HIF8_ERR_ARG;
     if (!aligned16(x) || !aligned16(out)) return HIF8_ERR_ALIGN;
-    int grid = grid_for((n + 15) / 16, cu_count() * (mode == 0 ? kEncodeWgPerCu : kQdqWgPerCu));
+    const int wpc = mode == 0 ? kEncodeWgPerCu : kQdqWgPerCu;
     hipStream_t s = (hipStream_t)stream;
     const State *st = (const State *)state;
-#define HIF8_LAUNCH(DT, MODE) \
-    hipLaunchKernelGGL((k_quant<DT, MODE>), dim3(grid), dim3(kTPB), 0, s, x, n, st, out, sem, use_state)
+#define HIF8_LAUNCH(DT, MODE) launch_k_quant<DT, MODE>(x, n, st, out, sem, use_state, wpc, s)
     if (gelu) {
         if (dtype != HIF8_DTYPE_BF16 || mode != 1) return HIF8_ERR_ARG;
-        hipLaunchKernelGGL((k_quant<kBF16, 1, true>), dim3(grid), dim3(kTPB), 0, s, x, n, st, out, sem, use_state);
+        launch_k_quant<kBF16, 1, true>(x, n, st, out, sem, use_state, wpc, s);
     } else if (dtype == HIF8_DTYPE_BF16) {
         if (mode == 0) HIF8_LAUNCH(kBF16, 0);
         else if (mode == 1 || mode == 3) HIF8_LAUNCH(kBF16, 1);
