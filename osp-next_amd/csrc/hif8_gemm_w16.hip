@@ -31,6 +31,12 @@
 //     every 256 consecutive tiles and its L2 fetches that many X and W panels.  Measured on the
 //     14B shapes (ms, groups of 16 / 32 / 64 m-tiles): FFN up 7.37 / 7.22 / 7.17, FFN down
 //     (N = 5120) 7.22 / 7.19 / 7.30, o 2.74 / 2.74 / 2.71; 128 was 10 % slower on FFN up.
+//   - Token-major operands (TR, the weight gradient grad_q^T x_q on the tensors as they lie):
+//     the same loop with k-major LDS stages and fragments built by transposing reads
+//     (ds_read_b64_tr_b16), the same products in the same order.
+//   - Split tail: for a grid of a few waves whose last one would leave most CUs idle, the tail
+//     tiles are computed over k ranges into fp32 partials (EPI 2) that k_split_reduce adds in a
+//     fixed order.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -151,8 +157,9 @@ template <int I, bool TR> __device__ __forceinline__ void adv(Ctx<TR> &c)
     }
 }
 
-// DTL item i (8 rows x 128 B, rows (8 wave + i) * 8 ..) of the X (OP 0) or W (OP 1) stage at
-// the current source offsets, into the stage at `stage`.
+// DTL item i of the X (OP 0) or W (OP 1) stage at the current source offsets, into the stage at
+// `stage`: 1 KB at (8 wave + i) KB, rows (8 wave + i) * 8 .. + 7 x 128 B, or (TR) one half of the
+// columns of 4 k-rows.
 template <int OP, bool TR> __device__ __forceinline__ void issue_dtl(Ctx<TR> &c, uint32_t stage, int i)
 {
     const uint32_t m0v = __builtin_amdgcn_readfirstlane(stage + (c.wave * 8u + uint32_t(i)) * 1024u);
