@@ -200,6 +200,49 @@ def time_ffn(pkg, torch, x, reps):
     return out
 
 
+def time_module_graph(pkg, torch, M, reps):
+    """HIF8Linear.forward (prepacked, no autograd) on the 1.3B 480P shapes, called eagerly and
+    replayed from a HIP graph (torch.cuda.CUDAGraph) that captured the same call: at these sizes
+    the four launches of a step (amax, fake quant, weight decode, GEMM) and their host-side
+    overhead are a visible part of it."""
+    out = {}
+    for name, n_, k_, seed in (("qkvo", 1536, 1536, 2), ("ffn_up", 8960, 1536, 3), ("ffn_down", 1536, 8960, 4)):
+        x, _, _ = make_inputs(torch, M, k_, n_, seed=seed, outlier_channels=8)
+        torch.manual_seed(seed)
+        lin = pkg.HIF8Linear(k_, n_, bias=True, device=x.device, dtype=torch.bfloat16)
+        with torch.no_grad():
+            lin.weight.normal_(0, 0.02)
+            lin.bias.zero_()
+            lin.prepack()
+            side = torch.cuda.Stream()
+            side.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(side):
+                for _ in range(2):
+                    lin(x)
+            torch.cuda.current_stream().wait_stream(side)
+            torch.cuda.synchronize()
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                lin(x)
+            res = {}
+            for label, fn in (("eager_ms", lambda: lin(x)), ("graph_ms", graph.replay)):
+                for _ in range(3):
+                    fn()
+                torch.cuda.synchronize()
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record()
+                for _ in range(reps):
+                    fn()
+                e1.record()
+                torch.cuda.synchronize()
+                res[label] = round(e0.elapsed_time(e1) / reps, 4)
+            res["graph_TFLOPs"] = round(2.0 * M * n_ * k_ / (res["graph_ms"] * 1e-3) / 1e12, 1)
+            out[name] = res
+            del graph
+        del lin, x
+    return out
+
+
 def time_backward(pkg, torch, x, packed, reps):
     """The backward of the FFN-up HIF8Linear (hif8_linear.py:88-111) at the 14B 720P shape: the
     gradient's _quant with scale_max 224, dgrad grad_q [M, N] @ w_q [N, K] (the transposed codes
@@ -883,6 +926,10 @@ def main():
         extra_shapes["c2"] = {name: linear_line(32760, n_, k_, seed, 8)
                               for name, n_, k_, seed in (("qkvo", 1536, 1536, 2), ("ffn_up", 8960, 1536, 3),
                                                          ("ffn_down", 1536, 8960, 4))}
+        try:
+            extra_shapes["c2"]["module_eager_vs_graph"] = time_module_graph(pkg, torch, 32760, args.steps)
+        except Exception as ex:  # informative only
+            extra_shapes["c2"]["module_eager_vs_graph"] = {"error": repr(ex)}
 
     # the vendor bf16 GEMM on the same shape, for context (not part of the product)
     vendor = None

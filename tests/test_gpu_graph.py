@@ -1,0 +1,103 @@
+"""The inference paths under HIP graph capture (torch.cuda.CUDAGraph): HIF8Linear on both GEMM
+routes, the fused FFN (GELU-statistic GEMM, settle kernel, GELU fake quant) and the modulated
+LayerNorm producer launch only kernels -- no host synchronisation, allocation outside torch's
+graph pool, or memset nodes -- so a captured step replays them.  Each graph is replayed several
+times with eager work on the same modules and states in between, and every replay is compared
+bit for bit with the eager result."""
+from __future__ import annotations
+
+import pytest
+
+torch = pytest.importorskip("torch")
+pytestmark = pytest.mark.gpu
+
+DEV = "cuda:0"
+
+
+def capture(fn):
+    """Warm fn up on a side stream, then capture one call; returns (graph, output)."""
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        for _ in range(2):
+            fn()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        out = fn()
+    return graph, out
+
+
+def bits(t):
+    return t.view(torch.int16)
+
+
+def replay_and_check(graph, out, ref, eager):
+    for rep in range(3):
+        eager()                       # eager work on the same modules and states
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(bits(out), bits(ref)), f"replay {rep}"
+
+
+@pytest.mark.parametrize("M", [1000, 9000])   # the fused route, and the decode-once route from 8192 rows
+def test_hif8linear_forward_replays(pkg, M):
+    print(f"[graph] HIF8Linear M={M}", flush=True)
+    torch.manual_seed(M)
+    lin = pkg.HIF8Linear(1024, 768, bias=True, device=DEV, dtype=torch.bfloat16)
+    with torch.no_grad():
+        lin.bias.normal_(0, 0.02)
+        lin.prepack()
+        x = torch.randn(M, 1024, device=DEV).to(torch.bfloat16)
+        x2 = (x * 3).contiguous()
+        ref = lin(x).clone()
+        graph, out = capture(lambda: lin(x))
+        replay_and_check(graph, out, ref, lambda: lin(x2))
+
+
+def test_fused_ffn_replays(pkg):
+    """The GELU route: the up-projection's statistic settles the down-projection's scale inside
+    the graph, and an eager call on other data between replays leaves nothing behind."""
+    print("[graph] HIF8FFN", flush=True)
+    torch.manual_seed(5)
+    ffn = pkg.HIF8FFN(512, 1536, device=DEV, dtype=torch.bfloat16)
+    with torch.no_grad():
+        for p in ffn.parameters():
+            p.normal_(0, 0.05)
+        ffn[0].prepack()
+        ffn[2].prepack()
+        x = torch.randn(2048, 512, device=DEV).to(torch.bfloat16)
+        x2 = (-2 * x).contiguous()   # mostly negative pre-activations: the pending path
+        ref = ffn(x).clone()
+        graph, out = capture(lambda: ffn(x))
+        replay_and_check(graph, out, ref, lambda: ffn(x2))
+
+
+def test_modulated_norm_quant_replays(pkg):
+    print("[graph] modulated_norm_quant", flush=True)
+    g = torch.Generator(device=DEV).manual_seed(7)
+    x = torch.randn(4096, 1024, generator=g, device=DEV).to(torch.bfloat16)
+    shift = torch.randn(1, 1024, generator=g, device=DEV).to(torch.bfloat16)
+    scale = (torch.randn(1, 1024, generator=g, device=DEV) * 0.1).to(torch.bfloat16)
+    with torch.no_grad():
+        ref, _ = pkg.modulated_norm_quant(x, shift, scale, 1e-6, 15.0)
+        ref = ref.clone()
+        graph, out = capture(lambda: pkg.modulated_norm_quant(x, shift, scale, 1e-6, 15.0)[0])
+        replay_and_check(graph, out, ref, lambda: pkg.modulated_norm_quant(x * 2, shift, scale, 1e-6, 15.0))
+
+
+def test_static_producer_replays(pkg):
+    """The allocation-free producer (static device workspace) is what graph-captured callers that
+    cannot allocate use: its workspace clear is a kernel, not a memset node."""
+    print("[graph] modulated_norm_quant_static", flush=True)
+    g = torch.Generator(device=DEV).manual_seed(8)
+    x = torch.randn(3000, 1024, generator=g, device=DEV).to(torch.bfloat16)
+    shift = torch.randn(1, 1024, generator=g, device=DEV).to(torch.bfloat16)
+    scale = (torch.randn(1, 1024, generator=g, device=DEV) * 0.1).to(torch.bfloat16)
+    with torch.no_grad():
+        ref, _ = pkg.modulated_norm_quant(x, shift, scale, 1e-6, 15.0)
+        ref = ref.clone()
+        graph, out = capture(lambda: pkg.modulated_norm_quant_static(x, shift, scale, 1e-6, 15.0))
+        replay_and_check(graph, out, ref, lambda: pkg.modulated_norm_quant_static(x[:1000] * 2, shift, scale, 1e-6, 15.0))
