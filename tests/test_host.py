@@ -204,3 +204,19 @@ def test_lds_encode_table(hostlib, R):
     idx = np.clip(u, lo.value, hi.value) - lo.value
     xf = (u << 16).view(np.float32)
     assert np.array_equal(tab[idx], R.encode_npu(xf) & 0x7F)
+
+
+def test_split_tail_plan_on_256_cus(pkg):
+    """The split-tail plan (hif8_linear_split_workspace_bytes) as it is made for MI355X's 256 CUs
+    (without a GPU the library assumes 256): only grids under 8 waves whose tail fills at most
+    half the CUs split, into at most 8 ranges of at least 8 k-steps; 256 KB of fp32 per range."""
+    L = pkg._lib.load()
+    tile = 256 * 256 * 4
+    assert L.hif8_linear_split_workspace_bytes(13824, 5120, 75600) == 56 * 4 * tile   # 1080 tiles: 4 ranges
+    assert L.hif8_linear_split_workspace_bytes(4352, 4096, 4100) == 16 * 8 * tile     # 272 tiles: 8 ranges
+    assert L.hif8_linear_split_workspace_bytes(4352, 4096, 1024) == 16 * 2 * tile     # 16 k-steps: 2 ranges
+    assert L.hif8_linear_split_workspace_bytes(4352, 4096, 960) == 0                  # 15 k-steps: no split
+    assert L.hif8_linear_split_workspace_bytes(75600, 5120, 13824) == 0               # 23 waves
+    assert L.hif8_linear_split_workspace_bytes(4096, 4096, 75648) == 0                # whole waves
+    assert L.hif8_linear_split_workspace_bytes(9216, 4096, 75648) == 64 * 4 * tile    # 576 tiles: tail of 64
+    assert L.hif8_linear_split_workspace_bytes(12288, 5120, 75648) == 0               # tail of 192 > 128
