@@ -641,6 +641,18 @@ def _cpu_info():
     return model or platform.machine(), details, {n: n in flags for n in names}
 
 
+def _mem_available():
+    """MemAvailable from /proc/meminfo in bytes (None where it cannot be read)."""
+    try:
+        with open("/proc/meminfo") as f:
+            for line in f:
+                if line.startswith("MemAvailable:"):
+                    return int(line.split()[1]) * 1024
+    except (OSError, ValueError, IndexError):
+        pass
+    return None
+
+
 def _cpu_threads():
     """Threads for the CPU baseline: every CPU this process may run on (its affinity set), capped
     by OMP_NUM_THREADS when the environment sets it (the GPU box grants each one-GPU job a CPU
@@ -672,12 +684,14 @@ def _time_cpu(fn, warm, max_runs=3, budget_s=15.0):
 def cpu_baseline(torch, M, K, N, sample_rows=4096, target_s=10.0):
     """The reference CPU path (torch ops: _quant + quant_hif8 + F.linear in bf16) on the host.
 
-    Headline (``value``): the 14B FFN-up shape on a bounded sample -- a [sample_rows, K] slice of
-    x (quantise + GEMM against the quantised W) repeated until about ``target_s`` seconds of CPU
-    work, and the per-call weight quantisation twice; the full step is the weight part plus the
-    slice time scaled to M (both the qdq and the GEMM are linear in M).  Beside it, BASELINE
-    config 1 (the qdq of a [4096, 5120] tensor) and config 2 (the three Wan-1.3B 480P linears) at
-    full size: a warm-up on a slice, then the median of three runs."""
+    Headline (``value``): the 14B FFN-up step.  A [sample_rows, K] slice of x (quantise + GEMM
+    against the quantised W) is repeated until about ``target_s`` seconds of CPU work, and the
+    per-call weight quantisation runs twice; the step estimate is the weight part plus the slice
+    time scaled to M (both the qdq and the GEMM are linear in M).  When the host has the memory
+    (twice the ~12 GB the step holds), the whole step then runs once at M rows and ``value`` is
+    that run; otherwise ``value`` is the estimate.  Beside it, BASELINE config 1 (the qdq of a
+    [4096, 5120] tensor) and config 2 (the three Wan-1.3B 480P linears) at full size: a warm-up
+    on a slice, then the median of three runs."""
     sys.path.insert(0, ROOT)
     import numpy as np
     import torch.nn.functional as F
@@ -708,9 +722,30 @@ def cpu_baseline(torch, M, K, N, sample_rows=4096, target_s=10.0):
             break
     total = time.perf_counter() - t_start
     tw, ts = median(t_w), median(t_slice)
-    t_full = tw + (M / sample_rows) * ts
+    t_est = tw + (M / sample_rows) * ts
+    del xq
+
+    # the whole step at M rows, once, when the host has room for it (x, its fp32 temporaries
+    # and the [M, N] bf16 output: about 12 GB at the 14B FFN-up shape); x is the slice tiled to M
+    # rows, so its amax is the slice's
+    full = None
+    need = 4 * M * K * 4 + 2 * M * N
+    avail = _mem_available()
+    if avail is not None and avail >= 2 * need:
+        reps = -(-M // sample_rows)
+        xf = x.repeat(reps, 1)[:M].contiguous()
+        t0 = time.perf_counter()
+        wq2, _ = R.quant_torch_cpu(w, 15.0)
+        xq, _ = R.quant_torch_cpu(xf, 15.0)
+        y = F.linear(xq, wq2)
+        t_one = time.perf_counter() - t0
+        full = {"M": M, "s": round(t_one, 3), "TFLOPs": round(2.0 * M * N * K / t_one / 1e12, 4),
+                "what": "W qdq + x qdq + bf16 F.linear at full size, one run (its first touch of "
+                        "the output and temporaries included, as in the reference's own call)"}
+        del xf, xq, y, wq2
+    t_full = full["s"] if full else t_est
     value = 2.0 * M * N * K / t_full / 1e12
-    del x, w, wq, xq
+    del x, w, wq
 
     # config 1: _quant of the [4096, 5120] bf16 tensor (N(0, 0.02), 0.1 % outliers x50, seed 0)
     c1_bits = R.c1_input(0)
@@ -737,10 +772,13 @@ def cpu_baseline(torch, M, K, N, sample_rows=4096, target_s=10.0):
     model, details, flags = _cpu_info()
     return {
         "value": round(value, 4), "unit": "TFLOP/s", "cores": threads, "kind": "port",
-        "sample": (f"reference CPU path (torch ops, bf16 F.linear) on the FFN-up shape: W[{N},{K}] qdq x2 "
+        "sample": ((f"one full step at M={M} ({t_full:.2f}s); " if full else
+                    f"no full-size step (host memory available {avail} B, wanted {2 * need} B); ") +
+                   f"reference CPU path (torch ops, bf16 F.linear) on the FFN-up shape: W[{N},{K}] qdq x2 "
                    f"(median {tw:.2f}s) and {len(t_slice)} reps of an x[{sample_rows},{K}] slice, qdq + GEMM "
-                   f"(median {ts:.3f}s), {total:.1f}s of CPU work; one step at M={M} = W qdq + "
-                   f"{M / sample_rows:.2f} slices = {t_full:.2f}s"),
+                   f"(median {ts:.3f}s), {total:.1f}s of CPU work; estimated step at M={M} = W qdq + "
+                   f"{M / sample_rows:.2f} slices = {t_est:.2f}s"),
+        "full_step": full, "slice_estimate_s": round(t_est, 3),
         "cpu_model": model, "cpu_lscpu": details, "cpu_flags": flags, "os_cpu_count": os.cpu_count(),
         "affinity_cpus": len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else None,
         "omp_num_threads": os.environ.get("OMP_NUM_THREADS"),
