@@ -358,6 +358,36 @@ int hif8_ln_affine_fake_quant(const uint16_t *x, const float *weight, const floa
                               int64_t dim, const float *stats, const void *state, int semantics, uint16_t *x_q,
                               uint16_t *y, hif8_stream_t stream);
 
+/* ---------------------------------------------------------------------------
+ * The DiT's attention with the o projection's amax in its epilogue: attention_with_mask
+ * (ospnext/modules/attention.py:460-518, the SDPA branch, attn_mask_kv as a list of the kept
+ * keys) followed by the amax of _quant at the o projection (osp_next.py:777 ->
+ * hif8_linear.py:42-46).
+ *
+ * out[b, i, h, :] = sum_j softmax_j(softmax_scale * q[b, i, h, :] . k[b, j, h, :]) v[b, j, h, :]
+ * over the keys j kept for batch b; bf16 in and out, fp32 scores and accumulation.  q, k, v, out
+ * are bf16 [batch][tokens][heads][head_dim] with token row strides row_strides[0..3] and batch
+ * strides batch_strides[0..3] (elements, in the order q, k, v, out; a batch stride may be 0,
+ * e.g. keys shared by every batch).  head_dim must be 128; strides multiples of 8, at least
+ * heads * 128; (n_kv - 1) * row stride * 2 + 256 below 2^31 for k and v; 16-byte aligned tensors.
+ * key_idx NULL and key_count NULL: every key 0 .. n_kv - 1.  key_count [batch] alone: the first
+ * key_count[b] keys.  key_idx [batch][idx_batch_stride] with key_count: the key rows
+ * key_idx[b][0 .. key_count[b] - 1] (entries clamped to [0, n_kv)).  A query with no key gets
+ * zeros (the reference raises for a sequence whose keys are all masked).
+ * row_strides and batch_strides are host arrays of 4.
+ * out_state NULL: attention only.  Otherwise the o projection's input state: the kernel folds the
+ * amax of out and a one-workgroup kernel after it writes amax, scale (rule for scale_max) and
+ * tables exactly as hif8_absmax_scale(out, out_state_dtype, ...) over out would, so the
+ * quantisation of out needs no amax pass.  out_state_dtype HIF8_DTYPE_BF16_AS_F32: the o input
+ * is out as fp32 values (the self-attention, whose q is fp32 after the rotary embedding);
+ * HIF8_DTYPE_BF16: out itself (the cross-attention).
+ */
+int hif8_attention_fwd(const uint16_t *q, const uint16_t *k, const uint16_t *v, uint16_t *out, int64_t batch,
+                       int64_t n_q, int64_t n_kv, int64_t heads, int64_t head_dim, const int64_t *row_strides,
+                       const int64_t *batch_strides, const int32_t *key_idx, int64_t idx_batch_stride,
+                       const int32_t *key_count, float softmax_scale, void *out_state, int out_state_dtype,
+                       float scale_max, hif8_stream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -56,8 +56,11 @@ from .norm import (WanLayerNorm, affine_norm_quant, grouped_weight, modulate, mo
                    modulated_norm_quant_static, qkv_from_modulated_norm)
 from .hif8_attention import (  # noqa: F401
     _HIF8QKVQuantFunction,
+    attention_fwd,
+    attention_fwd_ok,
     attention_with_mask,
     hif8_attention_with_mask,
+    key_list,
     scaled_dot_product_attention_with_mask,
 )
 from .qlinear import (  # noqa: F401
@@ -82,5 +85,6 @@ __all__ = [
     "save_packed", "load_packed", "pack_state_dict", "packed_from_codes", "fused_shape_ok", "linear_any",
     "linear_fwd_gelu_stat", "gelu_absmax_scale", "gelu_fake_quant", "HIF8FFN", "WanLayerNorm", "modulate", "modulated_norm_quant", "affine_norm_quant",
     "qkv_from_modulated_norm", "modulated_norm_quant_static", "GroupedWeight", "grouped_ok", "linear_fwd_grouped", "grouped_weight",
+    "attention_fwd", "attention_fwd_ok", "key_list",
     "dit", "OSPNextAttentionBlock", "OSPNextBlocks", "linear_fwd_wq", "linear_fwd_wq_split", "linear_wgrad", "transpose_bf16", "wgrad_ok",
 ]

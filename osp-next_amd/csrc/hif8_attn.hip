@@ -1,0 +1,409 @@
+// Attention forward of the DiT block for MI355X (gfx950), with the HiF8 amax of its output folded
+// into the o projection's quantisation state.
+//
+// The reference's attention (attention_with_mask, attention.py:460-518, SDPA branch) computes, per
+// batch b, head h and query i,
+//   out[b, i, h] = sum_j softmax_j(q[b, i, h] . k[b, j, h] / sqrt(128)) v[b, j, h]
+// over the keys j its key mask keeps, in bf16 with fp32 accumulation, and the o projection then
+// runs _quant on that output (hif8_linear.py:42-50 via osp_next.py:777): a full pass for amax|out|
+// before the quantisation pass.  Here the attention kernel's epilogue keeps the max of the
+// magnitudes it stores, so the amax pass is not needed.
+//
+// Design (flash attention, online softmax; head_dim 128):
+//   - One workgroup per 256 queries of one (batch, head); 8 waves, two per SIMD, each owning 32
+//     queries.  Keys go in tiles of 64: K and V tiles (16 KB each) are loaded global -> LDS with
+//     buffer_load ... lds into one of two buffers while the other is computed.
+//   - Scores are computed transposed, S^T = K Q^T, with v_mfma_f32_16x16x32_bf16: the A operand is
+//     a K fragment from LDS, the B operand the wave's Q fragments, held in registers for the whole
+//     kernel.  In the accumulator layout a lane holds one query and 4 keys of each 16 x 16 block,
+//     which is exactly the B-operand layout of P^T for O^T = V^T P^T (the key order inside an MFMA's
+//     reduction is free, and both operands use the same one), so P goes from the softmax to the
+//     matrix cores without leaving the lane.  The V^T fragments come from LDS through
+//     ds_read_b64_tr_b16 (transposing reads).
+//   - Online softmax in the log2 domain with a lazily moved reference: the running max a tile's
+//     exponentials are taken against only moves when a tile's max exceeds it by more than 8 (the
+//     exponentials stay below 2^8 in between), so the O accumulators are rescaled a handful of times
+//     per query instead of at every tile.  Row sums are per-lane partials, reduced once at the end.
+//   - Keys: an optional per-batch list of key rows (the rows the key mask keeps) and count; tiles
+//     past the count are masked to -inf.  The whole key tensor is never gathered.
+//   - Tile order: workgroup w runs on XCD w % 8; consecutive query tiles of one head are given to
+//     one XCD, so the CUs of an XCD stream the same K/V tiles through its L2.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "hif8_internal.h"
+#include "hif8_state_dev.h"
+
+namespace hif8 {
+namespace attn {
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kD = 128;                  // head dim
+constexpr int kBN = 64;                  // keys per tile
+constexpr int kWaves = 8;
+constexpr int kThreads = kWaves * 64;
+constexpr int kQW = 32;                  // queries per wave
+constexpr int kBM = kWaves * kQW;        // queries per workgroup
+constexpr uint32_t kTile = kBN * kD * 2;  // bytes of one K or V tile
+constexpr uint32_t kLds = 4 * kTile;      // K and V, two buffers each
+constexpr float kLazy = 8.0f;             // log2 headroom before the reference max moves
+
+struct Params {
+    const uint16_t *q, *k, *v;
+    uint16_t *out;
+    int64_t q_rs, k_rs, v_rs, o_rs;  // token row strides (elements)
+    int64_t q_bs, k_bs, v_bs, o_bs;  // batch strides (elements)
+    const int32_t *key_idx;          // [batch][idx_bs] key rows, or null (all n_kv keys in order)
+    const int32_t *key_count;        // [batch] keys used, or null (n_kv)
+    int64_t idx_bs;
+    int n_q, n_kv, heads, q_tiles;
+    float c;                         // softmax scale * log2(e)
+    State *o_st;                     // amax of the output folded here, or null
+    uint32_t o_shift;                // 16: folded as fp32 magnitude bits, 0: as bf16 bits
+};
+
+#define ASMV asm volatile
+
+// 64 lanes x 16 B from the buffer (voffset per lane) into LDS at m0v + lane * 16
+__device__ __forceinline__ void dtl_load(uint32_t m0v, uint32_t voff, const u32x4 &rs)
+{
+    ASMV("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds" ::"s"(m0v), "v"(voff), "s"(rs) : "memory", "m0");
+}
+
+__device__ __forceinline__ uint32_t pk_bf16(float lo, float hi)
+{
+    typedef float f32x2 __attribute__((ext_vector_type(2)));
+    typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+    f32x2 v = {lo, hi};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2));
+}
+
+__device__ __forceinline__ f32x4 mfma(const u32x4 &a, const u32x4 &b, const f32x4 &c)
+{
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
+                                                   0, 0, 0);
+}
+
+__device__ __forceinline__ u32x2 ld_tr(const uint8_t *lds_base, uint32_t off)
+{
+    typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+    const i16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4 *)(lds_base + off));
+    return __builtin_bit_cast(u32x2, v);
+}
+
+// The physical key row of logical key kk, or row 0 for keys past the count (loaded, then masked).
+__device__ __forceinline__ uint32_t key_row(int raw, int kk, int nk, int n_kv)
+{
+    if (kk >= nk) return 0u;
+    return uint32_t(raw < 0 ? 0 : (raw >= n_kv ? n_kv - 1 : raw));
+}
+
+// LDS layout of a tile (64 keys x 128 dims, bf16):
+//   K: key row r at r * 256, its 16-byte chunk c (dims 8c .. 8c + 7) at ((c ^ (r & 15)) * 16): the
+//      16 rows an MFMA fragment read takes hit 16 distinct chunk positions, all 64 banks.
+//   V: 128-byte blocks of 4 keys x 16 dims; block (q, P) -- keys 4q .. 4q + 3, dims 16P .. 16P + 15
+//      -- at (8q + (P ^ (q & 1))) * 128, key 4q + e at +32e.  A ds_read_b64_tr_b16 gives lane l of
+//      each 16-lane group element j of the four values loaded by lane 4j + (l % 16) / 4 of the group,
+//      at position l % 4: lane 4j + u of group g loading dims 16P + 4u .. +3 of key 4g + j gives
+//      lane (d, g) the keys 4g .. 4g + 3 of dim 16P + d.  Groups g and g + 1 (read in the same
+//      cycle) read blocks of opposite parity, opposite halves of the banks.
+//   A DTL instruction writes 1 KB: 4 K rows, or the 8 V blocks of one 4-key group.
+__global__ __launch_bounds__(kThreads, 1) void k_attn_fwd(const Params p)
+{
+    __shared__ __attribute__((aligned(1024))) uint8_t smem[kLds];
+    const uint32_t tid = threadIdx.x, lane = tid & 63u;
+    const uint32_t wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const uint32_t cq = lane & 15u, g = lane >> 4;
+
+    // workgroup -> (batch, head, query tile), consecutive query tiles of a head on one XCD
+    const int nwg = gridDim.x, w = blockIdx.x;
+    const int per = nwg >> 3, rem = nwg & 7, xcd = w & 7, slot = w >> 3;
+    const int L = xcd < rem ? xcd * (per + 1) + slot : rem * (per + 1) + (xcd - rem) * per + slot;
+    const int qt = L % p.q_tiles, bh = L / p.q_tiles;
+    const int h = bh % p.heads, b = bh / p.heads;
+
+    int nk = p.n_kv;
+    if (p.key_count) {
+        nk = p.key_count[b];
+        nk = nk < 0 ? 0 : (nk > p.n_kv ? p.n_kv : nk);
+        if (p.key_idx && int64_t(nk) > p.idx_bs) nk = int(p.idx_bs);
+    }
+    const int ntiles = (nk + kBN - 1) / kBN;
+    const int32_t *idx = p.key_idx ? p.key_idx + int64_t(b) * p.idx_bs : nullptr;
+
+    // buffer resources of this (batch, head)'s K and V: rows of 256 bytes at the row stride; the
+    // range ends with the last key row
+    u32x4 rk, rv;
+    {
+        const uint64_t ka = uint64_t(p.k + int64_t(b) * p.k_bs + int64_t(h) * kD);
+        const uint64_t va = uint64_t(p.v + int64_t(b) * p.v_bs + int64_t(h) * kD);
+        const uint32_t kn = uint32_t(int64_t(p.n_kv - 1) * p.k_rs * 2 + kD * 2);
+        const uint32_t vn = uint32_t(int64_t(p.n_kv - 1) * p.v_rs * 2 + kD * 2);
+        rk = u32x4{uint32_t(ka), uint32_t(ka >> 32), kn, 0x00020000u};
+        rv = u32x4{uint32_t(va), uint32_t(va >> 32), vn, 0x00020000u};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            rk[i] = __builtin_amdgcn_readfirstlane(rk[i]);
+            rv[i] = __builtin_amdgcn_readfirstlane(rv[i]);
+        }
+    }
+    const uint32_t krs = uint32_t(p.k_rs * 2), vrs = uint32_t(p.v_rs * 2);
+    // this lane's share of the DTL: K rows kr[j] (instructions 2 wave + j) and V rows vr[j]
+    uint32_t kr[2], kch[2], vr[2], vcol[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const uint32_t it = 2u * wave + uint32_t(j);
+        kr[j] = 4u * it + (lane >> 4);
+        kch[j] = ((lane & 15u) ^ (kr[j] & 15u)) * 16u;
+        vr[j] = 4u * it + ((lane & 7u) >> 1);
+        vcol[j] = (16u * (((lane >> 3) ^ (it & 1u))) + 8u * (lane & 1u)) * 2u;
+    }
+    const uint32_t lds0 = uint32_t(uintptr_t(smem));
+    // raw key list entries of the next tile for this lane's four rows
+    int nraw[4] = {0, 0, 0, 0};
+    auto fetch_raw = [&](int t) {
+        if (idx) {
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const int kk = t * kBN + int(kr[j]), kv = t * kBN + int(vr[j]);
+                nraw[j] = kk < nk ? idx[kk] : 0;
+                nraw[2 + j] = kv < nk ? idx[kv] : 0;
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                nraw[j] = t * kBN + int(kr[j]);
+                nraw[2 + j] = t * kBN + int(vr[j]);
+            }
+        }
+    };
+    auto issue_tile = [&](int t) {
+        const uint32_t buf = uint32_t(t & 1);
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const uint32_t it = 2u * wave + uint32_t(j);
+            const uint32_t rowk = key_row(nraw[j], t * kBN + int(kr[j]), nk, p.n_kv);
+            const uint32_t rowv = key_row(nraw[2 + j], t * kBN + int(vr[j]), nk, p.n_kv);
+            dtl_load(__builtin_amdgcn_readfirstlane(lds0 + buf * kTile + it * 1024u), rowk * krs + kch[j], rk);
+            dtl_load(__builtin_amdgcn_readfirstlane(lds0 + 2u * kTile + buf * kTile + it * 1024u), rowv * vrs + vcol[j],
+                     rv);
+        }
+    };
+
+    if (ntiles > 0) {
+        fetch_raw(0);
+        issue_tile(0);
+        if (ntiles > 1) fetch_raw(1);
+    }
+
+    // Q fragments: lane (cq, g) holds dims 32 pp + 8 g .. +7 of query 16 qb + cq of the wave's 32
+    const int qbase = qt * kBM + int(wave) * kQW;
+    u32x4 qf[2][4];
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) {
+        const int row = qbase + 16 * qb + int(cq);
+        const uint16_t *qr = p.q + int64_t(b) * p.q_bs + int64_t(row < p.n_q ? row : 0) * p.q_rs + int64_t(h) * kD;
+#pragma unroll
+        for (int pp = 0; pp < 4; ++pp) {
+            qf[qb][pp] = *(const u32x4 *)(qr + 32 * pp + 8 * g);
+            if (row >= p.n_q) qf[qb][pp] = u32x4{0u, 0u, 0u, 0u};
+        }
+    }
+
+    f32x4 o[8][2];
+#pragma unroll
+    for (int d = 0; d < 8; ++d)
+        o[d][0] = o[d][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float mref[2] = {-__builtin_inff(), -__builtin_inff()};
+    float lsum[2] = {0.f, 0.f};
+    const float c = p.c;
+
+    // fragment read offsets (bytes) inside a tile
+    const uint32_t kfrag = cq * 256u;                       // + kb * 4096, chunk ((4 pp + g) ^ cq) * 16
+    const uint32_t vfrag = (8u * g) * 128u + 32u * ((lane & 15u) >> 2) + 8u * (lane & 3u);  // + block
+
+    for (int t = 0; t < ntiles; ++t) {
+        ASMV("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        if (t + 1 < ntiles) {
+            issue_tile(t + 1);
+            if (t + 2 < ntiles) fetch_raw(t + 2);
+        }
+        const uint8_t *ks = smem + uint32_t(t & 1) * kTile;
+        const uint8_t *vs = smem + 2u * kTile + uint32_t(t & 1) * kTile;
+
+        // S^T = K Q^T for the 64 keys x 32 queries of this wave
+        f32x4 s[4][2];
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) {
+            s[kb][0] = s[kb][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int pp = 0; pp < 4; ++pp) {
+                const u32x4 kf = *(const u32x4 *)(ks + kb * 4096 + kfrag + (((4u * pp + g) ^ cq) << 4));
+                s[kb][0] = mfma(kf, qf[0][pp], s[kb][0]);
+                s[kb][1] = mfma(kf, qf[1][pp], s[kb][1]);
+            }
+        }
+        // keys past the count (last tile only)
+        if ((t + 1) * kBN > nk) {
+#pragma unroll
+            for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+                    if (t * kBN + 16 * kb + 4 * int(g) + i >= nk) s[kb][0][i] = s[kb][1][i] = -__builtin_inff();
+        }
+
+        u32x4 pf[2][2];
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb) {
+            float mx = s[0][qb][0];
+#pragma unroll
+            for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) mx = __builtin_fmaxf(mx, s[kb][qb][i]);
+            mx = __builtin_fmaxf(mx, __shfl_xor(mx, 16, 64));
+            mx = __builtin_fmaxf(mx, __shfl_xor(mx, 32, 64));
+            const float mt = mx * c;
+            if (__builtin_amdgcn_ballot_w64(mt > mref[qb] + kLazy)) {
+                const float mn = __builtin_fmaxf(mref[qb], mt);
+                const float alpha = __builtin_amdgcn_exp2f(mref[qb] - mn);
+                lsum[qb] *= alpha;
+#pragma unroll
+                for (int d = 0; d < 8; ++d) o[d][qb] *= alpha;
+                mref[qb] = mn;
+            }
+            const float nm = -mref[qb];
+            float e[4][4];
+#pragma unroll
+            for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    e[kb][i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kb][qb][i], c, nm));
+                    lsum[qb] += e[kb][i];
+                }
+#pragma unroll
+            for (int kc = 0; kc < 2; ++kc)
+                pf[qb][kc] = u32x4{pk_bf16(e[2 * kc][0], e[2 * kc][1]), pk_bf16(e[2 * kc][2], e[2 * kc][3]),
+                                   pk_bf16(e[2 * kc + 1][0], e[2 * kc + 1][1]),
+                                   pk_bf16(e[2 * kc + 1][2], e[2 * kc + 1][3])};
+        }
+
+        // O^T += V^T P^T
+#pragma unroll
+        for (int d = 0; d < 8; ++d) {
+#pragma unroll
+            for (int kc = 0; kc < 2; ++kc) {
+                const uint32_t blk = (64u * kc + (uint32_t(d) ^ (g & 1u))) * 128u + vfrag;
+                const u32x2 lo = ld_tr(vs, blk), hi = ld_tr(vs, blk + 4096u);
+                const u32x4 vf = u32x4{lo.x, lo.y, hi.x, hi.y};
+                o[d][0] = mfma(vf, pf[0][kc], o[d][0]);
+                o[d][1] = mfma(vf, pf[1][kc], o[d][1]);
+            }
+        }
+    }
+
+    // epilogue: O / l, rounded to bf16; lane (cq, g) holds dims 16 d + 4 g .. +3 of query 16 qb + cq
+    uint32_t amax = 0;
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb) {
+        float l = lsum[qb];
+        l += __shfl_xor(l, 16, 64);
+        l += __shfl_xor(l, 32, 64);
+        const float inv = l > 0.f ? 1.0f / l : 0.f;
+        const int row = qbase + 16 * qb + int(cq);
+        if (row < p.n_q) {
+            uint16_t *orow = p.out + int64_t(b) * p.o_bs + int64_t(row) * p.o_rs + int64_t(h) * kD + 4 * g;
+#pragma unroll
+            for (int d = 0; d < 8; ++d) {
+                const u32x2 wv = u32x2{pk_bf16(o[d][qb][0] * inv, o[d][qb][1] * inv),
+                                       pk_bf16(o[d][qb][2] * inv, o[d][qb][3] * inv)};
+                *(u32x2 *)(orow + 16 * d) = wv;
+                const uint32_t m0 = wv.x & 0x7FFF7FFFu, m1 = wv.y & 0x7FFF7FFFu;
+                amax = max(amax, max(max(m0 & 0xFFFFu, m0 >> 16), max(m1 & 0xFFFFu, m1 >> 16)));
+            }
+        }
+    }
+    if (p.o_st) {
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) amax = max(amax, (uint32_t)__shfl_xor((int)amax, off, 64));
+        // bf16 values the o projection takes as fp32: the fp32 magnitude bits of the same value
+        if (lane == 0)
+            __hip_atomic_fetch_max(&p.o_st->amax_acc, amax << p.o_shift, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
+// The o projection's state after the attention: amax of the output (bf16, or as fp32 values),
+// its scale for smax and the tables.
+__global__ __launch_bounds__(256) void k_attn_amax_settle(State *__restrict__ st, int dtype, float smax)
+{
+    __shared__ uint32_t lds[1];
+    settle_amax(st, dtype, smax, lds);
+}
+
+}  // namespace attn
+
+extern "C" int hif8_attention_fwd(const uint16_t *q, const uint16_t *k, const uint16_t *v, uint16_t *out,
+                                  int64_t batch, int64_t n_q, int64_t n_kv, int64_t heads, int64_t head_dim,
+                                  const int64_t *row_strides, const int64_t *batch_strides, const int32_t *key_idx,
+                                  int64_t idx_batch_stride, const int32_t *key_count, float softmax_scale,
+                                  void *out_state, int out_state_dtype, float scale_max, hif8_stream_t stream)
+{
+    using namespace attn;
+    if (!q || !k || !v || !out || !row_strides || !batch_strides) return HIF8_ERR_ARG;
+    if (batch <= 0 || n_q <= 0 || n_kv <= 0 || heads <= 0 || !(softmax_scale > 0.0f)) return HIF8_ERR_ARG;
+    if (key_idx && (!key_count || idx_batch_stride <= 0)) return HIF8_ERR_ARG;
+    if (out_state && (!(scale_max > 0.0f) || (out_state_dtype != kBF16 && out_state_dtype != kBF16F32)))
+        return HIF8_ERR_ARG;
+    if (head_dim != kD) return HIF8_ERR_SHAPE;
+    const int64_t q_tiles = (n_q + kBM - 1) / kBM;
+    if (n_q >= (int64_t(1) << 30) || n_kv >= (int64_t(1) << 30) || batch * heads * q_tiles >= (int64_t(1) << 31))
+        return HIF8_ERR_SHAPE;
+    for (int i = 0; i < 4; ++i) {
+        if (row_strides[i] < heads * kD || row_strides[i] % 8 != 0 || batch_strides[i] < 0 || batch_strides[i] % 8 != 0)
+            return HIF8_ERR_SHAPE;
+    }
+    // key offsets are 32-bit inside the buffer of one (batch, head)
+    if ((n_kv - 1) * row_strides[1] * 2 + kD * 2 >= (int64_t(1) << 31) ||
+        (n_kv - 1) * row_strides[2] * 2 + kD * 2 >= (int64_t(1) << 31))
+        return HIF8_ERR_SHAPE;
+    if (((uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)out) & 15u) return HIF8_ERR_ALIGN;
+    if (((uintptr_t)key_idx | (uintptr_t)key_count) & 3u) return HIF8_ERR_ALIGN;
+
+    Params p;
+    p.q = q;
+    p.k = k;
+    p.v = v;
+    p.out = out;
+    p.q_rs = row_strides[0];
+    p.k_rs = row_strides[1];
+    p.v_rs = row_strides[2];
+    p.o_rs = row_strides[3];
+    p.q_bs = batch_strides[0];
+    p.k_bs = batch_strides[1];
+    p.v_bs = batch_strides[2];
+    p.o_bs = batch_strides[3];
+    p.key_idx = key_idx;
+    p.key_count = key_count;
+    p.idx_bs = idx_batch_stride;
+    p.n_q = int(n_q);
+    p.n_kv = int(n_kv);
+    p.heads = int(heads);
+    p.q_tiles = int(q_tiles);
+    p.c = float(double(softmax_scale) * 1.4426950408889634);
+    p.o_st = (State *)out_state;
+    p.o_shift = out_state_dtype == kBF16F32 ? 16u : 0u;
+    hipStream_t s = (hipStream_t)stream;
+    hipLaunchKernelGGL(k_attn_fwd, dim3(unsigned(batch * heads * q_tiles)), dim3(kThreads), 0, s, p);
+    if (out_state)
+        hipLaunchKernelGGL(k_attn_amax_settle, dim3(1), dim3(256), 0, s, (State *)out_state,
+                           out_state_dtype == kBF16F32 ? kF32 : kBF16, scale_max);
+    return hipGetLastError() == hipSuccess ? HIF8_OK : HIF8_ERR_HIP;
+}
+
+}  // namespace hif8

@@ -55,6 +55,20 @@ __device__ __forceinline__ void fill_luts(State *st, float s, uint32_t c)
     st->lut_bf16[c] = uint16_t(f2bf(y));
 }
 
+// Thread 0: amax a (magnitude bits) -> amax, scale, flags of st; returns the scale.
+__device__ __forceinline__ float write_amax_state(State *st, uint32_t a, int dtype, float smax)
+{
+    bool fast;
+    const float s = scale_from_amax(a, dtype, smax, fast);
+    st->amax_bits = a;
+    st->scale = s;
+    st->fast = fast ? 1u : 0u;
+    st->finite = fast ? 1u : 0u;   // amax finite => every element finite
+    st->dtype = uint32_t(dtype);
+    st->pending = 0u;
+    return s;
+}
+
 // Fold one workgroup's amax (magnitude bits; NaN above every finite value) into st;
 // the last of `nwg` workgroups resets the accumulators and writes amax, scale, flags
 // and the tables.  Called by all 256 threads of the workgroup with `m` already reduced
@@ -73,18 +87,25 @@ __device__ __forceinline__ void fold_amax(State *st, uint32_t m, uint32_t nwg, i
     if (tid == 0) {
         const uint32_t a = __hip_atomic_exchange(&st->amax_acc, 0u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
         __hip_atomic_store(&st->counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        bool fast;
-        const float s = scale_from_amax(a, dtype, smax, fast);
-        st->amax_bits = a;
-        st->scale = s;
-        st->fast = fast ? 1u : 0u;
-        st->finite = fast ? 1u : 0u;   // amax finite => every element finite
-        st->dtype = uint32_t(dtype);
-        st->pending = 0u;
-        lds[1] = f2u(s);
+        lds[1] = f2u(write_amax_state(st, a, dtype, smax));
     }
     __syncthreads();
     fill_luts(st, u2f(lds[1]), tid);
+}
+
+// Settle st after a kernel that folded the amax of its output into st->amax_acc with relaxed
+// atomics (one workgroup of 256 threads, launched after it on the same stream): reset the
+// accumulator and write amax, scale, flags and tables as an amax pass over that output would.
+__device__ __forceinline__ void settle_amax(State *st, int dtype, float smax, uint32_t *lds)
+{
+    const uint32_t tid = threadIdx.x;
+    if (tid == 0) {
+        const uint32_t a = st->amax_acc;
+        st->amax_acc = 0u;
+        lds[0] = f2u(write_amax_state(st, a, dtype, smax));
+    }
+    __syncthreads();
+    fill_luts(st, u2f(lds[0]), tid);
 }
 
 }  // namespace hif8

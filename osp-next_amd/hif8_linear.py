@@ -646,6 +646,22 @@ class HIF8Linear(nn.Linear):
         y = linear_any(a, a_fmt, a_st, self._packed_weight(), self.bias)
         return y.view(*x.shape[:-1], y.shape[-1])
 
+    def forward_settled(self, x: Tensor, x_state: QuantState, as_f32: bool = False) -> Tensor:
+        """``forward(x)`` (``as_f32``: ``forward(x.float())``) for a bf16 x whose amax, scale and
+        tables ``x_state`` already holds for this layer's ``scale_max_forward``, left there by the
+        kernel that wrote x (the attention's epilogue): the quantisation pass and the GEMM, no
+        amax pass.  Inference only."""
+        if torch.is_grad_enabled() and (x.requires_grad or self.weight.requires_grad
+                                        or (self.bias is not None and self.bias.requires_grad)):
+            raise RuntimeError("forward_settled has no autograd; call forward(x)")
+        if x.dtype != torch.bfloat16:
+            raise TypeError(f"forward_settled takes a bfloat16 tensor, got {x.dtype}")
+        K = x.shape[-1]
+        x2 = x.reshape(-1, K).contiguous()
+        a = fake_quant_to_bf16(x2, x_state, as_f32=True) if as_f32 else fake_quant(x2, x_state)
+        y = linear_any(a, _lib.A_BF16, x_state, self._packed_weight(), self.bias)
+        return y.view(*x.shape[:-1], y.shape[-1])
+
     def extra_repr(self) -> str:
         return (f"in_features={self.in_features}, out_features={self.out_features}, "
                 f"bias={self.bias is not None}, "

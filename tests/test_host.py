@@ -101,6 +101,23 @@ def test_status_codes_without_gpu(pkg):
     assert L.hif8_linear_fwd_wq_split(fake, fake, None, fake, 128, 256, 100, None, 0, None) == -2
     assert L.hif8_linear_fwd_wq_split(fake, fake, None, odd, 128, 256, 512, None, 0, None) == -3
     assert L.hif8_linear_split_workspace_bytes(0, 256, 512) == 0
+    # attention: pointers, sizes, head dim 128, strides, the 32-bit key offsets, the state's dtype,
+    # alignment (all checked before any device call)
+    def att(q=fake, out=fake, B=2, nq=300, nkv=200, H=4, D=128, rs=(512,) * 4, bs=(512 * 300,) * 4,
+            idx=None, idx_bs=0, cnt=None, scale=0.088, st=None, st_dt=2, smax=15.0):
+        return L.hif8_attention_fwd(q, fake, fake, out, B, nq, nkv, H, D, (I64 * 4)(*rs), (I64 * 4)(*bs), idx, idx_bs,
+                                    cnt, scale, st, st_dt, smax, None)
+    assert att(q=None) == -1
+    assert att(nkv=0) == -1
+    assert att(scale=0.0) == -1
+    assert att(idx=fake) == -1                          # a key list needs its counts
+    assert att(st=fake, st_dt=1) == -1                  # the o state: bf16 or bf16-as-fp32 rules
+    assert att(D=64) == -2
+    assert att(rs=(256, 512, 512, 512)) == -2           # row stride below heads * 128
+    assert att(rs=(516, 512, 512, 512)) == -2           # row stride not a multiple of 8
+    assert att(nkv=(1 << 20) + 1, rs=(512, 1024, 512, 512)) == -2   # 2 GB of key rows: 32-bit offsets
+    assert att(out=odd) == -3
+    assert att(idx=fake + 2, idx_bs=200, cnt=fake) == -3
     # modulated LayerNorm: dim % 8, dim <= 8192, alignment of x and of the row statistics
     assert L.hif8_modln_amax(None, None, None, 4, 5120, 4, 1e-6, fake, 15.0, fake, None) == -1
     assert L.hif8_modln_amax(fake, None, None, 0, 5120, 4, 1e-6, fake, 15.0, fake, None) == -1
