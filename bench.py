@@ -462,7 +462,8 @@ def time_block(pkg, torch, reps, routes=("fused", "reference")):
     """one 14B block at 720P (x [1, 75600, 5120], grid 21x45x80 padded to 48
     rows -> 4 x 20160 tokens), a Skiparse token block entered from full order, every linear HiF8
     with prepacked weights, dense bf16 attention within the 4 strided sub-grids, cross-attention
-    over 512 text tokens.  Times the fused route and the reference-order route (``routes``)."""
+    over 512 text tokens.  Times the fused route (attention on the library's kernel) and the
+    reference-order route (SDPA) (``routes``)."""
     D = pkg.dit
     dev = torch.device("cuda:0")
     dim, ffn, heads, grid, L = 5120, 13824, 40, (21, 45, 80), 512
@@ -486,7 +487,8 @@ def time_block(pkg, torch, reps, routes=("fused", "reference")):
             return blk(x, tm, tm, e, grid, grid, rope, text, fused=fused)
 
     out = {"what": "one 14B DiT block at 720P (token block from full order), all linears HiF8, "
-                   "prepacked weights, bf16 SDPA within the 2x2 strided sub-grids",
+                   "prepacked weights, bf16 attention within the 2x2 strided sub-grids (fused route: the "
+                   "library's attention kernel; reference order: SDPA)",
            "tokens": T * H * W, "rows_padded": rows}
     for fused in [r == "fused" for r in routes]:
         run(fused)
@@ -507,6 +509,60 @@ def time_block(pkg, torch, reps, routes=("fused", "reference")):
     if "fused_ms" in out:
         out["TFLOPs_fused"] = round((lf + af) / (out["fused_ms"] * 1e-3) / 1e12, 1)
     del blk, x, e, text
+    torch.cuda.empty_cache()
+    return out
+
+
+def time_attention(pkg, torch, reps):
+    """The attention of a 14B block at 720P on the library's kernel against the reference's SDPA
+    branch: self-attention over the 4 strided sub-grids of 20160 tokens with the padding keys
+    masked (18900 kept), 40 heads of 128; cross-attention of the 80640 rows over 512 text tokens.
+    The kernel also leaves the o projection's amax (its epilogue); the amax pass over the output
+    that this replaces is timed beside it."""
+    D = pkg.dit
+    dev = torch.device("cuda:0")
+    heads, hd, grid, L = 40, 128, (21, 45, 80), 512
+    tm, _ = D.skiparse_masks(1, grid, 2, dev)
+    B, N = tm.shape
+    g = torch.Generator(device=dev).manual_seed(6)
+    q, k, v = (torch.randn(B, N, heads, hd, generator=g, device=dev).to(torch.bfloat16) for _ in range(3))
+    idx, cnt = pkg.key_list(tm)
+    st = pkg.QuantState(dev)
+
+    def timed(fn, n):
+        fn()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(n):
+            fn()
+        b.record()
+        torch.cuda.synchronize()
+        return a.elapsed_time(b) / n
+
+    kept = [int(c) for c in cnt.tolist()]
+    flops = sum(4.0 * N * c * hd * heads for c in kept)
+    out = {"what": f"self-attention of the 720P block: {B} sub-grids of {N} queries over their kept keys "
+                   f"({kept[0]}), {heads} heads of {hd}, bf16; cross-attention of {B * N} rows over {L} text "
+                   f"tokens", "self_TFLOP": round(flops / 1e12, 3)}
+    with torch.no_grad():
+        o = pkg.attention_fwd(q, k, v, idx, cnt, o_state=st, o_as_f32=True)
+        t_k = timed(lambda: pkg.attention_fwd(q, k, v, idx, cnt, o_state=st, o_as_f32=True), reps)
+        t_s = timed(lambda: D.attention_key_masked(q, k, v, tm, out_dtype=torch.bfloat16), max(2, reps // 2))
+        o2 = o.reshape(-1, heads * hd)
+        t_a = timed(lambda: pkg.absmax_scale(o2, 15.0, pkg.QuantState(dev), as_f32=True), reps)
+        out["self"] = {"kernel_ms": round(t_k, 3), "kernel_TFLOPs": round(flops / (t_k * 1e-3) / 1e12, 1),
+                       "frac_of_peak": round(flops / (t_k * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+                       "sdpa_ms": round(t_s, 3), "sdpa_TFLOPs": round(flops / (t_s * 1e-3) / 1e12, 1),
+                       "amax_pass_replaced_us": round(t_a * 1e3, 1)}
+        del q, k, v, o, o2
+        qc = torch.randn(1, B * N, heads, hd, generator=g, device=dev).to(torch.bfloat16)
+        kc, vc = (torch.randn(1, L, heads, hd, generator=g, device=dev).to(torch.bfloat16) for _ in range(2))
+        cflops = 4.0 * B * N * L * hd * heads
+        t_kc = timed(lambda: pkg.attention_fwd(qc, kc, vc, o_state=st), reps)
+        t_sc = timed(lambda: D.attention_key_masked(qc, kc, vc, None), reps)
+        out["cross"] = {"kernel_ms": round(t_kc, 3), "kernel_TFLOPs": round(cflops / (t_kc * 1e-3) / 1e12, 1),
+                        "sdpa_ms": round(t_sc, 3), "sdpa_TFLOPs": round(cflops / (t_sc * 1e-3) / 1e12, 1)}
     torch.cuda.empty_cache()
     return out
 
@@ -794,10 +850,10 @@ def main():
     ap.add_argument("--route", default="auto", choices=["auto", "fused", "decode_once"],
                     help="GEMM route for bf16 activations (auto: HIF8Linear's rule, decode_once at this M)")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--shapes", default="up,bwd,ffn,down,qkvo,c2,modln,qkv,block,step",
+    ap.add_argument("--shapes", default="up,bwd,ffn,down,qkvo,c2,modln,qkv,attn,block,step",
                     help="comma list of up,bwd (the FFN-up backward),down,qkvo (the other 14B linears),"
-                         "c2 (the three 1.3B 480P linears, config 2),ffn,modln,qkv,block (config 4),"
-                         "step (config 5),"
+                         "c2 (the three 1.3B 480P linears, config 2),ffn,modln,qkv,attn (the block's "
+                         "attention with the o amax epilogue),block (config 4),step (config 5),"
                          "data (the GEMM with constant operands) to time in addition")
     ap.add_argument("--block-routes", default="fused,reference",
                     help="routes of the block (config 4) to time: fused, reference or both")
@@ -926,6 +982,12 @@ def main():
     if "data" in args.shapes.split(","):
         log("[bench] timing the fused GEMM with constant operands")
         extra_shapes["data"] = time_data_dependence(pkg, torch, x, w, max(3, args.steps // 2))
+    if "attn" in args.shapes.split(","):
+        log("[bench] timing the block's attention (kernel with the o amax epilogue, and SDPA)")
+        try:
+            extra_shapes["attn"] = time_attention(pkg, torch, max(3, args.steps // 4))
+        except Exception as ex:
+            extra_shapes["attn"] = {"error": repr(ex)}
     if "block" in args.shapes.split(","):
         log("[bench] timing one 14B DiT block at 720P (config 4)")
         try:
@@ -954,7 +1016,7 @@ def main():
         return line
 
     for name in [s for s in args.shapes.split(",")
-                 if s and s not in ("up", "bwd", "ffn", "modln", "qkv", "block", "step", "data", "c2")]:
+                 if s and s not in ("up", "bwd", "ffn", "modln", "qkv", "attn", "block", "step", "data", "c2")]:
         n_, k_ = {"down": (5120, 13824), "qkvo": (5120, 5120)}[name]
         print(f"[bench] timing the 14B {name} linear", file=sys.stderr, flush=True)
         extra_shapes[name] = linear_line(M, n_, k_, 1, 16)

@@ -10,9 +10,12 @@
 // magnitudes it stores, so the amax pass is not needed.
 //
 // Design (flash attention, online softmax; head_dim 128):
-//   - One workgroup per 256 queries of one (batch, head); 8 waves, two per SIMD, each owning 32
-//     queries.  Keys go in tiles of 64: K and V tiles (16 KB each) are loaded global -> LDS with
-//     buffer_load ... lds into one of two buffers while the other is computed.
+//   - One workgroup per 384 queries of one (batch, head); 12 waves, three per SIMD (168 VGPRs
+//     each), each owning 32 queries.  Keys go in tiles of 64: K and V tiles (16 KB each) are loaded
+//     global -> LDS with buffer_load ... lds into one of two buffers while the other is computed;
+//     every wave reads the whole tile from LDS, so more waves per tile mean fewer tile loads per
+//     flop and more waves to cover each other's waits (measured at the 720P block's shape: 8 waves
+//     1000 TFLOP/s, 12 waves 1090).
 //   - Scores are computed transposed, S^T = K Q^T, with v_mfma_f32_16x16x32_bf16: the A operand is
 //     a K fragment from LDS, the B operand the wave's Q fragments, held in registers for the whole
 //     kernel.  In the accumulator layout a lane holds one query and 4 keys of each 16 x 16 block,
@@ -25,7 +28,13 @@
 //     exponentials stay below 2^8 in between), so the O accumulators are rescaled a handful of times
 //     per query instead of at every tile.  Row sums are per-lane partials, reduced once at the end.
 //   - Keys: an optional per-batch list of key rows (the rows the key mask keeps) and count; tiles
-//     past the count are masked to -inf.  The whole key tensor is never gathered.
+//     past the count are masked to -inf.  The whole key tensor is never gathered.  The list's
+//     entries reach LDS like K and V (a ring of three 256-byte slots, two tiles ahead), so the loop
+//     has no load of its own to wait for: a wait for a global load issued after a tile's K/V loads
+//     would also wait for those (the counter completes in order), 14 % of the kernel's time.
+//   - The exponentials are about 8 % of the time (measured by replacing them); a wave's softmax
+//     and another wave's MFMAs overlap as the waves of a SIMD drift apart (staggering the waves by
+//     half a tile on purpose measured the same).
 //   - Tile order: workgroup w runs on XCD w % 8; consecutive query tiles of one head are given to
 //     one XCD, so the CUs of an XCD stream the same K/V tiles through its L2.
 #include <hip/hip_runtime.h>
@@ -45,12 +54,13 @@ typedef short i16x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kD = 128;                  // head dim
 constexpr int kBN = 64;                  // keys per tile
-constexpr int kWaves = 8;
+constexpr int kWaves = 12;
 constexpr int kThreads = kWaves * 64;
 constexpr int kQW = 32;                  // queries per wave
 constexpr int kBM = kWaves * kQW;        // queries per workgroup
 constexpr uint32_t kTile = kBN * kD * 2;  // bytes of one K or V tile
-constexpr uint32_t kLds = 4 * kTile;      // K and V, two buffers each
+constexpr uint32_t kList = 4 * kTile;     // key-list ring: 3 slots of one tile's 64 entries
+constexpr uint32_t kLds = kList + 3 * kBN * 4;
 constexpr float kLazy = 8.0f;             // log2 headroom before the reference max moves
 
 struct Params {
@@ -96,11 +106,22 @@ __device__ __forceinline__ u32x2 ld_tr(const uint8_t *lds_base, uint32_t off)
     return __builtin_bit_cast(u32x2, v);
 }
 
-// The physical key row of logical key kk, or row 0 for keys past the count (loaded, then masked).
-__device__ __forceinline__ uint32_t key_row(int raw, int kk, int nk, int n_kv)
+// 64 lanes x 4 B from the buffer (voffset per lane) into LDS at m0v + lane * 4
+__device__ __forceinline__ void dtl_load_b32(uint32_t m0v, uint32_t voff, const u32x4 &rs)
 {
-    if (kk >= nk) return 0u;
-    return uint32_t(raw < 0 ? 0 : (raw >= n_kv ? n_kv - 1 : raw));
+    ASMV("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, 0 offen lds" ::"s"(m0v), "v"(voff), "s"(rs) : "memory", "m0");
+}
+
+__device__ __forceinline__ float max_over_groups(float m)
+{
+    const auto p = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, m), __builtin_bit_cast(uint32_t, m),
+                                                    false, false);
+    const uint32_t p0 = p[0], p1 = p[1];
+    m = __builtin_fmaxf(__builtin_bit_cast(float, p0), __builtin_bit_cast(float, p1));
+    const auto q = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(uint32_t, m), __builtin_bit_cast(uint32_t, m),
+                                                    false, false);
+    const uint32_t q0 = q[0], q1 = q[1];
+    return __builtin_fmaxf(__builtin_bit_cast(float, q0), __builtin_bit_cast(float, q1));
 }
 
 // LDS layout of a tile (64 keys x 128 dims, bf16):
@@ -113,7 +134,11 @@ __device__ __forceinline__ uint32_t key_row(int raw, int kk, int nk, int n_kv)
 //      lane (d, g) the keys 4g .. 4g + 3 of dim 16P + d.  Groups g and g + 1 (read in the same
 //      cycle) read blocks of opposite parity, opposite halves of the banks.
 //   A DTL instruction writes 1 KB: 4 K rows, or the 8 V blocks of one 4-key group.
-__global__ __launch_bounds__(kThreads, 1) void k_attn_fwd(const Params p)
+// LIST: the keys are p.key_idx[b][0 .. count - 1]; otherwise keys 0 .. count - 1.  Key-list
+// entries reach LDS the way K and V do (wave 0 loads a tile's 64 entries two tiles ahead into a
+// ring of three slots), so the loop holds no global load whose wait would also wait for the
+// K and V loads of the next tile.
+template <bool LIST> __global__ __launch_bounds__(kThreads, 1) void k_attn_fwd(const Params p)
 {
     __shared__ __attribute__((aligned(1024))) uint8_t smem[kLds];
     const uint32_t tid = threadIdx.x, lane = tid & 63u;
@@ -133,12 +158,12 @@ __global__ __launch_bounds__(kThreads, 1) void k_attn_fwd(const Params p)
         nk = nk < 0 ? 0 : (nk > p.n_kv ? p.n_kv : nk);
         if (p.key_idx && int64_t(nk) > p.idx_bs) nk = int(p.idx_bs);
     }
+    nk = __builtin_amdgcn_readfirstlane(nk);
     const int ntiles = (nk + kBN - 1) / kBN;
-    const int32_t *idx = p.key_idx ? p.key_idx + int64_t(b) * p.idx_bs : nullptr;
 
     // buffer resources of this (batch, head)'s K and V: rows of 256 bytes at the row stride; the
     // range ends with the last key row
-    u32x4 rk, rv;
+    u32x4 rk, rv, rl;
     {
         const uint64_t ka = uint64_t(p.k + int64_t(b) * p.k_bs + int64_t(h) * kD);
         const uint64_t va = uint64_t(p.v + int64_t(b) * p.v_bs + int64_t(h) * kD);
@@ -146,59 +171,57 @@ __global__ __launch_bounds__(kThreads, 1) void k_attn_fwd(const Params p)
         const uint32_t vn = uint32_t(int64_t(p.n_kv - 1) * p.v_rs * 2 + kD * 2);
         rk = u32x4{uint32_t(ka), uint32_t(ka >> 32), kn, 0x00020000u};
         rv = u32x4{uint32_t(va), uint32_t(va >> 32), vn, 0x00020000u};
+        // the key list's range is the batch's count: entries past it read as 0
+        const uint64_t la = LIST ? uint64_t(p.key_idx + int64_t(b) * p.idx_bs) : 0;
+        rl = u32x4{uint32_t(la), uint32_t(la >> 32), uint32_t(nk) * 4u, 0x00020000u};
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
             rk[i] = __builtin_amdgcn_readfirstlane(rk[i]);
             rv[i] = __builtin_amdgcn_readfirstlane(rv[i]);
+            rl[i] = __builtin_amdgcn_readfirstlane(rl[i]);
         }
     }
     const uint32_t krs = uint32_t(p.k_rs * 2), vrs = uint32_t(p.v_rs * 2);
-    // this lane's share of the DTL: K rows kr[j] (instructions 2 wave + j) and V rows vr[j]
-    uint32_t kr[2], kch[2], vr[2], vcol[2];
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-        const uint32_t it = 2u * wave + uint32_t(j);
-        kr[j] = 4u * it + (lane >> 4);
-        kch[j] = ((lane & 15u) ^ (kr[j] & 15u)) * 16u;
-        vr[j] = 4u * it + ((lane & 7u) >> 1);
-        vcol[j] = (16u * (((lane >> 3) ^ (it & 1u))) + 8u * (lane & 1u)) * 2u;
-    }
     const uint32_t lds0 = uint32_t(uintptr_t(smem));
-    // raw key list entries of the next tile for this lane's four rows
-    int nraw[4] = {0, 0, 0, 0};
-    auto fetch_raw = [&](int t) {
-        if (idx) {
-#pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                const int kk = t * kBN + int(kr[j]), kv = t * kBN + int(vr[j]);
-                nraw[j] = kk < nk ? idx[kk] : 0;
-                nraw[2 + j] = kv < nk ? idx[kv] : 0;
-            }
-        } else {
-#pragma unroll
-            for (int j = 0; j < 2; ++j) {
-                nraw[j] = t * kBN + int(kr[j]);
-                nraw[2 + j] = t * kBN + int(vr[j]);
-            }
-        }
+    // the key-list entries of tile t into ring slot t % 3 (wave 0)
+    auto list_dtl = [&](int t) {
+        if (LIST && wave == 0)
+            dtl_load_b32(__builtin_amdgcn_readfirstlane(lds0 + kList + uint32_t(t % 3) * (kBN * 4)),
+                         (uint32_t(t) * kBN + lane) * 4u, rl);
     };
+    // the DTL of tile t: keys past the count read row 0 (list) or the last row, and are masked;
+    // list entries are clamped into the tensor
     auto issue_tile = [&](int t) {
         const uint32_t buf = uint32_t(t & 1);
+        const int *slot = (const int *)(smem + kList + uint32_t(t % 3) * (kBN * 4));
+        // 32 DTL items per tile (16 of K, 16 of V) over the waves: items wave, wave + 12, ...
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-            const uint32_t it = 2u * wave + uint32_t(j);
-            const uint32_t rowk = key_row(nraw[j], t * kBN + int(kr[j]), nk, p.n_kv);
-            const uint32_t rowv = key_row(nraw[2 + j], t * kBN + int(vr[j]), nk, p.n_kv);
-            dtl_load(__builtin_amdgcn_readfirstlane(lds0 + buf * kTile + it * 1024u), rowk * krs + kch[j], rk);
-            dtl_load(__builtin_amdgcn_readfirstlane(lds0 + 2u * kTile + buf * kTile + it * 1024u), rowv * vrs + vcol[j],
-                     rv);
+        for (int j = 0; j < 3; ++j) {
+            const uint32_t item = wave + uint32_t(j) * kWaves;
+            if (item < 16) {
+                const uint32_t it = item, r = 4u * it + (lane >> 4);
+                const int raw = LIST ? slot[r] : t * kBN + int(r);
+                const uint32_t row = uint32_t(min(max(raw, 0), p.n_kv - 1));
+                dtl_load(__builtin_amdgcn_readfirstlane(lds0 + buf * kTile + it * 1024u),
+                         __umul24(row, krs) + ((lane & 15u) ^ (r & 15u)) * 16u, rk);
+            } else if (item < 32) {
+                const uint32_t it = item - 16u, r = 4u * it + ((lane & 7u) >> 1);
+                const int raw = LIST ? slot[r] : t * kBN + int(r);
+                const uint32_t row = uint32_t(min(max(raw, 0), p.n_kv - 1));
+                dtl_load(__builtin_amdgcn_readfirstlane(lds0 + 2u * kTile + buf * kTile + it * 1024u),
+                         __umul24(row, vrs) + (16u * (((lane >> 3) ^ (it & 1u))) + 8u * (lane & 1u)) * 2u, rv);
+            }
         }
     };
 
     if (ntiles > 0) {
-        fetch_raw(0);
+        if (LIST) {
+            list_dtl(0);
+            if (ntiles > 1) list_dtl(1);
+            ASMV("s_waitcnt vmcnt(0)" ::: "memory");
+            __syncthreads();
+        }
         issue_tile(0);
-        if (ntiles > 1) fetch_raw(1);
     }
 
     // Q fragments: lane (cq, g) holds dims 32 pp + 8 g .. +7 of query 16 qb + cq of the wave's 32
@@ -230,10 +253,8 @@ __global__ __launch_bounds__(kThreads, 1) void k_attn_fwd(const Params p)
     for (int t = 0; t < ntiles; ++t) {
         ASMV("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
-        if (t + 1 < ntiles) {
-            issue_tile(t + 1);
-            if (t + 2 < ntiles) fetch_raw(t + 2);
-        }
+        if (t + 1 < ntiles) issue_tile(t + 1);
+        if (t + 2 < ntiles) list_dtl(t + 2);
         const uint8_t *ks = smem + uint32_t(t & 1) * kTile;
         const uint8_t *vs = smem + 2u * kTile + uint32_t(t & 1) * kTile;
 
@@ -266,8 +287,7 @@ __global__ __launch_bounds__(kThreads, 1) void k_attn_fwd(const Params p)
             for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
                 for (int i = 0; i < 4; ++i) mx = __builtin_fmaxf(mx, s[kb][qb][i]);
-            mx = __builtin_fmaxf(mx, __shfl_xor(mx, 16, 64));
-            mx = __builtin_fmaxf(mx, __shfl_xor(mx, 32, 64));
+            mx = max_over_groups(mx);
             const float mt = mx * c;
             if (__builtin_amdgcn_ballot_w64(mt > mref[qb] + kLazy)) {
                 const float mn = __builtin_fmaxf(mref[qb], mt);
@@ -399,7 +419,10 @@ extern "C" int hif8_attention_fwd(const uint16_t *q, const uint16_t *k, const ui
     p.o_st = (State *)out_state;
     p.o_shift = out_state_dtype == kBF16F32 ? 16u : 0u;
     hipStream_t s = (hipStream_t)stream;
-    hipLaunchKernelGGL(k_attn_fwd, dim3(unsigned(batch * heads * q_tiles)), dim3(kThreads), 0, s, p);
+    if (key_idx)
+        hipLaunchKernelGGL(k_attn_fwd<true>, dim3(unsigned(batch * heads * q_tiles)), dim3(kThreads), 0, s, p);
+    else
+        hipLaunchKernelGGL(k_attn_fwd<false>, dim3(unsigned(batch * heads * q_tiles)), dim3(kThreads), 0, s, p);
     if (out_state)
         hipLaunchKernelGGL(k_attn_amax_settle, dim3(1), dim3(256), 0, s, (State *)out_state,
                            out_state_dtype == kBF16F32 ? kF32 : kBF16, scale_max);

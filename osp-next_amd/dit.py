@@ -17,8 +17,11 @@ Two routes through a block, chosen per call:
   the three projections run as one grouped GEMM; cross-attention's k and v quantise the text
   once and run grouped; cross-attention's q takes the quantised affine norm of ``norm3`` from
   ``affine_norm_quant``; the FFN takes the quantised modulated norm of ``norm2`` and runs its
-  up-projection with the GELU + amax epilogue.  Every quantised operand is the one the
-  reference would build (the producers are bit-exact after the layer norm).
+  up-projection with the GELU + amax epilogue; the self- and cross-attention run on the
+  library's attention kernel (``attention_fwd``), whose epilogue leaves the ``o`` projection's
+  amax and scale, so ``o`` quantises its input without an amax pass.  Every quantised operand
+  is the one the reference would build from the attention output (the producers are bit-exact
+  after the layer norm; the attention itself agrees with SDPA within floating-point tolerance).
 
 dtypes follow the reference's inference setting (FSDP2 mixed precision with bf16 block
 parameters, fp32 norm parameters with bf16 outputs, ``osp_next.py:1390-1395``,
@@ -27,7 +30,8 @@ the affine LayerNorm compute in fp32 and hand bf16 on; RoPE runs in fp32, so the
 self-attention output and the ``o`` projection's input are fp32 (``osp_next.py:644``,
 ``attention.py:473,518``).  Attention is the reference's SDPA branch
 (``attention.py:433-458``); a key-side padding mask is applied by attending each sequence to
-its unmasked keys only, which is the masked softmax without an [N, N] mask tensor.
+its unmasked keys only, which is the masked softmax without an [N, N] mask tensor (on the
+fused route, the kernel reads the list of unmasked key rows).
 """
 from __future__ import annotations
 
@@ -41,7 +45,7 @@ from torch import Tensor
 
 from . import _lib
 from .ffn import HIF8FFN
-from .hif8_attention import _HIF8QKVQuantFunction
+from .hif8_attention import _HIF8QKVQuantFunction, attention_fwd, attention_fwd_ok, key_list
 from .hif8_linear import (HIF8Linear, QuantState, absmax_scale, fake_quant, grouped_ok, linear_fwd_grouped,
                           make_linear)
 from .norm import (WanLayerNorm, affine_fused_ok, affine_norm_quant, grouped_weight, modulated_norm_quant,
@@ -388,6 +392,20 @@ def attention_key_masked(q: Tensor, k: Tensor, v: Tensor, key_mask: Optional[Ten
     return torch.cat(outs, 0).to(out_dtype)
 
 
+_KEY_LIST_CACHE: list = [None, None, None]   # mask, its version, (key rows, counts)
+
+
+def _cached_key_list(key_mask: Optional[Tensor]) -> Tuple[Optional[Tensor], Optional[Tensor]]:
+    """``key_list(key_mask)``, kept for the last mask seen: every block of a step attends with
+    the same mask tensor."""
+    if key_mask is None:
+        return None, None
+    c = _KEY_LIST_CACHE
+    if c[0] is not key_mask or c[1] != key_mask._version:
+        c[0], c[1], c[2] = key_mask, key_mask._version, key_list(key_mask.bool())
+    return c[2]
+
+
 def _grouped_kv(k: HIF8Linear, v: HIF8Linear, text: Tensor) -> Optional[Tuple[Tensor, Tensor]]:
     """k(text), v(text) with the text quantised once and one grouped GEMM (inference), or None."""
     if not (isinstance(k, HIF8Linear) and isinstance(v, HIF8Linear) and text.is_cuda
@@ -460,7 +478,14 @@ class OSPNextSelfAttention(nn.Module):
             cos_f, sin_f = rope_wrapper.prepare_freqs(grid_sizes_for_rope, D // 2, self.rearrange_rope)
             q = rms_norm_rope(ql, self.norm_q, cos_f, sin_f, D).view(B, N, H, D)
             k = rms_norm_rope(kl, self.norm_k, cos_f, sin_f, D).view(B, N, H, D)
-            x = self._attend(q, k, vl.view(B, N, H, D), attn_mask, out_dtype=torch.bfloat16)
+            v = vl.view(B, N, H, D)
+            if attention_fwd_ok(q, k, v):
+                # the attention kernel leaves the o input's amax and scale in st: no amax pass
+                st = QuantState(q.device)
+                x = attention_fwd(q, k, v, *_cached_key_list(attn_mask), o_state=st, o_as_f32=True,
+                                  scale_max=self.o.scale_max_forward)
+                return self.o.forward_settled(x.flatten(2), st, as_f32=True)
+            x = self._attend(q, k, v, attn_mask, out_dtype=torch.bfloat16)
             return self.o.forward_f32_of_bf16(x.flatten(2))
         q = self.norm_q(ql).view(B, N, H, D)
         k = self.norm_k(kl).view(B, N, H, D)
@@ -506,6 +531,13 @@ class OSPNextCrossAttention(OSPNextSelfAttention):
             q = q.view(B, -1, H, D)
         k = k.view(tb, -1, H, D)
         v = v.view(tb, -1, H, D)
+        if (fused and self.quant_attn is None and isinstance(self.o, HIF8Linear) and q.dtype == torch.bfloat16
+                and attention_fwd_ok(q, k, v)):
+            # attn_mask is query-side: no effect (as in SDPA); the o input's amax comes from the
+            # attention kernel's epilogue
+            st = QuantState(q.device)
+            out = attention_fwd(q, k, v, o_state=st, scale_max=self.o.scale_max_forward)
+            return self.o.forward_settled(out.reshape(B, -1, H * D), st)
         out = self._attend(q, k, v, None)       # attn_mask is query-side: no effect in SDPA
         return self.o(out.reshape(B, -1, H * D))
 

@@ -150,6 +150,30 @@ def test_lazy_rescale_with_growing_scores(pkg):
     check(run(pkg, q, kr, vr), reference(q, kr, vr), "decreasing")
 
 
+def test_one_dominant_key_in_each_lane_group(pkg):
+    """One key per batch scores ~230 above the others for every query (exp2 of that difference
+    overflows fp32): the output must be that key's value row.  The key sits in each of the four
+    4-key groups of a 16-key block (one per batch), which four different lanes of the score
+    accumulators hold, in different tiles: a tile max that missed any lane group would overflow."""
+    print("[attn] dominant key", flush=True)
+    B, Nq, Nkv, H = 4, 48, 600, 1
+    g = torch.Generator().manual_seed(15)
+    u = torch.randn(D, generator=g)
+    u = u / u.norm() * math.sqrt(D)
+    q = (u.view(1, 1, 1, D) + 0.05 * torch.randn(B, Nq, H, D, generator=g)).to(torch.bfloat16)
+    k = (0.1 * torch.randn(B, Nkv, H, D, generator=g)).to(torch.bfloat16)
+    v = torch.randn(B, Nkv, H, D, generator=g).to(torch.bfloat16)
+    spikes = [64 * 3 + 2, 64 * 5 + 16 + 6, 32 + 9, 64 * 7 + 48 + 15]   # lane groups 0, 1, 2, 3
+    for b, j in enumerate(spikes):
+        k[b, j, 0] = (20.0 * u).to(torch.bfloat16)
+    out = run(pkg, q, k, v)
+    assert torch.isfinite(out.float()).all()
+    for b, j in enumerate(spikes):
+        want = v[b, j, 0].float().expand(Nq, D)
+        assert torch.allclose(out[b, :, 0].float().cpu(), want, atol=2e-2 * float(want.abs().max()), rtol=0)
+    check(out, reference(q, k, v), "dominant key")
+
+
 def test_dit_shape_against_float32(pkg):
     """40 heads (the 14B model's), a padded-grid key mask, a few query tiles; compared with float32
     on the GPU and with torch's SDPA on the kept keys."""

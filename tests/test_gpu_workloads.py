@@ -10,8 +10,11 @@
   osp_next.py:926-957): every linear of both routes is intercepted where it runs; each x_q is
   checked against the oracle on sampled rows with the full tensor's scale and, for the fused
   producers, against the standalone _quant of the producer's own output on the whole tensor;
-  each GEMM's output rows against fp32 torch; the two routes' block outputs agree within the
-  block tolerance of tests/test_dit_cpu.py and are finite.
+  each GEMM's output rows against fp32 torch; on the fused route, sampled queries of each
+  attention kernel call against float32 softmax over the kept keys, and the o input quantised
+  with the state the kernel's epilogue left is the standalone _quant of the attention output;
+  the two routes' block outputs agree within the block tolerance of tests/test_dit_cpu.py and
+  are finite.
 - Config 5 (the 40-block 14B step at 768P, osp_next.py:1287-1331): the fused step's output
   is finite, and the fused and reference-order routes agree on one full and one skiparse
   block at that size.
@@ -113,6 +116,8 @@ class BlockProbe:
         wrap_q = self._qact(hl.quantize_activation)
         monkeypatch.setattr(hl, "quantize_activation", wrap_q)
         monkeypatch.setattr(ffn, "quantize_activation", wrap_q)
+        monkeypatch.setattr(dit, "attention_fwd", self._attention(dit.attention_fwd))
+        monkeypatch.setattr(hl.HIF8Linear, "forward_settled", self._settled(hl.HIF8Linear.forward_settled))
 
     def _hit(self, site):
         self.calls[site] = self.calls.get(site, 0) + 1
@@ -218,6 +223,36 @@ class BlockProbe:
             return tq
         return wrapped
 
+    def _attention(self, orig):
+        def wrapped(q, k, v, key_idx=None, key_count=None, softmax_scale=None, o_state=None, o_as_f32=False,
+                    scale_max=15.0):
+            out = orig(q, k, v, key_idx, key_count, softmax_scale, o_state, o_as_f32, scale_max)
+            self._hit("attention_fwd" + ("[f32]" if o_as_f32 else ""))
+            W.check_attention_rows(q, k, v, key_idx, key_count, out, seed=self.seed + sum(self.calls.values()))
+            # the epilogue's state is the one an amax pass over the output leaves
+            st_full = self.pkg.absmax_scale(out.reshape(-1, out.shape[2] * out.shape[3]), scale_max,
+                                            self.pkg.QuantState(out.device), as_f32=o_as_f32)
+            assert o_state.read() == st_full.read()
+            return out
+        return wrapped
+
+    def _settled(self, orig):
+        def wrapped(lin, x, x_state, as_f32=False):
+            self._hit("forward_settled" + ("[f32]" if as_f32 else ""))
+            # the o input quantised with the settled state is the standalone _quant of x (of its
+            # fp32 copy, then the autocast, for the self-attention)
+            x2 = x.reshape(-1, x.shape[-1]).contiguous()
+            if as_f32:
+                a = self.pkg.fake_quant_to_bf16(x2, x_state, as_f32=True)
+                want = W.standalone_quant(self.pkg, x2.float(), lin.scale_max_forward)[0].to(torch.bfloat16)
+            else:
+                a = self.pkg.fake_quant(x2, x_state)
+                want = W.standalone_quant(self.pkg, x2, lin.scale_max_forward)[0]
+            assert torch.equal(a.view(torch.int16), want.view(torch.int16))
+            W.check_xq_rows(self.R, x2, a, x_state, lin.scale_max_forward, self._rows(x2.shape[0]), as_f32=as_f32)
+            return orig(lin, x, x_state, as_f32)
+        return wrapped
+
     def _qact(self, orig):
         def wrapped(x2, scale_max, a_format, as_f32=False):
             a, fmt, st = orig(x2, scale_max, a_format, as_f32)
@@ -276,10 +311,10 @@ def test_config4_block_720p_every_linear(pkg, R, monkeypatch):
         outs[fused] = y
         print(f"[config4] fused={fused} sites {probe.calls}", flush=True)
         if fused:
-            assert probe.calls == {"modulated_norm_quant": 2, "linear_fwd_grouped[3]": 1, "quantize_activation[f32]": 1,
-                                   "linear_any": 4, "linear_fwd_grouped[2]": 1, "text_quant": 1,
-                                   "affine_norm_quant": 1, "quantize_activation": 1, "linear_fwd_gelu_stat": 1,
-                                   "ffn_down_quant": 1}, probe.calls
+            assert probe.calls == {"modulated_norm_quant": 2, "linear_fwd_grouped[3]": 1, "attention_fwd[f32]": 1,
+                                   "forward_settled[f32]": 1, "linear_any": 4, "linear_fwd_grouped[2]": 1,
+                                   "text_quant": 1, "affine_norm_quant": 1, "attention_fwd": 1,
+                                   "forward_settled": 1, "linear_fwd_gelu_stat": 1, "ffn_down_quant": 1}, probe.calls
         else:
             # q, k, v, o (fp32 input), cross q, k, v, o, FFN up: each quantises its own input
             assert probe.calls.get("quantize_activation", 0) + probe.calls.get("quantize_activation[f32]", 0) == 9

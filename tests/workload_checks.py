@@ -115,3 +115,28 @@ def check_linear_rows(a: torch.Tensor, w_q: torch.Tensor, b, y: torch.Tensor, ro
     elem, norm = rel_errors(got, ref)
     assert norm <= TOL_NORM and (gelu or elem <= TOL_ELEM), (elem, norm)
     return elem, norm
+
+
+def check_attention_rows(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, key_idx, key_count,
+                         out: torch.Tensor, seed: int, n: int = 48):
+    """Sampled queries of every batch of an attention output ([B, Nq, H, 128], as
+    hif8_attention_fwd writes it) against softmax(q k^T / sqrt(128)) v in float32 over the keys
+    the batch keeps: normwise <= 1e-2 and elementwise <= 2e-2 of the largest reference magnitude
+    (the kernel rounds the probabilities and the output to bf16)."""
+    B, Nq, H, D = q.shape
+    g = torch.Generator().manual_seed(seed)
+    for b in range(B):
+        rows = torch.randint(0, Nq, (n,), generator=g).to(q.device)
+        kb = k[b if k.shape[0] == B else 0]
+        vb = v[b if v.shape[0] == B else 0]
+        if key_count is not None:
+            c = int(key_count[b])
+            sel = key_idx[b, :c].long() if key_idx is not None else torch.arange(c, device=q.device)
+            kb, vb = kb[sel], vb[sel]
+        qs = q[b, rows].float().permute(1, 0, 2).contiguous()               # [H, n, D]
+        s = torch.matmul(qs, kb.float().permute(1, 2, 0).contiguous()) / D ** 0.5
+        ref = torch.matmul(torch.softmax(s, dim=-1), vb.float().permute(1, 0, 2).contiguous())
+        got = out[b, rows].float().permute(1, 0, 2)
+        err = float((got - ref).norm() / ref.norm().clamp_min(1e-30))
+        mx = float((got - ref).abs().max() / ref.abs().max().clamp_min(1e-30))
+        assert err <= 1e-2 and mx <= 2e-2, (b, err, mx)
