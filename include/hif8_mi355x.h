@@ -369,7 +369,8 @@ int hif8_ln_affine_fake_quant(const uint16_t *x, const float *weight, const floa
  * are bf16 [batch][tokens][heads][head_dim] with token row strides row_strides[0..3] and batch
  * strides batch_strides[0..3] (elements, in the order q, k, v, out; a batch stride may be 0,
  * e.g. keys shared by every batch).  head_dim must be 128; strides multiples of 8, at least
- * heads * 128; (n_kv - 1) * row stride * 2 + 256 below 2^31 for k and v; 16-byte aligned tensors.
+ * heads * 128; for k and v, (n_kv - 1) * row stride * 2 + 256 below 2^31 and the row stride below
+ * 2^23 elements; 16-byte aligned tensors.
  * key_idx NULL and key_count NULL: every key 0 .. n_kv - 1.  key_count [batch] alone: the first
  * key_count[b] keys.  key_idx [batch][idx_batch_stride] with key_count: the key rows
  * key_idx[b][0 .. key_count[b] - 1] (entries clamped to [0, n_kv)).  A query with no key gets

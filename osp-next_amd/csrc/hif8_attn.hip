@@ -388,9 +388,11 @@ extern "C" int hif8_attention_fwd(const uint16_t *q, const uint16_t *k, const ui
         if (row_strides[i] < heads * kD || row_strides[i] % 8 != 0 || batch_strides[i] < 0 || batch_strides[i] % 8 != 0)
             return HIF8_ERR_SHAPE;
     }
-    // key offsets are 32-bit inside the buffer of one (batch, head)
+    // key offsets are 32-bit inside the buffer of one (batch, head), formed as a 24 x 24-bit
+    // product of the key row and the row stride in bytes
     if ((n_kv - 1) * row_strides[1] * 2 + kD * 2 >= (int64_t(1) << 31) ||
-        (n_kv - 1) * row_strides[2] * 2 + kD * 2 >= (int64_t(1) << 31))
+        (n_kv - 1) * row_strides[2] * 2 + kD * 2 >= (int64_t(1) << 31) ||
+        row_strides[1] * 2 >= (int64_t(1) << 24) || row_strides[2] * 2 >= (int64_t(1) << 24))
         return HIF8_ERR_SHAPE;
     if (((uintptr_t)q | (uintptr_t)k | (uintptr_t)v | (uintptr_t)out) & 15u) return HIF8_ERR_ALIGN;
     if (((uintptr_t)key_idx | (uintptr_t)key_count) & 3u) return HIF8_ERR_ALIGN;

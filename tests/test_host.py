@@ -116,6 +116,7 @@ def test_status_codes_without_gpu(pkg):
     assert att(rs=(256, 512, 512, 512)) == -2           # row stride below heads * 128
     assert att(rs=(516, 512, 512, 512)) == -2           # row stride not a multiple of 8
     assert att(nkv=(1 << 20) + 1, rs=(512, 1024, 512, 512)) == -2   # 2 GB of key rows: 32-bit offsets
+    assert att(nkv=2, rs=(512, 1 << 23, 512, 512)) == -2      # key row stride of 16 MB: 24-bit products
     assert att(out=odd) == -3
     assert att(idx=fake + 2, idx_bs=200, cnt=fake) == -3
     # modulated LayerNorm: dim % 8, dim <= 8192, alignment of x and of the row statistics
