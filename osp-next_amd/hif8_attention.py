@@ -122,7 +122,10 @@ def attention_fwd(q: Tensor, k: Tensor, v: Tensor, key_idx: Optional[Tensor] = N
     key_idx[b, :key_count[b]], as ``key_list`` gives them).  ``softmax_scale`` defaults to
     1/sqrt(128), SDPA's.  With ``o_state``, the amax of out is left in it with the scale rule
     for ``scale_max`` (as fp32 values with ``o_as_f32``, the self-attention's o input), as
-    ``absmax_scale(out, scale_max, o_state, o_as_f32)`` would leave it."""
+    ``absmax_scale(out, scale_max, o_state, o_as_f32)`` would leave it.  Inference only (no
+    backward)."""
+    if torch.is_grad_enabled() and (q.requires_grad or k.requires_grad or v.requires_grad):
+        raise RuntimeError("attention_fwd has no backward; use attention_with_mask under autograd")
     if not attention_fwd_ok(q, k, v):
         raise ValueError("attention_fwd takes bf16 GPU tensors [B, N, H, 128] with heads contiguous per token")
     if key_idx is not None and key_count is None:

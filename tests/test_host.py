@@ -146,6 +146,15 @@ def test_python_layer_refuses_cpu_tensors(pkg):
     with pytest.raises(ValueError):
         pkg.quant_dequant_float(x, pkg.QType("hif8"))
     assert pkg.quant_dequant_float(x, pkg.QType("bf16")) is x
+    # the attention kernel: GPU bf16 [B, N, H, 128] only, and no autograd
+    q = torch.zeros(1, 4, 1, 128, dtype=torch.bfloat16)
+    assert not pkg.attention_fwd_ok(q, q, q)
+    with pytest.raises(ValueError):
+        pkg.attention_fwd(q, q, q)
+    with pytest.raises(RuntimeError):
+        pkg.attention_fwd(q.clone().requires_grad_(True), q, q)
+    with pytest.raises(ValueError):
+        pkg.key_list(torch.ones(2, 3))          # not a bool mask
 
 
 @pytest.fixture(scope="module")
