@@ -46,8 +46,8 @@ from torch import Tensor
 from . import _lib
 from .ffn import HIF8FFN
 from .hif8_attention import _HIF8QKVQuantFunction, attention_fwd, attention_fwd_ok, key_list
-from .hif8_linear import (HIF8Linear, QuantState, absmax_scale, fake_quant, grouped_ok, linear_fwd_grouped,
-                          make_linear)
+from .hif8_linear import (HIF8Linear, QuantState, absmax_scale, fake_quant, fake_quant_to_bf16, grouped_ok,
+                          linear_fwd_grouped, make_linear)
 from .norm import (WanLayerNorm, affine_fused_ok, affine_norm_quant, grouped_weight, modulated_norm_quant,
                    qkv_from_modulated_norm)
 
@@ -461,6 +461,29 @@ class OSPNextSelfAttention(nn.Module):
             q, k, v = _HIF8QKVQuantFunction.apply(q, k, v, self.scale_max_forward, self.scale_max_backward)
         return attention_key_masked(q, k, v, key_mask, out_dtype=out_dtype)
 
+    def _kernel_quant_attn_ok(self, q: Tensor) -> bool:
+        """quant_attn="hif8" can run on the attention kernel: inference on the GPU, head dim 128,
+        an HIF8Linear o."""
+        return (self.quant_attn == "hif8" and q.is_cuda and not torch.is_grad_enabled()
+                and q.shape[-1] == 128 and isinstance(self.o, HIF8Linear))
+
+    def _quantised_attention(self, q: Tensor, k: Tensor, v: Tensor, key_mask: Optional[Tensor],
+                             o_as_f32: bool) -> Tuple[Tensor, QuantState]:
+        """quant_attn="hif8" on the attention kernel: the kernel's inputs are bf16(_quant(q)),
+        bf16(_quant(k)) and _quant(v) -- the HiF8 qdq of each with its own per-tensor scale
+        (hif8_attention.py:60-74), then the attention's bf16 cast (attention.py:460-518) -- and
+        the o projection's state comes from its epilogue.  Returns (out bf16, o state)."""
+        def quantised(t: Tensor) -> Tensor:
+            t2 = t.reshape(-1, t.shape[-1]).contiguous()
+            st = absmax_scale(t2, self.scale_max_forward, QuantState(t.device))
+            tq = fake_quant_to_bf16(t2, st) if t.dtype == torch.float32 else fake_quant(t2, st)
+            return tq.view(t.shape)
+        qq, kq, vq = quantised(q), quantised(k), quantised(v)
+        st = QuantState(q.device)
+        out = attention_fwd(qq, kq, vq, *_cached_key_list(key_mask), o_state=st, o_as_f32=o_as_f32,
+                            scale_max=self.o.scale_max_forward)
+        return out, st
+
     def forward(self, x: Optional[Tensor], attn_mask: Optional[Tensor], grid_sizes_for_rope,
                 rope_wrapper: SkiparseRopeWrapper, qkv: Optional[Sequence[Tensor]] = None) -> Tensor:
         """``qkv`` = the three projections of x computed by the caller (the fused route, which
@@ -494,6 +517,9 @@ class OSPNextSelfAttention(nn.Module):
         k = rope_wrapper.apply_rope(k, grid_sizes_for_rope, self.rearrange_rope)
         if qkv_given and isinstance(self.o, HIF8Linear) and q.dtype == torch.float32:
             # the attention output is bf16 values returned as fp32: quantise them as such
+            if self._kernel_quant_attn_ok(q) and k.dtype == torch.float32 and v.dtype == torch.bfloat16:
+                x, st = self._quantised_attention(q, k, v, attn_mask, o_as_f32=True)
+                return self.o.forward_settled(x.flatten(2), st, as_f32=True)
             x = self._attend(q, k, v, attn_mask, out_dtype=torch.bfloat16)
             return self.o.forward_f32_of_bf16(x.flatten(2))
         x = self._attend(q, k, v, attn_mask)
@@ -537,6 +563,9 @@ class OSPNextCrossAttention(OSPNextSelfAttention):
             # attention kernel's epilogue
             st = QuantState(q.device)
             out = attention_fwd(q, k, v, o_state=st, scale_max=self.o.scale_max_forward)
+            return self.o.forward_settled(out.reshape(B, -1, H * D), st)
+        if fused and self._kernel_quant_attn_ok(q) and q.dtype == k.dtype == v.dtype == torch.bfloat16:
+            out, st = self._quantised_attention(q, k, v, None, o_as_f32=False)
             return self.o.forward_settled(out.reshape(B, -1, H * D), st)
         out = self._attend(q, k, v, None)       # attn_mask is query-side: no effect in SDPA
         return self.o(out.reshape(B, -1, H * D))

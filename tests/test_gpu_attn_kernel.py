@@ -235,3 +235,28 @@ def test_o_projection_settled_equals_forward(pkg):
             got = lin.forward_settled(out, st, as_f32=as_f32)
             want = lin(out.float()) if as_f32 else lin(out)
             assert torch.equal(got.view(torch.int16), want.view(torch.int16)), f"as_f32={as_f32}"
+
+
+@pytest.mark.parametrize("o_as_f32", [True, False])
+def test_quant_attn_route_equals_hif8_qkv_quant(pkg, o_as_f32):
+    """quant_attn="hif8" on the attention kernel (the block's inference route): its inputs are the
+    bf16 casts of _HIF8QKVQuantFunction's outputs (hif8_attention.py:60-74, the per-tensor _quant
+    of q and k in fp32 for the self-attention, of v in bf16), so its output equals the kernel run
+    on those tensors bit for bit, and the o state equals an amax pass over the output."""
+    print(f"[attn] quant_attn route o_as_f32={o_as_f32}", flush=True)
+    B, N, H = 2, 300, 2
+    att = pkg.dit.OSPNextSelfAttention(H * D, H, quant="hif8", quant_attn="hif8", device=DEV, dtype=torch.bfloat16)
+    g = torch.Generator().manual_seed(16)
+    dt = torch.float32 if o_as_f32 else torch.bfloat16
+    q = (torch.randn(B, N, H, D, generator=g) * 2).to(dt).to(DEV)
+    k = torch.randn(B, N, H, D, generator=g).to(dt).to(DEV)
+    v = torch.randn(B, N, H, D, generator=g).to(torch.bfloat16).to(DEV)
+    mask = (torch.rand(B, N, generator=g) < 0.8).to(DEV)
+    with torch.no_grad():
+        out, st = att._quantised_attention(q, k, v, mask, o_as_f32=o_as_f32)
+        qq, kq, vq = pkg._HIF8QKVQuantFunction.apply(q, k, v, 15.0, 224.0)
+        idx, cnt = pkg.key_list(mask)
+        want = pkg.attention_fwd(qq.to(torch.bfloat16), kq.to(torch.bfloat16), vq, idx, cnt)
+        full = pkg.absmax_scale(out.reshape(-1, H * D), 15.0, pkg.QuantState(DEV), as_f32=o_as_f32)
+    assert torch.equal(out.view(torch.int16), want.view(torch.int16))
+    assert st.read() == full.read()
