@@ -112,6 +112,10 @@ __device__ __forceinline__ void dtl_load_b32(uint32_t m0v, uint32_t voff, const 
     ASMV("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, 0 offen lds" ::"s"(m0v), "v"(voff), "s"(rs) : "memory", "m0");
 }
 
+// max over the 4 lanes holding the same query (lanes l, l ^ 16, l ^ 32, l ^ 48): permlane32_swap
+// of (m, m) gives lane l the pair m[l % 32], m[l % 32 + 32]; permlane16_swap the pair of rows 2k,
+// 2k + 1 at lane l % 16.  The elements are copied out before the casts: a bit cast of a vector
+// element reads element 0.
 __device__ __forceinline__ float max_over_groups(float m)
 {
     const auto p = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, m), __builtin_bit_cast(uint32_t, m),
