@@ -461,11 +461,15 @@ class OSPNextSelfAttention(nn.Module):
             q, k, v = _HIF8QKVQuantFunction.apply(q, k, v, self.scale_max_forward, self.scale_max_backward)
         return attention_key_masked(q, k, v, key_mask, out_dtype=out_dtype)
 
+    def _kernel_ok(self, q: Tensor) -> bool:
+        """The attention can run on the attention kernel: inference on the GPU, head dim 128, an
+        HIF8Linear o (which takes the state the kernel's epilogue leaves)."""
+        return (q.is_cuda and not torch.is_grad_enabled() and q.shape[-1] == 128
+                and isinstance(self.o, HIF8Linear))
+
     def _kernel_quant_attn_ok(self, q: Tensor) -> bool:
-        """quant_attn="hif8" can run on the attention kernel: inference on the GPU, head dim 128,
-        an HIF8Linear o."""
-        return (self.quant_attn == "hif8" and q.is_cuda and not torch.is_grad_enabled()
-                and q.shape[-1] == 128 and isinstance(self.o, HIF8Linear))
+        """quant_attn="hif8" on the attention kernel."""
+        return self.quant_attn == "hif8" and self._kernel_ok(q)
 
     def _quantised_attention(self, q: Tensor, k: Tensor, v: Tensor, key_mask: Optional[Tensor],
                              o_as_f32: bool) -> Tuple[Tensor, QuantState]:
@@ -520,6 +524,14 @@ class OSPNextSelfAttention(nn.Module):
             if self._kernel_quant_attn_ok(q) and k.dtype == torch.float32 and v.dtype == torch.bfloat16:
                 x, st = self._quantised_attention(q, k, v, attn_mask, o_as_f32=True)
                 return self.o.forward_settled(x.flatten(2), st, as_f32=True)
+            if self.quant_attn is None and self._kernel_ok(q) and v.dtype == torch.bfloat16:
+                # the attention's bf16 cast of q and k (attention.py:460-518), then the kernel
+                q16, k16 = q.to(torch.bfloat16), k.to(torch.bfloat16)
+                if attention_fwd_ok(q16, k16, v):
+                    st = QuantState(q.device)
+                    x = attention_fwd(q16, k16, v, *_cached_key_list(attn_mask), o_state=st, o_as_f32=True,
+                                      scale_max=self.o.scale_max_forward)
+                    return self.o.forward_settled(x.flatten(2), st, as_f32=True)
             x = self._attend(q, k, v, attn_mask, out_dtype=torch.bfloat16)
             return self.o.forward_f32_of_bf16(x.flatten(2))
         x = self._attend(q, k, v, attn_mask)

@@ -101,3 +101,27 @@ def test_static_producer_replays(pkg):
         ref = ref.clone()
         graph, out = capture(lambda: pkg.modulated_norm_quant_static(x, shift, scale, 1e-6, 15.0))
         replay_and_check(graph, out, ref, lambda: pkg.modulated_norm_quant_static(x[:1000] * 2, shift, scale, 1e-6, 15.0))
+
+
+def test_dit_block_fused_route_replays(pkg):
+    """A whole DiT block on its inference route -- producers, grouped GEMMs, q/k norm + rope, the
+    attention kernel with a key padding mask and the o amax in its epilogue, the FFN's GELU route,
+    residual updates -- captured once and replayed bit-identically, with eager calls on other
+    data in between (grid 2x5x8: H padded to 6 for the 2x2 sub-grids, so the mask has padding)."""
+    print("[graph] DiT block, fused route", flush=True)
+    from ospnext_amd import dit as D
+    from test_dit_cpu import block_inputs, make_block
+    blk = make_block(D, "token", True, False, quant="hif8", device=DEV)
+    for m in blk.modules():
+        if isinstance(m, pkg.HIF8Linear):
+            m.prepack()
+    grid = (2, 5, 8)
+    x, e, text = (t.to(DEV) for t in block_inputs(grid))
+    x2 = (x * -1.5).contiguous()
+    rope = D.SkiparseRopeWrapper(D.rope_freqs(128).to(DEV))
+    tm, _ = D.skiparse_masks(1, grid, 2, DEV)
+    assert tm is not None and not bool(tm.all())
+    with torch.no_grad():
+        ref = blk(x, tm, tm, e, grid, grid, rope, text, fused=True).clone()
+        graph, out = capture(lambda: blk(x, tm, tm, e, grid, grid, rope, text, fused=True))
+        replay_and_check(graph, out, ref, lambda: blk(x2, tm, tm, e, grid, grid, rope, text, fused=True))
