@@ -392,18 +392,20 @@ def attention_key_masked(q: Tensor, k: Tensor, v: Tensor, key_mask: Optional[Ten
     return torch.cat(outs, 0).to(out_dtype)
 
 
-_KEY_LIST_CACHE: list = [None, None, None]   # mask, its version, (key rows, counts)
+_KEY_LIST_CACHE: list = [None]   # (mask, its version, (key rows, counts)), replaced as one tuple
 
 
 def _cached_key_list(key_mask: Optional[Tensor]) -> Tuple[Optional[Tensor], Optional[Tensor]]:
     """``key_list(key_mask)``, kept for the last mask seen: every block of a step attends with
-    the same mask tensor."""
+    the same mask tensor.  The entry is one tuple, swapped whole, so concurrent callers never
+    pair one mask with another's list."""
     if key_mask is None:
         return None, None
-    c = _KEY_LIST_CACHE
-    if c[0] is not key_mask or c[1] != key_mask._version:
-        c[0], c[1], c[2] = key_mask, key_mask._version, key_list(key_mask.bool())
-    return c[2]
+    hit = _KEY_LIST_CACHE[0]
+    if hit is None or hit[0] is not key_mask or hit[1] != key_mask._version:
+        hit = (key_mask, key_mask._version, key_list(key_mask.bool()))
+        _KEY_LIST_CACHE[0] = hit
+    return hit[2]
 
 
 def _grouped_kv(k: HIF8Linear, v: HIF8Linear, text: Tensor) -> Optional[Tuple[Tensor, Tensor]]:
