@@ -458,19 +458,20 @@ def _linear_flops(rows, dim, ffn, L):
     return 2.0 * rows * dim * dim * 6 + 2.0 * L * dim * dim * 2 + 2.0 * rows * dim * ffn * 2
 
 
-def time_block(pkg, torch, reps, routes=("fused", "reference")):
+def time_block(pkg, torch, reps, routes=("fused", "reference"), quant_attn=None):
     """one 14B block at 720P (x [1, 75600, 5120], grid 21x45x80 padded to 48
     rows -> 4 x 20160 tokens), a Skiparse token block entered from full order, every linear HiF8
     with prepacked weights, dense bf16 attention within the 4 strided sub-grids, cross-attention
     over 512 text tokens.  Times the fused route (attention on the library's kernel) and the
-    reference-order route (SDPA) (``routes``)."""
+    reference-order route (SDPA) (``routes``).  ``quant_attn="hif8"``: Q/K/V quantised before
+    the attention, as the reference's 14B HiF8 inference config sets it."""
     D = pkg.dit
     dev = torch.device("cuda:0")
     dim, ffn, heads, grid, L = 5120, 13824, 40, (21, 45, 80), 512
     torch.manual_seed(4)
     blk = D.OSPNextAttentionBlock(dim, ffn, heads, cross_attn_norm=True, sparse_ratio=2,
                                   skiparse_block_type="token", is_full2skiparse_block=True, quant="hif8",
-                                  device=dev)
+                                  quant_attn=quant_attn, device=dev)
     g = torch.Generator(device=dev).manual_seed(4)
     D.init_block_weights(blk, 0.02, g)
     for m in blk.modules():
@@ -853,7 +854,8 @@ def main():
     ap.add_argument("--shapes", default="up,bwd,ffn,down,qkvo,c2,modln,qkv,attn,block,step",
                     help="comma list of up,bwd (the FFN-up backward),down,qkvo (the other 14B linears),"
                          "c2 (the three 1.3B 480P linears, config 2),ffn,modln,qkv,attn (the block's "
-                         "attention with the o amax epilogue),block (config 4),step (config 5),"
+                         "attention with the o amax epilogue),block (config 4),block_qa (config 4 with "
+                         "quant_attn=hif8),step (config 5),"
                          "data (the GEMM with constant operands) to time in addition")
     ap.add_argument("--block-routes", default="fused,reference",
                     help="routes of the block (config 4) to time: fused, reference or both")
@@ -994,6 +996,12 @@ def main():
             extra_shapes["block"] = time_block(pkg, torch, 3, tuple(args.block_routes.split(",")))
         except Exception as ex:  # the harness around the path (attention backend) may be missing
             extra_shapes["block"] = {"error": repr(ex)}
+    if "block_qa" in args.shapes.split(","):
+        log("[bench] timing one 14B DiT block at 720P with quant_attn=hif8")
+        try:
+            extra_shapes["block_qa"] = time_block(pkg, torch, 3, ("fused",), quant_attn="hif8")
+        except Exception as ex:
+            extra_shapes["block_qa"] = {"error": repr(ex)}
     if "step" in args.shapes.split(","):
         log("[bench] timing the 40-block denoising step at 768P (config 5)")
         try:
@@ -1016,7 +1024,8 @@ def main():
         return line
 
     for name in [s for s in args.shapes.split(",")
-                 if s and s not in ("up", "bwd", "ffn", "modln", "qkv", "attn", "block", "step", "data", "c2")]:
+                 if s and s not in ("up", "bwd", "ffn", "modln", "qkv", "attn", "block", "block_qa", "step", "data",
+                                    "c2")]:
         n_, k_ = {"down": (5120, 13824), "qkvo": (5120, 5120)}[name]
         print(f"[bench] timing the 14B {name} linear", file=sys.stderr, flush=True)
         extra_shapes[name] = linear_line(M, n_, k_, 1, 16)

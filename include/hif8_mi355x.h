@@ -239,6 +239,22 @@ int hif8_linear_fwd_wq_grouped(const uint16_t *a, const uint16_t *w_q, const uin
 int hif8_rms_norm_rope(const uint16_t *x, const float *weight, const float *cos_t, const float *sin_t, uint16_t *out,
                        int64_t rows, int64_t dim, int64_t head_dim, int64_t seq, int64_t rep, float eps,
                        hif8_stream_t stream);
+/* The same pass as producers of quant_attn="hif8" (hif8_attention.py:60-74): the reference
+ * hands hif8_attention_with_mask the fp32 rope output of q and k (the norm's bf16 output when
+ * there is no rope, the cross-attention's q) and quantises each with _quant before the
+ * attention's bf16 cast.
+ * hif8_rms_norm_rope_amax folds the amax of that output (fp32 with cos_t/sin_t, bf16 without)
+ * into state with the scale rule for scale_max (fp32 rule with rope, bf16 rule without); the last
+ * workgroup settles the state.  hif8_rms_norm_rope_fake_quant writes x_q, bf16 [rows, dim]: the
+ * bf16 value of the output's fake quant with the state's scale (semantics HIF8_SEM_NPU or
+ * HIF8_SEM_TORCH), and y, when not NULL, the output itself (fp32 [rows, dim] with rope, bf16
+ * without; 16-byte aligned).  Shapes, tables and alignment as for hif8_rms_norm_rope. */
+int hif8_rms_norm_rope_amax(const uint16_t *x, const float *weight, const float *cos_t, const float *sin_t,
+                            int64_t rows, int64_t dim, int64_t head_dim, int64_t seq, int64_t rep, float eps,
+                            float scale_max, void *state, hif8_stream_t stream);
+int hif8_rms_norm_rope_fake_quant(const uint16_t *x, const float *weight, const float *cos_t, const float *sin_t,
+                                  int64_t rows, int64_t dim, int64_t head_dim, int64_t seq, int64_t rep, float eps,
+                                  const void *state, int semantics, uint16_t *x_q, void *y, hif8_stream_t stream);
 
 /* ---------------------------------------------------------------------------
  * Backward support.  The reference's dgrad is grad_q @ w_q (hif8_linear.py:97), a

@@ -57,6 +57,8 @@ SIGNATURES = {
     "hif8_linear_fwd_wq_gelu_stat": (_i, [_p, _p, _p, _p, _i64, _i64, _i64, _f, _p, _p]),
     "hif8_linear_fwd_wq_grouped": (_i, [_p, _p, _p, ctypes.POINTER(_p), ctypes.POINTER(_i64), _i, _i64, _i64, _p]),
     "hif8_rms_norm_rope": (_i, [_p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _f, _p]),
+    "hif8_rms_norm_rope_amax": (_i, [_p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _f, _f, _p, _p]),
+    "hif8_rms_norm_rope_fake_quant": (_i, [_p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _f, _p, _i, _p, _p, _p]),
     "hif8_attention_fwd": (_i, [_p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, ctypes.POINTER(_i64),
                                 ctypes.POINTER(_i64), _p, _i64, _p, _f, _p, _i, _f, _p]),
 }

@@ -22,6 +22,7 @@
 #include <stdint.h>
 
 #include "hif8_internal.h"
+#include "hif8_qdq_dev.h"
 
 namespace hif8 {
 namespace dit {
@@ -43,13 +44,23 @@ __device__ __forceinline__ uint32_t bf(float f)
 }
 __device__ __forceinline__ uint32_t pack(float a, float b) { return bf(a) | (bf(b) << 16); }
 
-template <int NC, bool ROPE>
+// MODE 0: out = the bf16 output.  MODE 1: no output; the amax of the output before that rounding
+// -- the fp32 rope output, or without rope the bf16 norm output -- folded into st with the scale
+// rule for smax (fp32 with rope, bf16 without), the last workgroup settling st: the _quant amax of
+// the q or k the reference hands hif8_attention_with_mask (hif8_attention.py:60-74).  MODE 2:
+// out = bf16 of that output's HiF8 fake quant with st's scale (the attention's bf16 cast of
+// _quant(q)), and y_out, if not null, the output itself (fp32 with rope, bf16 without).
+template <int NC, bool ROPE, int MODE>
 __global__ __launch_bounds__(kThreads) void k_rms_norm_rope(const uint16_t *__restrict__ x, const float *__restrict__ w,
                                                             const float *__restrict__ cs, const float *__restrict__ sn,
                                                             uint16_t *__restrict__ out, int64_t rows, int dim,
-                                                            int head_dim, int64_t seq, int64_t rep, float eps)
+                                                            int head_dim, int64_t seq, int64_t rep, float eps,
+                                                            State *__restrict__ st, float smax, int sem,
+                                                            void *__restrict__ y_out)
 {
     const int lane = threadIdx.x & 63;
+    uint32_t amax = 0;
+    const float qs = MODE == 2 ? st->scale : 0.0f;
     const int64_t wstride = int64_t(gridDim.x) * (kThreads / 64);
     const float inv_dim = 1.0f / float(dim);
     for (int64_t row = int64_t(blockIdx.x) * (kThreads / 64) + (threadIdx.x >> 6); row < rows; row += wstride) {
@@ -97,20 +108,68 @@ __global__ __launch_bounds__(kThreads) void k_rms_norm_rope(const uint16_t *__re
                 const float y1 = __builtin_bit_cast(float, bf(y[e] * r) << 16);
                 y[e] = __builtin_bit_cast(float, bf(y1 * wv[e]) << 16);
             }
-            u32x4 o;
+            float f[8];
             if (ROPE) {
 #pragma unroll
                 for (int t = 0; t < 4; ++t) {
                     const float x1 = y[2 * t], x2 = y[2 * t + 1];
                     const float p1 = x1 * ca[t], p2 = x2 * sa[t], p3 = x1 * sa[t], p4 = x2 * ca[t];
-                    o[t] = pack(p1 - p2, p3 + p4);
+                    f[2 * t] = p1 - p2;
+                    f[2 * t + 1] = p3 + p4;
                 }
             } else {
 #pragma unroll
-                for (int t = 0; t < 4; ++t) o[t] = pack(y[2 * t], y[2 * t + 1]);
+                for (int e = 0; e < 8; ++e) f[e] = y[e];   // bf16 values
             }
-            orow[c * 64 + lane] = o;
+            if (MODE == 0) {
+                u32x4 o;
+#pragma unroll
+                for (int t = 0; t < 4; ++t) o[t] = pack(f[2 * t], f[2 * t + 1]);
+                orow[c * 64 + lane] = o;
+            } else if (MODE == 1) {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    const uint32_t mb = ROPE ? (__builtin_bit_cast(uint32_t, f[e]) & 0x7FFFFFFFu) : (bf(f[e]) & 0x7FFFu);
+                    amax = mb > amax ? mb : amax;
+                }
+            } else {
+                uint32_t qb[8];
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    uint32_t yb, code;
+                    if (ROPE) {
+                        slow_elem<kF32>(__builtin_bit_cast(uint32_t, f[e]), qs, sem, yb, code);
+                        qb[e] = f2bf(u2f(yb));
+                    } else {
+                        slow_elem<kBF16>(bf(f[e]), qs, sem, yb, code);
+                        qb[e] = yb;
+                    }
+                }
+                orow[c * 64 + lane] = u32x4{qb[0] | (qb[1] << 16), qb[2] | (qb[3] << 16), qb[4] | (qb[5] << 16),
+                                            qb[6] | (qb[7] << 16)};
+                if (y_out) {
+                    if (ROPE) {
+                        f32x4 *yr = (f32x4 *)((float *)y_out + row * dim + c * 512 + lane * 8);
+                        yr[0] = f32x4{f[0], f[1], f[2], f[3]};
+                        yr[1] = f32x4{f[4], f[5], f[6], f[7]};
+                    } else {
+                        u32x4 o;
+#pragma unroll
+                        for (int t = 0; t < 4; ++t) o[t] = pack(f[2 * t], f[2 * t + 1]);
+                        ((u32x4 *)((uint16_t *)y_out + row * dim))[c * 64 + lane] = o;
+                    }
+                }
+            }
         }
+    }
+    if (MODE == 1) {
+#pragma unroll
+        for (int o = 32; o > 0; o >>= 1) amax = max(amax, (uint32_t)__shfl_xor((int)amax, o, 64));
+        __shared__ uint32_t red[kThreads / 64 + 2];
+        if (lane == 0) red[threadIdx.x >> 6] = amax;
+        __syncthreads();
+        amax = max(max(red[0], red[1]), max(red[2], red[3]));
+        fold_amax(st, amax, gridDim.x, ROPE ? kF32 : kBF16, smax, red + kThreads / 64);
     }
 }
 
@@ -162,18 +221,24 @@ __global__ __launch_bounds__(kThreads) void k_gated_residual(const u32x4 *x, con
 
 using namespace hif8;
 
-extern "C" int hif8_rms_norm_rope(const uint16_t *x, const float *weight, const float *cos_t, const float *sin_t,
-                                  uint16_t *out, int64_t rows, int64_t dim, int64_t head_dim, int64_t seq,
-                                  int64_t rep, float eps, hif8_stream_t stream)
+namespace {
+
+// Checks and launches k_rms_norm_rope<., ., MODE> (see hif8_rms_norm_rope and its quantising forms).
+int launch_rms_norm_rope(int mode, const uint16_t *x, const float *weight, const float *cos_t, const float *sin_t,
+                         uint16_t *out, int64_t rows, int64_t dim, int64_t head_dim, int64_t seq, int64_t rep,
+                         float eps, State *st, float smax, int sem, void *y_out, hif8_stream_t stream)
 {
-    if (!x || !weight || !out || rows <= 0) return HIF8_ERR_ARG;
+    if (!x || !weight || rows <= 0) return HIF8_ERR_ARG;
+    if ((mode != 1 && !out) || (mode != 0 && !st)) return HIF8_ERR_ARG;
+    if (mode == 1 && !(smax > 0.0f)) return HIF8_ERR_ARG;
+    if (mode == 2 && sem != kSemNpu && sem != kSemTorch) return HIF8_ERR_ARG;
     if ((cos_t == nullptr) != (sin_t == nullptr)) return HIF8_ERR_ARG;
     if (dim <= 0 || dim % 512 != 0 || dim > 512 * dit::kMaxChunks) return HIF8_ERR_SHAPE;
     const bool rope = cos_t != nullptr;
     if (rope && (head_dim < 8 || head_dim % 8 != 0 || 512 % head_dim != 0 || dim % head_dim != 0 || seq <= 0 ||
                  rep <= 0 || rows % seq != 0))
         return HIF8_ERR_SHAPE;
-    if (((uintptr_t)x | (uintptr_t)out | (uintptr_t)weight) & 15u) return HIF8_ERR_ALIGN;
+    if (((uintptr_t)x | (uintptr_t)out | (uintptr_t)weight | (uintptr_t)y_out) & 15u) return HIF8_ERR_ALIGN;
     if (rope && (((uintptr_t)cos_t | (uintptr_t)sin_t) & 15u)) return HIF8_ERR_ALIGN;
     if (rows >= (int64_t(1) << 40)) return HIF8_ERR_SHAPE;
     static int cu_cache[64] = {0};
@@ -190,16 +255,10 @@ extern "C" int hif8_rms_norm_rope(const uint16_t *x, const float *weight, const 
     const int grid = int(want < int64_t(cus) * 8 ? want : int64_t(cus) * 8);
     hipStream_t s = (hipStream_t)stream;
     const int nc = int(dim / 512);
-    const int hd = int(head_dim);
-#define HIF8_RN(NC)                                                                                                   \
-    case NC:                                                                                                          \
-        if (rope)                                                                                                     \
-            hipLaunchKernelGGL((dit::k_rms_norm_rope<NC, true>), dim3(grid), dim3(dit::kThreads), 0, s, x, weight,   \
-                               cos_t, sin_t, out, rows, int(dim), hd, seq, rep, eps);                                 \
-        else                                                                                                          \
-            hipLaunchKernelGGL((dit::k_rms_norm_rope<NC, false>), dim3(grid), dim3(dit::kThreads), 0, s, x, weight,  \
-                               cos_t, sin_t, out, rows, int(dim), 8, int64_t(1), int64_t(1), eps);                     \
-        break;
+    const int hd = rope ? int(head_dim) : 8;
+    const int64_t sq = rope ? seq : 1, rp = rope ? rep : 1;
+#define HIF8_RN_MODE(NC, R, M)                                                                                            hipLaunchKernelGGL((dit::k_rms_norm_rope<NC, R, M>), dim3(grid), dim3(dit::kThreads), 0, s, x, weight, cos_t,                           sin_t, out, rows, int(dim), hd, sq, rp, eps, st, smax, sem, y_out)
+#define HIF8_RN(NC)                                                                                                       case NC:                                                                                                                  if (mode == 0) {                                                                                                          if (rope) HIF8_RN_MODE(NC, true, 0);                                                                                  else HIF8_RN_MODE(NC, false, 0);                                                                                  } else if (mode == 1) {                                                                                                   if (rope) HIF8_RN_MODE(NC, true, 1);                                                                                  else HIF8_RN_MODE(NC, false, 1);                                                                                  } else {                                                                                                                  if (rope) HIF8_RN_MODE(NC, true, 2);                                                                                  else HIF8_RN_MODE(NC, false, 2);                                                                                  }                                                                                                                     break;
     switch (nc) {
         HIF8_RN(1) HIF8_RN(2) HIF8_RN(3) HIF8_RN(4) HIF8_RN(5) HIF8_RN(6) HIF8_RN(7) HIF8_RN(8)
         HIF8_RN(9) HIF8_RN(10) HIF8_RN(11) HIF8_RN(12) HIF8_RN(13) HIF8_RN(14) HIF8_RN(15) HIF8_RN(16)
@@ -207,7 +266,35 @@ extern "C" int hif8_rms_norm_rope(const uint16_t *x, const float *weight, const 
         return HIF8_ERR_SHAPE;
     }
 #undef HIF8_RN
+#undef HIF8_RN_MODE
     return hipGetLastError() == hipSuccess ? HIF8_OK : HIF8_ERR_HIP;
+}
+
+}  // namespace
+
+extern "C" int hif8_rms_norm_rope(const uint16_t *x, const float *weight, const float *cos_t, const float *sin_t,
+                                  uint16_t *out, int64_t rows, int64_t dim, int64_t head_dim, int64_t seq,
+                                  int64_t rep, float eps, hif8_stream_t stream)
+{
+    return launch_rms_norm_rope(0, x, weight, cos_t, sin_t, out, rows, dim, head_dim, seq, rep, eps, nullptr, 0.0f,
+                                kSemNpu, nullptr, stream);
+}
+
+extern "C" int hif8_rms_norm_rope_amax(const uint16_t *x, const float *weight, const float *cos_t, const float *sin_t,
+                                       int64_t rows, int64_t dim, int64_t head_dim, int64_t seq, int64_t rep,
+                                       float eps, float scale_max, void *state, hif8_stream_t stream)
+{
+    return launch_rms_norm_rope(1, x, weight, cos_t, sin_t, nullptr, rows, dim, head_dim, seq, rep, eps,
+                                (State *)state, scale_max, kSemNpu, nullptr, stream);
+}
+
+extern "C" int hif8_rms_norm_rope_fake_quant(const uint16_t *x, const float *weight, const float *cos_t,
+                                             const float *sin_t, int64_t rows, int64_t dim, int64_t head_dim,
+                                             int64_t seq, int64_t rep, float eps, const void *state, int semantics,
+                                             uint16_t *x_q, void *y, hif8_stream_t stream)
+{
+    return launch_rms_norm_rope(2, x, weight, cos_t, sin_t, x_q, rows, dim, head_dim, seq, rep, eps,
+                                (State *)state, 0.0f, semantics, y, stream);
 }
 
 extern "C" int hif8_gated_residual(const uint16_t *x, const uint16_t *y, const uint16_t *gate, uint16_t *out,

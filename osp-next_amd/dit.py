@@ -322,6 +322,46 @@ def rms_norm_rope(x: Tensor, norm: "OSPNextRMSNorm", cos_f: Optional[Tensor] = N
     return out
 
 
+def rms_norm_rope_quant(x: Tensor, norm: "OSPNextRMSNorm", scale_max: float, cos_f: Optional[Tensor] = None,
+                        sin_f: Optional[Tensor] = None, head_dim: int = 128,
+                        return_y: bool = False):
+    """quant_attn="hif8" on q or k as a producer: the attention's bf16 cast of
+    ``_quant(apply_rope(norm(x)))`` (the rope output in fp32, hif8_attention.py:60-74), or without
+    the angle tables of ``_quant(norm(x))`` (the bf16 norm output), in two passes over x
+    (hif8_rms_norm_rope_amax, hif8_rms_norm_rope_fake_quant), never writing the fp32 rope output.
+    Returns (x_q bf16 [B, N, dim], state), and with ``return_y`` the output that was quantised
+    (fp32 with rope, bf16 without) as a third element."""
+    B, N, dim = x.shape
+    x = x.contiguous()
+    w = norm.weight.detach().contiguous()
+    L = _lib.load()
+    s = _lib.stream_ptr(x.device)
+    st = QuantState(x.device)
+    xq = torch.empty_like(x)
+    y = None
+    if return_y:
+        y = torch.empty(x.shape, dtype=torch.float32 if cos_f is not None else torch.bfloat16, device=x.device)
+    yp = y.data_ptr() if y is not None else None
+    if cos_f is None:
+        c = sn = None
+        cp = sp = None
+        seq, rep = 1, 1
+    else:
+        fb = cos_f.shape[0]
+        if cos_f.shape[1] != N or (fb > 1 and B % fb != 0):
+            raise ValueError(f"angle tables {tuple(cos_f.shape)} do not match x {tuple(x.shape)}")
+        c = cos_f.to(torch.float32).contiguous()
+        sn = sin_f.to(torch.float32).contiguous()
+        cp, sp = c.data_ptr(), sn.data_ptr()
+        seq, rep = N, (B if fb == 1 else B // fb)
+    _lib.check(L.hif8_rms_norm_rope_amax(x.data_ptr(), w.data_ptr(), cp, sp, B * N, dim, head_dim, seq, rep,
+                                         float(norm.eps), float(scale_max), st.ptr, s), "hif8_rms_norm_rope_amax")
+    _lib.check(L.hif8_rms_norm_rope_fake_quant(x.data_ptr(), w.data_ptr(), cp, sp, B * N, dim, head_dim, seq, rep,
+                                               float(norm.eps), st.ptr, _lib.SEM_NPU, xq.data_ptr(), yp, s),
+               "hif8_rms_norm_rope_fake_quant")
+    return (xq, st, y) if return_y else (xq, st)
+
+
 class OSPNextRMSNorm(nn.Module):
     """WanRMSNorm (want2v.py:77-93) with an fp32 weight and a bf16 output, as the model runs it
     under FSDP2's high-precision policy for norms (``output_dtype`` bf16)."""
@@ -473,6 +513,11 @@ class OSPNextSelfAttention(nn.Module):
         """quant_attn="hif8" on the attention kernel."""
         return self.quant_attn == "hif8" and self._kernel_ok(q)
 
+    def _quantise_v(self, v: Tensor) -> Tensor:
+        """_quant(v) of the bf16 v (hif8_attention.py:60-74), in its shape."""
+        v2 = v.reshape(-1, v.shape[-1]).contiguous()
+        return fake_quant(v2, absmax_scale(v2, self.scale_max_forward, QuantState(v.device))).view(v.shape)
+
     def _quantised_attention(self, q: Tensor, k: Tensor, v: Tensor, key_mask: Optional[Tensor],
                              o_as_f32: bool) -> Tuple[Tensor, QuantState]:
         """quant_attn="hif8" on the attention kernel: the kernel's inputs are bf16(_quant(q)),
@@ -500,6 +545,18 @@ class OSPNextSelfAttention(nn.Module):
         ql, kl, vl = qkv
         B, N = ql.shape[:2]
         H, D = self.num_heads, self.head_dim
+        if (qkv_given and self._kernel_quant_attn_ok(ql.view(B, N, H, D)) and fused_norm_ok(ql, self.norm_q)
+                and fused_norm_ok(kl, self.norm_k) and vl.dtype == torch.bfloat16):
+            # quant_attn="hif8": q and k quantised by the norm + rope producer (two passes each,
+            # the fp32 rope output never written), v by the codec, then the attention kernel
+            cos_f, sin_f = rope_wrapper.prepare_freqs(grid_sizes_for_rope, D // 2, self.rearrange_rope)
+            qq, _ = rms_norm_rope_quant(ql, self.norm_q, self.scale_max_forward, cos_f, sin_f, D)
+            kq, _ = rms_norm_rope_quant(kl, self.norm_k, self.scale_max_forward, cos_f, sin_f, D)
+            vq = self._quantise_v(vl.view(B, N, H, D))
+            st = QuantState(ql.device)
+            x = attention_fwd(qq.view(B, N, H, D), kq.view(B, N, H, D), vq, *_cached_key_list(attn_mask), o_state=st,
+                              o_as_f32=True, scale_max=self.o.scale_max_forward)
+            return self.o.forward_settled(x.flatten(2), st, as_f32=True)
         if (qkv_given and self.quant_attn is None and isinstance(self.o, HIF8Linear) and fused_norm_ok(ql, self.norm_q)
                 and fused_norm_ok(kl, self.norm_k)):
             # norms, rope and the attention's bf16 cast in one pass each; the attention output
@@ -555,13 +612,20 @@ class OSPNextCrossAttention(OSPNextSelfAttention):
         if kv is None:
             kv = (self.k(text), self.v(text))
         ql = self.q(x) if x_q is None else self.q.forward_quantized(x_q)
-        if fused and self.quant_attn is None and fused_norm_ok(ql, self.norm_q) and fused_norm_ok(kv[0], self.norm_k):
+        # quant_attn="hif8" through the norm producers: q and k come out quantised
+        qa = (fused and self.quant_attn == "hif8" and D == 128 and ql.is_cuda and not torch.is_grad_enabled()
+              and isinstance(self.o, HIF8Linear) and fused_norm_ok(ql, self.norm_q)
+              and fused_norm_ok(kv[0], self.norm_k) and kv[1].dtype == torch.bfloat16)
+        if qa:
+            q, _ = rms_norm_rope_quant(ql, self.norm_q, self.scale_max_forward, head_dim=D)
+            k, _ = rms_norm_rope_quant(kv[0], self.norm_k, self.scale_max_forward, head_dim=D)
+        elif fused and self.quant_attn is None and fused_norm_ok(ql, self.norm_q) and fused_norm_ok(kv[0], self.norm_k):
             q = rms_norm_rope(ql, self.norm_q, head_dim=D)
             k = rms_norm_rope(kv[0], self.norm_k, head_dim=D)
         else:
             q = self.norm_q(ql)
             k = self.norm_k(kv[0])
-        v = kv[1]
+        v = self._quantise_v(kv[1]) if qa else kv[1]
         tb = text.shape[0]
         if tb != B:
             if tb != 1:
@@ -578,9 +642,16 @@ class OSPNextCrossAttention(OSPNextSelfAttention):
             st = QuantState(q.device)
             out = attention_fwd(q, k, v, o_state=st, scale_max=self.o.scale_max_forward)
             return self.o.forward_settled(out.reshape(B, -1, H * D), st)
-        if fused and self._kernel_quant_attn_ok(q) and q.dtype == k.dtype == v.dtype == torch.bfloat16:
+        if qa and attention_fwd_ok(q, k, v):
+            st = QuantState(q.device)
+            out = attention_fwd(q, k, v, o_state=st, scale_max=self.o.scale_max_forward)
+            return self.o.forward_settled(out.reshape(B, -1, H * D), st)
+        if fused and not qa and self._kernel_quant_attn_ok(q) and q.dtype == k.dtype == v.dtype == torch.bfloat16:
             out, st = self._quantised_attention(q, k, v, None, o_as_f32=False)
             return self.o.forward_settled(out.reshape(B, -1, H * D), st)
+        if qa:   # the quantised operands on SDPA (the kernel does not take these strides)
+            out = attention_key_masked(q, k, v, None)
+            return self.o(out.reshape(B, -1, H * D))
         out = self._attend(q, k, v, None)       # attn_mask is query-side: no effect in SDPA
         return self.o(out.reshape(B, -1, H * D))
 

@@ -105,6 +105,28 @@ def test_block_with_hif8_attention(dit):
     assert nw < TOL_HIF8[0] and mx < TOL_HIF8[1], (nw, mx)
 
 
+def test_block_with_hif8_attention_producers(dit, monkeypatch):
+    """quant_attn="hif8" at dim 512 (head dim 128), where the fused route's q and k come out of the
+    quantising norm + rope producer (self-attention with rope, cross-attention without) and the
+    attention kernel runs on the quantised operands: against the oracle's CPU block."""
+    kind, f2s, s2f, grid = CASES[0]
+    blk = make_block(dit, kind, f2s, s2f, dim=512, heads=4, ffn=1024, quant="hif8", device=DEV, quant_attn="hif8")
+    x, e, text = block_inputs(grid, dim=512, seed=11)
+    sd = {k: v.detach().cpu() for k, v in blk.state_dict().items()}
+    want = dit_ref.block(sd, x, e, text, grid, kind, f2s, s2f, num_heads=4, quant_attn="hif8")
+    calls = []
+    orig = dit.rms_norm_rope_quant
+
+    def spy(x_, norm, scale_max, cos_f=None, sin_f=None, head_dim=128, return_y=False):
+        calls.append(cos_f is not None)
+        return orig(x_, norm, scale_max, cos_f, sin_f, head_dim, return_y)
+    monkeypatch.setattr(dit, "rms_norm_rope_quant", spy)
+    got = run_block(dit, blk, x, e, text, grid, kind, None)
+    assert sorted(calls) == [False, False, True, True], calls
+    nw, mx = block_errors(got, want, out_layout(kind, f2s, s2f, x, grid))
+    assert nw < TOL_HIF8[0] and mx < TOL_HIF8[1], (nw, mx)
+
+
 def test_block_stack_dual_end(dit):
     """The block loop with the dual-end schedule (8 layers, 4 full): full, full, token (from full),
     group, token, group (to full), full, full; the output is in (t, h, w) order again."""

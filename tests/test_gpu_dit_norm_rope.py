@@ -132,3 +132,59 @@ def test_gated_residual_fallback_and_rejects(pkg):
     assert L.hif8_gated_residual(a.data_ptr(), a.data_ptr(), None, a.data_ptr(), 4, 60, 1, s) != 0          # dim % 8
     assert L.hif8_gated_residual(a.data_ptr() + 2, a.data_ptr(), None, a.data_ptr(), 2, 64, 1, s) != 0      # alignment
     assert L.hif8_gated_residual(None, a.data_ptr(), None, a.data_ptr(), 4, 64, 1, s) != 0
+
+
+@pytest.mark.parametrize("rope_on", [True, False])
+def test_quantising_producer_equals_codec(pkg, rope_on):
+    """quant_attn's q/k producer (hif8_rms_norm_rope_amax + _fake_quant): the output it quantises
+    is the one hif8_rms_norm_rope writes (fp32 with rope; its bf16 cast equal bit for bit), the
+    state it leaves equals hif8_absmax_scale of that output (fp32 rule with rope, bf16 without),
+    and x_q equals the codec's fake quant of it with that state (the bf16 cast of the fp32 x_q
+    with rope), bit for bit: _quant of the q the reference hands the attention, then its cast."""
+    D = pkg.dit
+    H, hd = 40, 128
+    dim = H * hd
+    B, grid, P = 4, (3, 8, 10), 2
+    rearr = D.SkiparseRearrange(P, D.RearrangeType.Skiparse2DToken)
+    rope = D.SkiparseRopeWrapper(D.rope_freqs(hd).to(DEV))
+    N = rope.prepare_freqs(grid, hd // 2, rearr)[0].shape[1]
+    g = torch.Generator().manual_seed(31 + int(rope_on))
+    x = (torch.randn(B, N, dim, generator=g) * 3).to(torch.bfloat16).to(DEV)
+    norm = D.OSPNextRMSNorm(dim, eps=1e-6, device=DEV)
+    print(f"[norm_rope] quantising producer rope={rope_on}", flush=True)
+    with torch.no_grad():
+        norm.weight.copy_((1 + 0.3 * torch.randn(dim, generator=g)).to(DEV))
+        if rope_on:
+            cos_f, sin_f = rope.prepare_freqs(grid, hd // 2, rearr)
+            xq, st, y = D.rms_norm_rope_quant(x, norm, 15.0, cos_f, sin_f, hd, return_y=True)
+            plain = D.rms_norm_rope(x, norm, cos_f, sin_f, hd)
+            assert y.dtype == torch.float32
+        else:
+            xq, st, y = D.rms_norm_rope_quant(x, norm, 15.0, return_y=True)
+            plain = D.rms_norm_rope(x, norm)
+            assert y.dtype == torch.bfloat16
+        assert torch.equal(y.to(torch.bfloat16).view(torch.int16), plain.view(torch.int16))
+        y2 = y.reshape(-1, dim)
+        full = pkg.absmax_scale(y2, 15.0, pkg.QuantState(DEV))
+        want = pkg.fake_quant_to_bf16(y2, full) if rope_on else pkg.fake_quant(y2, full)
+    torch.cuda.synchronize()
+    assert st.read() == full.read()
+    assert torch.equal(xq.reshape(-1, dim).view(torch.int16), want.view(torch.int16))
+
+
+def test_quantising_producer_rejects_bad_arguments(pkg):
+    L = pkg._lib.load()
+    s = pkg._lib.stream_ptr(torch.device(DEV))
+    x = torch.zeros(8, 1024, dtype=torch.bfloat16, device=DEV)
+    w = torch.ones(1024, dtype=torch.float32, device=DEV)
+    o = torch.empty_like(x)
+    st = pkg.QuantState(DEV)
+    assert L.hif8_rms_norm_rope_amax(x.data_ptr(), w.data_ptr(), None, None, 8, 1024, 128, 1, 1, 1e-6, 15.0, None, s) != 0
+    assert L.hif8_rms_norm_rope_amax(x.data_ptr(), w.data_ptr(), None, None, 8, 1024, 128, 1, 1, 1e-6, 0.0, st.ptr, s) != 0
+    assert L.hif8_rms_norm_rope_amax(x.data_ptr(), w.data_ptr(), None, None, 8, 1000, 128, 1, 1, 1e-6, 15.0, st.ptr, s) != 0
+    assert L.hif8_rms_norm_rope_fake_quant(x.data_ptr(), w.data_ptr(), None, None, 8, 1024, 128, 1, 1, 1e-6, st.ptr, 7,
+                                           o.data_ptr(), None, s) != 0
+    assert L.hif8_rms_norm_rope_fake_quant(x.data_ptr(), w.data_ptr(), None, None, 8, 1024, 128, 1, 1, 1e-6, st.ptr, 0,
+                                           None, None, s) != 0
+    assert L.hif8_rms_norm_rope_fake_quant(x.data_ptr(), w.data_ptr(), None, None, 8, 1024, 128, 1, 1, 1e-6, st.ptr, 0,
+                                           o.data_ptr(), o.data_ptr() + 4, s) != 0
