@@ -851,7 +851,7 @@ def main():
     ap.add_argument("--route", default="auto", choices=["auto", "fused", "decode_once"],
                     help="GEMM route for bf16 activations (auto: HIF8Linear's rule, decode_once at this M)")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--shapes", default="up,bwd,ffn,down,qkvo,c2,modln,qkv,attn,block,step",
+    ap.add_argument("--shapes", default="up,bwd,ffn,down,qkvo,c2,modln,qkv,attn,block,block_qa,step",
                     help="comma list of up,bwd (the FFN-up backward),down,qkvo (the other 14B linears),"
                          "c2 (the three 1.3B 480P linears, config 2),ffn,modln,qkv,attn (the block's "
                          "attention with the o amax epilogue),block (config 4),block_qa (config 4 with "
