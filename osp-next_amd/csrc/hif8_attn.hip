@@ -10,8 +10,8 @@
 // magnitudes it stores, so the amax pass is not needed.
 //
 // Design (flash attention, online softmax; head_dim 128):
-//   - One workgroup per 384 queries of one (batch, head); 12 waves, three per SIMD (168 VGPRs
-//     each), each owning 32 queries.  Keys go in tiles of 64: K and V tiles (16 KB each) are loaded
+//   - One workgroup per 384 queries of one (batch, head); 12 waves, three per SIMD (at most 168
+//     VGPRs each), each owning 32 queries.  Keys go in tiles of 64: K and V tiles (16 KB each) are loaded
 //     global -> LDS with buffer_load ... lds into one of two buffers while the other is computed;
 //     every wave reads the whole tile from LDS, so more waves per tile mean fewer tile loads per
 //     flop and more waves to cover each other's waits (measured at the 720P block's shape: 8 waves
@@ -26,15 +26,21 @@
 //   - Online softmax in the log2 domain with a lazily moved reference: the running max a tile's
 //     exponentials are taken against only moves when a tile's max exceeds it by more than 8 (the
 //     exponentials stay below 2^8 in between), so the O accumulators are rescaled a handful of times
-//     per query instead of at every tile.  Row sums are per-lane partials, reduced once at the end.
+//     per query instead of at every tile.  Row sums are per-lane partials of the bf16 probabilities
+//     the P.V products take (v_dot2c_f32_bf16 with (1, 1): two per instruction), reduced once at
+//     the end.  The row max is a tree of v_maximum3_f32 (fmaxf adds a canonicalising v_max per
+//     input), and fragment addresses are one lane base per operand with the tile, key-block and
+//     dim-block parts as immediate offsets: 115 VALU per wave and tile besides the exponentials
+//     and their fmas, against 177 before (4 % of the kernel's time).
 //   - Keys: an optional per-batch list of key rows (the rows the key mask keeps) and count; tiles
 //     past the count are masked to -inf.  The whole key tensor is never gathered.  The list's
 //     entries reach LDS like K and V (a ring of three 256-byte slots, two tiles ahead), so the loop
 //     has no load of its own to wait for: a wait for a global load issued after a tile's K/V loads
 //     would also wait for those (the counter completes in order), 14 % of the kernel's time.
-//   - The exponentials are about 8 % of the time (measured by replacing them); a wave's softmax
-//     and another wave's MFMAs overlap as the waves of a SIMD drift apart (staggering the waves by
-//     half a tile on purpose measured the same).
+//   - The exponentials are about 7 % of the time and the K/V loads after the prologue 12 %, of
+//     which the traffic is 2 % (a copy loading the same 64 L2-resident rows every tile) and the
+//     rest their issue and LDS writes: loading two tiles ahead into three buffers was slower, and
+//     without the per-tile barrier the kernel ran the same (measured by removing each).
 //   - Tile order: workgroup w runs on XCD w % 8; consecutive query tiles of one head are given to
 //     one XCD, so the CUs of an XCD stream the same K/V tiles through its L2.
 #include <hip/hip_runtime.h>
@@ -99,6 +105,8 @@ __device__ __forceinline__ f32x4 mfma(const u32x4 &a, const u32x4 &b, const f32x
                                                    0, 0, 0);
 }
 
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
 __device__ __forceinline__ u32x2 ld_tr(const uint8_t *lds_base, uint32_t off)
 {
     typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
@@ -121,11 +129,11 @@ __device__ __forceinline__ float max_over_groups(float m)
     const auto p = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(uint32_t, m), __builtin_bit_cast(uint32_t, m),
                                                     false, false);
     const uint32_t p0 = p[0], p1 = p[1];
-    m = __builtin_fmaxf(__builtin_bit_cast(float, p0), __builtin_bit_cast(float, p1));
+    m = __builtin_elementwise_maximum(__builtin_bit_cast(float, p0), __builtin_bit_cast(float, p1));
     const auto q = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(uint32_t, m), __builtin_bit_cast(uint32_t, m),
                                                     false, false);
     const uint32_t q0 = q[0], q1 = q[1];
-    return __builtin_fmaxf(__builtin_bit_cast(float, q0), __builtin_bit_cast(float, q1));
+    return __builtin_elementwise_maximum(__builtin_bit_cast(float, q0), __builtin_bit_cast(float, q1));
 }
 
 // LDS layout of a tile (64 keys x 128 dims, bf16):
@@ -254,6 +262,13 @@ template <bool LIST> __global__ __launch_bounds__(kThreads, 1) void k_attn_fwd(c
     const uint32_t kfrag = cq * 256u;                       // + kb * 4096, chunk ((4 pp + g) ^ cq) * 16
     const uint32_t vfrag = (8u * g) * 128u + 32u * ((lane & 15u) >> 2) + 8u * (lane & 3u);  // + block
 
+    // lane parts of the fragment addresses (the tile, key block and dim block parts are immediates):
+    // K chunk ((4 pp + g) ^ cq) of row cq; V block d ^ (g & 1) is d + (g & 1) for even d, d - (g & 1)
+    // for odd d
+    uint32_t ka[4];
+#pragma unroll
+    for (int pp = 0; pp < 4; ++pp) ka[pp] = kfrag + (((4u * pp + g) ^ cq) << 4);
+    const uint32_t va_e = vfrag + (g & 1u) * 128u, va_o = vfrag - (g & 1u) * 128u;
     for (int t = 0; t < ntiles; ++t) {
         ASMV("s_waitcnt vmcnt(0)" ::: "memory");
         __syncthreads();
@@ -269,7 +284,7 @@ template <bool LIST> __global__ __launch_bounds__(kThreads, 1) void k_attn_fwd(c
             s[kb][0] = s[kb][1] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int pp = 0; pp < 4; ++pp) {
-                const u32x4 kf = *(const u32x4 *)(ks + kb * 4096 + kfrag + (((4u * pp + g) ^ cq) << 4));
+                const u32x4 kf = *(const u32x4 *)(ks + ka[pp] + kb * 4096);
                 s[kb][0] = mfma(kf, qf[0][pp], s[kb][0]);
                 s[kb][1] = mfma(kf, qf[1][pp], s[kb][1]);
             }
@@ -286,11 +301,14 @@ template <bool LIST> __global__ __launch_bounds__(kThreads, 1) void k_attn_fwd(c
         u32x4 pf[2][2];
 #pragma unroll
         for (int qb = 0; qb < 2; ++qb) {
-            float mx = s[0][qb][0];
+            float v[16];
 #pragma unroll
-            for (int kb = 0; kb < 4; ++kb)
-#pragma unroll
-                for (int i = 0; i < 4; ++i) mx = __builtin_fmaxf(mx, s[kb][qb][i]);
+            for (int i = 0; i < 16; ++i) v[i] = s[i >> 2][qb][i & 3];
+#define MAX3(a, b, c) __builtin_elementwise_maximum(a, __builtin_elementwise_maximum(b, c))
+            const float m0 = MAX3(v[0], v[1], v[2]), m1 = MAX3(v[3], v[4], v[5]), m2 = MAX3(v[6], v[7], v[8]);
+            const float m3 = MAX3(v[9], v[10], v[11]), m4 = MAX3(v[12], v[13], v[14]);
+            float mx = __builtin_elementwise_maximum(MAX3(m0, m1, m2), MAX3(m3, m4, v[15]));
+#undef MAX3
             mx = max_over_groups(mx);
             const float mt = mx * c;
             if (__builtin_amdgcn_ballot_w64(mt > mref[qb] + kLazy)) {
@@ -308,13 +326,21 @@ template <bool LIST> __global__ __launch_bounds__(kThreads, 1) void k_attn_fwd(c
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     e[kb][i] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[kb][qb][i], c, nm));
-                    lsum[qb] += e[kb][i];
                 }
 #pragma unroll
             for (int kc = 0; kc < 2; ++kc)
                 pf[qb][kc] = u32x4{pk_bf16(e[2 * kc][0], e[2 * kc][1]), pk_bf16(e[2 * kc][2], e[2 * kc][3]),
                                    pk_bf16(e[2 * kc + 1][0], e[2 * kc + 1][1]),
                                    pk_bf16(e[2 * kc + 1][2], e[2 * kc + 1][3])};
+            // the row sums of the bf16 probabilities the P.V products take, two per instruction
+#pragma unroll
+            for (int kc = 0; kc < 2; ++kc)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const uint32_t w = pf[qb][kc][j];  // a scalar copy: a bit cast of a vector element reads element 0
+                    lsum[qb] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w),
+                                                              __builtin_bit_cast(bf16x2, 0x3F803F80u), lsum[qb], false);
+                }
         }
 
         // O^T += V^T P^T
@@ -322,8 +348,8 @@ template <bool LIST> __global__ __launch_bounds__(kThreads, 1) void k_attn_fwd(c
         for (int d = 0; d < 8; ++d) {
 #pragma unroll
             for (int kc = 0; kc < 2; ++kc) {
-                const uint32_t blk = (64u * kc + (uint32_t(d) ^ (g & 1u))) * 128u + vfrag;
-                const u32x2 lo = ld_tr(vs, blk), hi = ld_tr(vs, blk + 4096u);
+                const uint8_t *vb = vs + ((d & 1) ? va_o : va_e);
+                const u32x2 lo = ld_tr(vb, 8192u * kc + 128u * d), hi = ld_tr(vb, 8192u * kc + 128u * d + 4096u);
                 const u32x4 vf = u32x4{lo.x, lo.y, hi.x, hi.y};
                 o[d][0] = mfma(vf, pf[0][kc], o[d][0]);
                 o[d][1] = mfma(vf, pf[1][kc], o[d][1]);
