@@ -49,7 +49,9 @@ __device__ __forceinline__ uint32_t pack(float a, float b) { return bf(a) | (bf(
 // rule for smax (fp32 with rope, bf16 without), the last workgroup settling st: the _quant amax of
 // the q or k the reference hands hif8_attention_with_mask (hif8_attention.py:60-74).  MODE 2:
 // out = bf16 of that output's HiF8 fake quant with st's scale (the attention's bf16 cast of
-// _quant(q)), and y_out, if not null, the output itself (fp32 with rope, bf16 without).
+// _quant(q)), and y_out, if not null, the output itself (fp32 with rope, bf16 without).  For a
+// state with a finite scale the fake quant is the codec's table route (the encode table and the
+// state's bf16 decode table in LDS, fast_elem_bf16), otherwise the scalar route; the same bits.
 template <int NC, bool ROPE, int MODE>
 __global__ __launch_bounds__(kThreads) void k_rms_norm_rope(const uint16_t *__restrict__ x, const float *__restrict__ w,
                                                             const float *__restrict__ cs, const float *__restrict__ sn,
@@ -61,6 +63,20 @@ __global__ __launch_bounds__(kThreads) void k_rms_norm_rope(const uint16_t *__re
     const int lane = threadIdx.x & 63;
     uint32_t amax = 0;
     const float qs = MODE == 2 ? st->scale : 0.0f;
+    // MODE 2: the tables of the table route (one lut entry per thread)
+    static_assert(kThreads == 256, "one decode-table entry per thread");
+    __shared__ __attribute__((aligned(16))) uint8_t qtab[MODE == 2 ? kLdsBytes : 16];
+    const bool qfast = MODE == 2 && st->fast != 0;
+    const bool nan_guard = MODE == 2 && st->finite == 0;
+    if (MODE == 2) {
+        if (qfast) {
+            ((uint16_t *)(qtab + kLdsLutBf16))[threadIdx.x] = st->lut_bf16[threadIdx.x];
+            const uint4 *src = (const uint4 *)&kEncTable;
+            uint4 *dst = (uint4 *)(qtab + kTabLo);
+            for (uint32_t i = threadIdx.x; i < sizeof(EncTable) / 16; i += kThreads) dst[i] = src[i];
+        }
+        __syncthreads();
+    }
     const int64_t wstride = int64_t(gridDim.x) * (kThreads / 64);
     const float inv_dim = 1.0f / float(dim);
     for (int64_t row = int64_t(blockIdx.x) * (kThreads / 64) + (threadIdx.x >> 6); row < rows; row += wstride) {
@@ -136,13 +152,17 @@ __global__ __launch_bounds__(kThreads) void k_rms_norm_rope(const uint16_t *__re
                 uint32_t qb[8];
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
-                    uint32_t yb, code;
-                    if (ROPE) {
-                        slow_elem<kF32>(__builtin_bit_cast(uint32_t, f[e]), qs, sem, yb, code);
-                        qb[e] = f2bf(u2f(yb));
+                    if (qfast) {
+                        qb[e] = fast_elem_bf16<ROPE ? kF32 : kBF16>(f[e], qs, sem, qtab, nan_guard);
                     } else {
-                        slow_elem<kBF16>(bf(f[e]), qs, sem, yb, code);
-                        qb[e] = yb;
+                        uint32_t yb, code;
+                        if (ROPE) {
+                            slow_elem<kF32>(__builtin_bit_cast(uint32_t, f[e]), qs, sem, yb, code);
+                            qb[e] = f2bf(u2f(yb));
+                        } else {
+                            slow_elem<kBF16>(bf(f[e]), qs, sem, yb, code);
+                            qb[e] = yb;
+                        }
                     }
                 }
                 orow[c * 64 + lane] = u32x4{qb[0] | (qb[1] << 16), qb[2] | (qb[3] << 16), qb[4] | (qb[5] << 16),

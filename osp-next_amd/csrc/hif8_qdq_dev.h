@@ -81,6 +81,39 @@ __device__ __forceinline__ uint32_t clampu(uint32_t u)
     return u < kTabLo ? kTabLo : (u > kTabHi ? kTabHi : u);
 }
 
+// Table route of one element whose fake quant is wanted as bf16 bits (an attention or GEMM
+// operand), for a fast state (finite scale s > 0): DT kF32, v an fp32 value: the bf16 rounding of
+// the fp32 x_q; DT kBF16, v a bf16 value: the bf16 x_q.  The same bits as slow_elem (then f2bf for
+// kF32).  tab: LDS with the encode table at [kTabLo, kTabHi] and the state's bf16 decode table at
+// kLdsLutBf16.  The magnitude bits of x * s, truncated to bf16 for fp32, index the encode table:
+// HiF8 keeps at most 3 mantissa bits and rounds half away from zero, so the dropped bits never
+// change the rounding.  nan_guard (the state did not prove the tensor finite): NaN takes the NaN
+// code.  The torch semantics differ from the table only below 2^-22 (non-zero) and from 40960 up.
+template <int DT>
+__device__ __forceinline__ uint32_t fast_elem_bf16(float v, float s, int sem, const uint8_t *tab, bool nan_guard)
+{
+    uint32_t xs, u, full;
+    if (DT == kF32) {
+        xs = f2u(v * s);
+        u = (xs >> 16) & 0x7FFFu;
+        full = xs & 0x7FFFFFFFu;
+    } else {
+        xs = f2bf(v * s);
+        u = xs & 0x7FFFu;
+        full = u;
+    }
+    const uint32_t mag = tab[clampu(u)];
+    const uint32_t sign = (DT == kF32 ? xs >> 24 : xs >> 8) & 0x80u;
+    uint32_t code = mag ? (mag | sign) : 0u;   // magnitude 0 stays 0x00 (0x80 is NaN)
+    if (nan_guard && u > 0x7F80u) code = kNanCode;
+    uint32_t y = ((const uint16_t *)(tab + kLdsLutBf16))[code];
+    if (sem == kSemTorch && ((full != 0u && u < 0x3480u) || u >= 0x4720u)) {
+        const float q = qdq_torch(DT == kF32 ? u2f(xs) : bf2f(xs));
+        y = DT == kF32 ? f2bf(q / s) : f2bf(bf2f(f2bf(q)) / s);
+    }
+    return y;
+}
+
 // Sign fix-up for 4 magnitude codes: a code of magnitude 0 stays 0x00 (0x80 is NaN).
 __device__ __forceinline__ uint32_t apply_signs(uint32_t mags, uint32_t signs80)
 {

@@ -172,6 +172,57 @@ def test_quantising_producer_equals_codec(pkg, rope_on):
     assert torch.equal(xq.reshape(-1, dim).view(torch.int16), want.view(torch.int16))
 
 
+@pytest.mark.parametrize("rope_on", [True, False])
+@pytest.mark.parametrize("sem", ["npu", "torch"])
+def test_quantising_producer_scales_and_semantics(pkg, rope_on, sem):
+    """The fake-quant pass (hif8_rms_norm_rope_fake_quant) under states set to explicit scales and
+    both semantics: a regular scale, scales that put most values past 40960 (Inf codes; the torch
+    route's own rounding there) and below 2^-22 (flushed; torch keeps them), and non-finite and zero
+    scales (the scalar route), with a NaN row (the state did not prove the tensor finite).  x_q must
+    equal the codec's fake quant of the output the pass wrote (y_out) with the same state and
+    semantics, bit for bit: fake_quant_to_bf16 of the fp32 rope output, fake_quant of the bf16 norm
+    output."""
+    D = pkg.dit
+    L = pkg._lib.load()
+    stream = pkg._lib.stream_ptr(torch.device(DEV))
+    H, hd = 8, 128
+    dim = H * hd
+    B, grid, P = 4, (2, 4, 6), 2    # B: the P * P sub-grids of one video
+    rearr = D.SkiparseRearrange(P, D.RearrangeType.Skiparse2DToken)
+    rope = D.SkiparseRopeWrapper(D.rope_freqs(hd).to(DEV))
+    cos_f, sin_f = rope.prepare_freqs(grid, hd // 2, rearr)
+    N = cos_f.shape[1]
+    g = torch.Generator().manual_seed(77 + int(rope_on))
+    x = (torch.randn(B, N, dim, generator=g) * 3).to(torch.bfloat16)
+    x[0, 1, 5] = float("nan")                                   # a NaN row
+    x = x.to(DEV)
+    norm = D.OSPNextRMSNorm(dim, eps=1e-6, device=DEV)
+    semantics = pkg._lib.SEM_NPU if sem == "npu" else pkg._lib.SEM_TORCH
+    dtype = torch.float32 if rope_on else torch.bfloat16
+    with torch.no_grad():
+        norm.weight.copy_((1 + 0.3 * torch.randn(dim, generator=g)).to(DEV))
+    w = norm.weight.detach().contiguous()
+    c, sn = cos_f.to(torch.float32).contiguous(), sin_f.to(torch.float32).contiguous()
+    cp, sp = (c.data_ptr(), sn.data_ptr()) if rope_on else (None, None)
+    seq, rep = (N, B // cos_f.shape[0] if cos_f.shape[0] > 1 else B) if rope_on else (1, 1)
+    for scale in (15.0 / 4.0, 20000.0, 3e-7, float("inf"), 0.0):
+        print(f"[norm_rope] fake-quant pass rope={rope_on} sem={sem} scale={scale}", flush=True)
+        st = pkg.QuantState(DEV)
+        assert L.hif8_set_scale(st.ptr, pkg._lib.dtype_code(dtype), scale, stream) == 0
+        xq = torch.empty_like(x)
+        y = torch.empty(x.shape, dtype=dtype, device=DEV)
+        assert L.hif8_rms_norm_rope_fake_quant(x.data_ptr(), w.data_ptr(), cp, sp, B * N, dim, hd, seq, rep,
+                                               float(norm.eps), st.ptr, semantics, xq.data_ptr(), y.data_ptr(),
+                                               stream) == 0
+        y2 = y.reshape(-1, dim)
+        want = (pkg.fake_quant_to_bf16(y2, st, semantics) if rope_on else pkg.fake_quant(y2, st, semantics))
+        torch.cuda.synchronize()
+        assert torch.isnan(y2[1]).all()
+        got = xq.reshape(-1, dim).view(torch.int16)
+        assert torch.equal(got, want.view(torch.int16)), \
+            f"scale {scale}: {(got != want.view(torch.int16)).sum().item()} of {got.numel()} differ"
+
+
 def test_quantising_producer_rejects_bad_arguments(pkg):
     L = pkg._lib.load()
     s = pkg._lib.stream_ptr(torch.device(DEV))
