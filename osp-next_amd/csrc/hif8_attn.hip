@@ -309,10 +309,12 @@ template <bool LIST> __global__ __launch_bounds__(kThreads, 1) void k_attn_fwd(c
             const float m3 = MAX3(v[9], v[10], v[11]), m4 = MAX3(v[12], v[13], v[14]);
             float mx = __builtin_elementwise_maximum(MAX3(m0, m1, m2), MAX3(m3, m4, v[15]));
 #undef MAX3
-            mx = max_over_groups(mx);
+            // this lane's scaled maximum: a query's tile maximum exceeds the reference by more than
+            // kLazy if one of its four lanes' does, and the reduction over the lanes (scaling by
+            // c > 0 commutes with it) is only needed when the reference moves
             const float mt = mx * c;
             if (__builtin_amdgcn_ballot_w64(mt > mref[qb] + kLazy)) {
-                const float mn = __builtin_fmaxf(mref[qb], mt);
+                const float mn = __builtin_fmaxf(mref[qb], max_over_groups(mt));
                 const float alpha = __builtin_amdgcn_exp2f(mref[qb] - mn);
                 lsum[qb] *= alpha;
 #pragma unroll
