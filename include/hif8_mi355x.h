@@ -352,6 +352,19 @@ int hif8_gated_residual(const uint16_t *x, const uint16_t *y, const uint16_t *ga
                         int64_t dim, int64_t rows_per_batch, hif8_stream_t stream);
 
 /* ---------------------------------------------------------------------------
+ * The block's token layout changes (the harness around the path): the Skiparse rearranges
+ * (skiparse_func.py:18-52: token, group, their reverses and token <-> group) with the zero padding
+ * of a full -> Skiparse change and the cropping of a Skiparse -> full one (SkiparseRearrange.forward,
+ * osp_next.py:239-283) are each one row permutation, run as a gather:
+ *     out[r, :] = x[src_row[r], :]  for 0 <= src_row[r] < in_rows, zeros otherwise.
+ * x bf16 [in_rows, cols], out bf16 [rows, cols], src_row int32 [rows]; cols % 8 == 0,
+ * rows * cols / 8 < 2^31, 16-byte aligned x and out.  The reference runs them as einops / torch
+ * permutes and pads; this replaces no reference interface of its own.
+ */
+int hif8_gather_rows(const uint16_t *x, int64_t in_rows, const int32_t *src_row, int64_t rows, int64_t cols,
+                     uint16_t *out, hif8_stream_t stream);
+
+/* ---------------------------------------------------------------------------
  * Producer fusion for the affine LayerNorm in front of the cross-attention's q
  * projection:
  *     y = norm3(x)                                        (osp_next.py:949-951)

@@ -52,6 +52,7 @@ SIGNATURES = {
     "hif8_modln_quant_static": (_i, [_p, _p, _p, _i64, _i64, _i64, _f, _f, _i, _p, _p]),
     "hif8_ln_affine_amax": (_i, [_p, _p, _p, _i64, _i64, _f, _p, _f, _p, _p]),
     "hif8_gated_residual": (_i, [_p, _p, _p, _p, _i64, _i64, _i64, _p]),
+    "hif8_gather_rows": (_i, [_p, _i64, _p, _i64, _i64, _p, _p]),
     "hif8_ln_affine_fake_quant": (_i, [_p, _p, _p, _i64, _i64, _p, _p, _i, _p, _p, _p]),
     "hif8_linear_fwd_wq": (_i, [_p, _p, _p, _p, _i64, _i64, _i64, _p]),
     "hif8_linear_fwd_wq_gelu_stat": (_i, [_p, _p, _p, _p, _i64, _i64, _i64, _f, _p, _p]),

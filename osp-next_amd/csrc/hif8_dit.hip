@@ -236,6 +236,37 @@ __global__ __launch_bounds__(kThreads) void k_gated_residual(const u32x4 *x, con
     }
 }
 
+// The block's layout changes as one row gather: the Skiparse rearranges (skiparse_func.py:18-52)
+// and the padding and cropping around them (SkiparseRearrange.forward, osp_next.py:239-283) each
+// send every token row to one output row and fill the padding rows with zeros.  out[r] = x[src[r]]
+// for 0 <= src[r] < in_rows, a zero row otherwise; rows of vpr 16-byte vectors.  Each thread
+// moves one vector per step, kGatherU steps in flight; n = rows * vpr < 2^31.
+constexpr int kGatherU = 4;
+__global__ __launch_bounds__(kThreads) void k_gather_rows(const u32x4 *__restrict__ x, const int32_t *__restrict__ src,
+                                                          uint32_t n, uint32_t vpr, int64_t in_rows,
+                                                          u32x4 *__restrict__ out)
+{
+    const uint32_t stride = gridDim.x * uint32_t(kThreads);
+    for (uint32_t base = blockIdx.x * uint32_t(kThreads) + threadIdx.x; base < n; base += stride * kGatherU) {
+        u32x4 v[kGatherU];
+#pragma unroll
+        for (int u = 0; u < kGatherU; ++u) {
+            const uint32_t i = base + uint32_t(u) * stride;
+            v[u] = u32x4{0u, 0u, 0u, 0u};
+            if (i < n) {
+                const uint32_t r = i / vpr, c = i - r * vpr;
+                const int32_t sr = src[r];
+                if (sr >= 0 && sr < in_rows) v[u] = __builtin_nontemporal_load(&x[int64_t(sr) * vpr + c]);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < kGatherU; ++u) {
+            const uint32_t i = base + uint32_t(u) * stride;
+            if (i < n) out[i] = v[u];
+        }
+    }
+}
+
 }  // namespace dit
 }  // namespace hif8
 
@@ -338,5 +369,23 @@ extern "C" int hif8_gated_residual(const uint16_t *x, const uint16_t *y, const u
     else
         hipLaunchKernelGGL(dit::k_gated_residual<false>, dim3(grid), dim3(dit::kThreads), 0, s, (const V *)x,
                            (const V *)y, (const uint16_t *)nullptr, (V *)out, nvec, dim, int64_t(1));
+    return hipGetLastError() == hipSuccess ? HIF8_OK : HIF8_ERR_HIP;
+}
+
+extern "C" int hif8_gather_rows(const uint16_t *x, int64_t in_rows, const int32_t *src_row, int64_t rows,
+                                int64_t cols, uint16_t *out, hif8_stream_t stream)
+{
+    if (!x || !src_row || !out || in_rows <= 0 || rows <= 0 || cols <= 0) return HIF8_ERR_ARG;
+    if (cols % 8 != 0 || rows * (cols / 8) >= (int64_t(1) << 31)) return HIF8_ERR_SHAPE;
+    if (((uintptr_t)x | (uintptr_t)out) & 15u || ((uintptr_t)src_row & 3u)) return HIF8_ERR_ALIGN;
+    const int64_t vpr = cols / 8, n = rows * vpr;
+    int dev = 0, cus = 256;
+    if (hipGetDevice(&dev) == hipSuccess && hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+        cus = 256;
+    const int64_t want = (n + int64_t(dit::kThreads) * dit::kGatherU - 1) / (int64_t(dit::kThreads) * dit::kGatherU);
+    const int grid = int(want < int64_t(cus) * 8 ? want : int64_t(cus) * 8);
+    typedef dit::u32x4 V;
+    hipLaunchKernelGGL(dit::k_gather_rows, dim3(grid), dim3(dit::kThreads), 0, (hipStream_t)stream, (const V *)x,
+                       src_row, uint32_t(n), uint32_t(vpr), in_rows, (V *)out);
     return hipGetLastError() == hipSuccess ? HIF8_OK : HIF8_ERR_HIP;
 }

@@ -146,13 +146,17 @@ _DISPATCH = {
 class SkiparseRearrange:
     """``SkiparseRearrange.forward`` (osp_next.py:239-283) on one GPU: H and W are padded with
     zero tokens to multiples of P*P before a full -> skiparse rearrange, and the padding is
-    cropped after a skiparse -> full one."""
+    cropped after a skiparse -> full one.  With ``gather`` (the block's fused route) a bf16 CUDA
+    tensor is moved in one pass (``hif8_gather_rows``) by a map of source rows that the torch
+    path itself makes of a row-index tensor (padding rows -1), built on the first call for a
+    shape and kept; the same bits as the torch path."""
 
     def __init__(self, sparse_ratio: int = 1, rearrange_type: str = RearrangeType.Identity):
         if rearrange_type != RearrangeType.Identity and rearrange_type not in _DISPATCH:
             raise ValueError(f"unsupported rearrange {rearrange_type}")
         self.sparse_ratio = sparse_ratio
         self.rearrange_type = rearrange_type
+        self._maps = {}
 
     def paddings(self, grid) -> Tuple[int, int]:
         """osp_next.py:222-237."""
@@ -161,10 +165,38 @@ class SkiparseRearrange:
         bs = self.sparse_ratio ** 2
         return (bs - grid[1] % bs) % bs, (bs - grid[2] % bs) % bs
 
-    def __call__(self, x: Optional[Tensor], grid=None) -> Optional[Tensor]:
+    def __call__(self, x: Optional[Tensor], grid=None, gather: bool = False) -> Optional[Tensor]:
         rt = self.rearrange_type
         if x is None or rt == RearrangeType.Identity:
             return x
+        if (gather and x.is_cuda and x.dtype == torch.bfloat16 and x.dim() == 3 and x.numel() > 0
+                and x.shape[-1] % 8 == 0):
+            out = self._gather(x, grid)
+            if out is not None:
+                return out
+        return self._torch(x, grid)
+
+    def _gather(self, x: Tensor, grid) -> Optional[Tensor]:
+        B, N, C = x.shape
+        key = (B, N, tuple(grid), x.device)
+        hit = self._maps.get(key)
+        if hit is None:
+            ids = torch.arange(B * N, dtype=torch.int32, device=x.device).view(B, N, 1)
+            m = self._torch(ids, grid, pad_value=-1)
+            if len(self._maps) >= 8:
+                self._maps.clear()
+            hit = self._maps[key] = (m.reshape(-1).contiguous(), tuple(m.shape[:2]))
+        src, (Bo, No) = hit
+        x = x.contiguous()
+        if x.data_ptr() % 16 != 0 or src.numel() * (C // 8) >= 2 ** 31:
+            return None
+        out = torch.empty((Bo, No, C), dtype=x.dtype, device=x.device)
+        _lib.check(_lib.load().hif8_gather_rows(x.data_ptr(), B * N, src.data_ptr(), src.numel(), C,
+                                                out.data_ptr(), _lib.stream_ptr(x.device)), "hif8_gather_rows")
+        return out
+
+    def _torch(self, x: Tensor, grid, pad_value: int = 0) -> Tensor:
+        rt = self.rearrange_type
         P = self.sparse_ratio
         T, H, W = grid
         ph, pw = self.paddings(grid)
@@ -174,7 +206,7 @@ class SkiparseRearrange:
         if rt in RearrangeType.FROM_FULL:
             x = x.contiguous()
             if ph or pw:
-                x = F.pad(x.view(B, T, H, W, C), (0, 0, 0, pw, 0, ph)).view(B, -1, C)
+                x = F.pad(x.view(B, T, H, W, C), (0, 0, 0, pw, 0, ph), value=pad_value).view(B, -1, C)
             return fn(x, (T, Hp, Wp), P)
         if rt in RearrangeType.TO_FULL:
             x = fn(x.contiguous(), (T, Hp, Wp), P)
@@ -754,12 +786,14 @@ class OSPNextAttentionBlock(nn.Module):
         """osp_next.py:960-1022 (no checkpointing).  With batch 1 the repeated text and
         modulation of a skiparse block (``context_rearrange_input``) are kept as one copy:
         broadcasting one row gives the same values as its P*P copies."""
-        x = self.rearrange_input(x, sub_grid_sizes)
+        # the fused route moves bf16 rows with one gather per layout change
+        g = self.fused_ok(x) if fused is None else bool(fused)
+        x = self.rearrange_input(x, sub_grid_sizes, gather=g)
         if self.repeats > 1 and text.shape[0] > 1:
             text = text.repeat(self.repeats, 1, 1)
             e = e.repeat(self.repeats, 1, 1)
         x = self.block_forward(x, attn_mask, cross_attn_mask, e, grid_sizes_for_rope, rope_wrapper, text, fused)
-        return self.rearrange_output(x, sub_grid_sizes)
+        return self.rearrange_output(x, sub_grid_sizes, gather=g)
 
 
 # -------------------------------------------------------------- block schedule

@@ -134,6 +134,57 @@ def test_gated_residual_fallback_and_rejects(pkg):
     assert L.hif8_gated_residual(None, a.data_ptr(), None, a.data_ptr(), 4, 64, 1, s) != 0
 
 
+@pytest.mark.parametrize("kind,grid,B", [("token", (3, 10, 14), 1), ("token", (2, 8, 12), 2), ("group", (3, 10, 14), 1),
+                                         ("token_rev", (3, 10, 14), 1), ("group_rev", (2, 8, 12), 2),
+                                         ("t2g", (3, 10, 14), 1), ("g2t", (2, 8, 12), 1)])
+def test_layout_gather_equals_torch(pkg, kind, grid, B):
+    """SkiparseRearrange with ``gather`` (hif8_gather_rows over a map of source rows) against its
+    torch path (skiparse_func.py:18-52 with the padding and cropping of osp_next.py:239-283): every
+    layout change, with and without padding rows (H, W not multiples of P * P), bit for bit, and
+    again with other values through the kept map."""
+    D = pkg.dit
+    RT = D.RearrangeType
+    P, C = 2, 136
+    T, H, W = grid
+    g = torch.Generator().manual_seed(len(kind) * 10 + T)
+    full = torch.randn(B, T * H * W, C, generator=g).to(torch.bfloat16).to(DEV)
+    src_rt, rt = {"token": (None, RT.Skiparse2DToken), "group": (None, RT.Skiparse2DGroup),
+                  "token_rev": (RT.Skiparse2DToken, RT.Skiparse2DTokenReverse),
+                  "group_rev": (RT.Skiparse2DGroup, RT.Skiparse2DGroupReverse),
+                  "t2g": (RT.Skiparse2DToken, RT.Skiparse2DToken2Group),
+                  "g2t": (RT.Skiparse2DGroup, RT.Skiparse2DGroup2Token)}[kind]
+    prep = (lambda t: t) if src_rt is None else (lambda t: D.SkiparseRearrange(P, src_rt)(t, grid))
+    r = D.SkiparseRearrange(P, rt)
+    print(f"[gather] {kind} grid={grid} B={B}", flush=True)
+    for rep in range(2):
+        x = prep(full if rep == 0 else torch.randn(full.shape, generator=g).to(torch.bfloat16).to(DEV))
+        want = r(x, grid)
+        got = r(x, grid, gather=True)
+        torch.cuda.synchronize()
+        assert got.shape == want.shape
+        assert torch.equal(got.view(torch.int16), want.view(torch.int16))
+    assert len(r._maps) == 1
+
+
+def test_layout_gather_rejects_bad_arguments(pkg):
+    L = pkg._lib.load()
+    s = pkg._lib.stream_ptr(torch.device(DEV))
+    x = torch.zeros(8, 64, dtype=torch.bfloat16, device=DEV)
+    o = torch.empty_like(x)
+    src = torch.arange(8, dtype=torch.int32, device=DEV)
+    assert L.hif8_gather_rows(x.data_ptr(), 8, src.data_ptr(), 8, 60, o.data_ptr(), s) != 0       # cols % 8
+    assert L.hif8_gather_rows(x.data_ptr() + 2, 8, src.data_ptr(), 4, 64, o.data_ptr(), s) != 0   # alignment
+    assert L.hif8_gather_rows(x.data_ptr(), 8, None, 8, 64, o.data_ptr(), s) != 0
+    assert L.hif8_gather_rows(x.data_ptr(), 0, src.data_ptr(), 8, 64, o.data_ptr(), s) != 0
+    # a source row out of range gives a zero row
+    x.fill_(1.0)
+    src[3] = 9
+    src[5] = -1
+    assert L.hif8_gather_rows(x.data_ptr(), 8, src.data_ptr(), 8, 64, o.data_ptr(), s) == 0
+    torch.cuda.synchronize()
+    assert float(o[3].abs().sum()) == 0.0 and float(o[5].abs().sum()) == 0.0 and bool((o[4] == 1).all())
+
+
 @pytest.mark.parametrize("rope_on", [True, False])
 def test_quantising_producer_equals_codec(pkg, rope_on):
     """quant_attn's q/k producer (hif8_rms_norm_rope_amax + _fake_quant): the output it quantises
