@@ -194,6 +194,22 @@ template <bool LIST> __global__ __launch_bounds__(kThreads, 1) void k_attn_fwd(c
         }
     }
     const uint32_t krs = uint32_t(p.k_rs * 2), vrs = uint32_t(p.v_rs * 2);
+    // contiguous keys: a DTL item's lane offset inside its tile is the same for every tile (the
+    // tile's first row goes into the buffer resource's base, rows past the tensor read as zero)
+    uint32_t voffc[3] = {0u, 0u, 0u};
+    if (!LIST) {
+#pragma unroll
+        for (int j = 0; j < 3; ++j) {
+            const uint32_t item = wave + uint32_t(j) * kWaves;
+            if (item < 16) {
+                const uint32_t r = 4u * item + (lane >> 4);
+                voffc[j] = r * krs + ((lane & 15u) ^ (r & 15u)) * 16u;
+            } else if (item < 32) {
+                const uint32_t it = item - 16u, r = 4u * it + ((lane & 7u) >> 1);
+                voffc[j] = r * vrs + (16u * (((lane >> 3) ^ (it & 1u))) + 8u * (lane & 1u)) * 2u;
+            }
+        }
+    }
     const uint32_t lds0 = uint32_t(uintptr_t(smem));
     // the key-list entries of tile t into ring slot t % 3 (wave 0)
     auto list_dtl = [&](int t) {
@@ -201,10 +217,28 @@ template <bool LIST> __global__ __launch_bounds__(kThreads, 1) void k_attn_fwd(c
             dtl_load_b32(__builtin_amdgcn_readfirstlane(lds0 + kList + uint32_t(t % 3) * (kBN * 4)),
                          (uint32_t(t) * kBN + lane) * 4u, rl);
     };
-    // the DTL of tile t: keys past the count read row 0 (list) or the last row, and are masked;
-    // list entries are clamped into the tensor
+    // the DTL of tile t: list entries are clamped into the tensor (keys past the count read row 0);
+    // contiguous keys past the tensor read as zero through the buffer's range; keys past the count
+    // are masked
     auto issue_tile = [&](int t) {
         const uint32_t buf = uint32_t(t & 1);
+        if (!LIST) {
+            // tile t's first row is row 64 t: base + 64 t rows, range less the same (t * 64 < n_kv)
+            const uint32_t ko = uint32_t(t) * (uint32_t(kBN) * krs), vo = uint32_t(t) * (uint32_t(kBN) * vrs);
+            const uint64_t kb = ((uint64_t(rk[1]) << 32) | rk[0]) + ko, vb = ((uint64_t(rv[1]) << 32) | rv[0]) + vo;
+            const u32x4 rkt = u32x4{uint32_t(kb), uint32_t(kb >> 32), rk[2] - ko, rk[3]};
+            const u32x4 rvt = u32x4{uint32_t(vb), uint32_t(vb >> 32), rv[2] - vo, rv[3]};
+#pragma unroll
+            for (int j = 0; j < 3; ++j) {
+                const uint32_t item = wave + uint32_t(j) * kWaves;
+                if (item < 16)
+                    dtl_load(__builtin_amdgcn_readfirstlane(lds0 + buf * kTile + item * 1024u), voffc[j], rkt);
+                else if (item < 32)
+                    dtl_load(__builtin_amdgcn_readfirstlane(lds0 + 2u * kTile + buf * kTile + (item - 16u) * 1024u),
+                             voffc[j], rvt);
+            }
+            return;
+        }
         const int *slot = (const int *)(smem + kList + uint32_t(t % 3) * (kBN * 4));
         // 32 DTL items per tile (16 of K, 16 of V) over the waves: items wave, wave + 12, ...
 #pragma unroll
