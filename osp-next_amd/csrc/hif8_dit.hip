@@ -35,14 +35,9 @@ constexpr int kMaxChunks = 16;  // dim <= 8192
 
 __device__ __forceinline__ float lo(uint32_t v) { return __builtin_bit_cast(float, v << 16); }
 __device__ __forceinline__ float hi(uint32_t v) { return __builtin_bit_cast(float, v & 0xFFFF0000u); }
-__device__ __forceinline__ uint32_t bf(float f)
-{
-    // round to nearest even; NaN stays NaN
-    const uint32_t u = __builtin_bit_cast(uint32_t, f);
-    if ((u & 0x7FFFFFFFu) > 0x7F800000u) return (u >> 16) | 0x40u;
-    return (u + 0x7FFFu + ((u >> 16) & 1u)) >> 16;
-}
-__device__ __forceinline__ uint32_t pack(float a, float b) { return bf(a) | (bf(b) << 16); }
+// Round-to-nearest-even to bf16 of two floats in one v_cvt_pk_bf16_f32 (f2bf_pk): the same bits
+// as the integer RNE for every finite value, as the codec relies on; NaN stays NaN.
+__device__ __forceinline__ uint32_t pack(float a, float b) { return f2bf_pk(a, b); }
 
 // MODE 0: out = the bf16 output.  MODE 1: no output; the amax of the output before that rounding
 // -- the fp32 rope output, or without rope the bf16 norm output -- folded into st with the scale
@@ -120,9 +115,11 @@ __global__ __launch_bounds__(kThreads) void k_rms_norm_rope(const uint16_t *__re
                 y[2 * t + 1] = hi(v[c][t]);
             }
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const float y1 = __builtin_bit_cast(float, bf(y[e] * r) << 16);
-                y[e] = __builtin_bit_cast(float, bf(y1 * wv[e]) << 16);
+            for (int e = 0; e < 8; e += 2) {
+                const uint32_t y1 = pack(y[e] * r, y[e + 1] * r);
+                const uint32_t y2 = pack(lo(y1) * wv[e], hi(y1) * wv[e + 1]);
+                y[e] = lo(y2);
+                y[e + 1] = hi(y2);
             }
             float f[8];
             if (ROPE) {
@@ -145,8 +142,10 @@ __global__ __launch_bounds__(kThreads) void k_rms_norm_rope(const uint16_t *__re
             } else if (MODE == 1) {
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
-                    const uint32_t mb = ROPE ? (__builtin_bit_cast(uint32_t, f[e]) & 0x7FFFFFFFu) : (bf(f[e]) & 0x7FFFu);
-                    amax = mb > amax ? mb : amax;
+                    // without rope f[e] is a bf16 value: its top half is its bf16 bits
+                    const uint32_t mb = __builtin_bit_cast(uint32_t, f[e]) & 0x7FFFFFFFu;
+                    const uint32_t m = ROPE ? mb : (mb >> 16);
+                    amax = m > amax ? m : amax;
                 }
             } else {
                 uint32_t qb[8];
@@ -160,7 +159,7 @@ __global__ __launch_bounds__(kThreads) void k_rms_norm_rope(const uint16_t *__re
                             slow_elem<kF32>(__builtin_bit_cast(uint32_t, f[e]), qs, sem, yb, code);
                             qb[e] = f2bf(u2f(yb));
                         } else {
-                            slow_elem<kBF16>(bf(f[e]), qs, sem, yb, code);
+                            slow_elem<kBF16>(__builtin_bit_cast(uint32_t, f[e]) >> 16, qs, sem, yb, code);
                             qb[e] = yb;
                         }
                     }
