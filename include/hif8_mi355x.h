@@ -55,11 +55,13 @@ enum { HIF8_DTYPE_BF16 = 0, HIF8_DTYPE_F32 = 1, HIF8_DTYPE_BF16_AS_F32 = 2 };
  * (ospnext/modules/attention.py:473,518 and osp_next.py:644): quantising the bf16 tensor
  * directly gives the same x_q without materialising the fp32 copy.  Taken by
  * hif8_absmax_scale, hif8_encode, hif8_fake_quant (y fp32) and hif8_fake_quant_to_bf16. */
-enum { HIF8_SEM_NPU = 0, HIF8_SEM_TORCH = 1, HIF8_SEM_TORCH_BF16 = 2 };
+enum { HIF8_SEM_NPU = 0, HIF8_SEM_TORCH = 1, HIF8_SEM_TORCH_BF16 = 2, HIF8_SEM_TORCH_F16 = 3 };
 /* HIF8_SEM_TORCH_BF16: QFuncs/hif8.py:6-23 evaluated in bf16 arithmetic, every op rounded to bf16
  * -- quant_dequant_float(x, QType('hif8'), force_py=True, force_fp32=False) of a bf16 tensor
  * (QTensor.py:99-102 skipped).  It differs from HIF8_SEM_TORCH only for |x| < 2^-43.  Taken by
- * hif8_quant_bf16 only. */
+ * hif8_quant_bf16 only.
+ * HIF8_SEM_TORCH_F16: the same for an fp16 tensor -- the fp16 branch of QFuncs/hif8.py:10-11
+ * (offset 2^-14) with every op rounded to fp16.  Taken by hif8_quant_f16 only. */
 
 /* Text for a status code (static storage). */
 const char *hif8_strerror(int status);
@@ -140,6 +142,13 @@ int hif8_decode(const uint8_t *codes, int64_t n, const void *state, int out_dtyp
 int hif8_quant_f32(const float *x, float *y, int64_t n, int semantics, hif8_stream_t stream);
 int hif8_quant_bf16(const uint16_t *x, uint16_t *y, int64_t n, int semantics,
                     hif8_stream_t stream);
+/* quant_dequant_float(x, QType('hif8'), force_py, force_fp32) of an fp16 tensor, fp16 in and
+ * out (QTensor.py:94-128 with its dtype routing at :66-79): HIF8_SEM_NPU -- the reference has no
+ * fp16 NPU kernel, so the fp32 kernel runs on x.float() and the result is cast back to fp16
+ * (QTensor.py:72-79,126-127); HIF8_SEM_TORCH -- force_py with force_fp32: QFuncs/hif8.py:6-23 in
+ * fp32, then the cast; HIF8_SEM_TORCH_F16 -- force_py alone: the function in fp16 arithmetic
+ * (QFuncs/hif8.py:10-11).  Any alignment; n >= 1. */
+int hif8_quant_f16(const uint16_t *x, uint16_t *y, int64_t n, int semantics, hif8_stream_t stream);
 
 /* ---------------------------------------------------------------------------
  * Fused HiF8 linear forward: hif8_linear.py:68-86
@@ -293,6 +302,26 @@ int hif8_transpose_bf16(const uint16_t *x, int64_t rows, int64_t cols, int64_t r
  * own in the reference. */
 int hif8_linear_wgrad(const uint16_t *g, const uint16_t *x, uint16_t *dw, int64_t tokens, int64_t n_out,
                       int64_t k_in, void *workspace, int64_t workspace_bytes, hif8_stream_t stream);
+
+/* The backward's products for a layer that computes in fp32: grad_q @ w_q and grad_q^T @ x_q
+ * (hif8_linear.py:97,104), which the reference evaluates as matmuls in the saved tensors' dtype.
+ *   c[m][n] = sum_k a[m*sa_m + k*sa_k] * b[k*sb_k + n*sb_n]      (fp32 fused multiply-adds)
+ * a, b: HIF8_DTYPE_BF16 or HIF8_DTYPE_F32 elements with any element strides (a transposed operand
+ * is a stride pair); c: [M, N] row-major, HIF8_DTYPE_F32 or HIF8_DTYPE_BF16 (RNE).  M < 2^22.
+ * An LDS-tiled fp32 kernel (the MFMA kernels take bf16 operands only); the sums' order differs
+ * from the vendor matmul's. */
+int hif8_gemm_f32(const void *a, int a_dtype, const void *b, int b_dtype, void *c, int c_dtype, int64_t M,
+                  int64_t N, int64_t K, int64_t sa_m, int64_t sa_k, int64_t sb_k, int64_t sb_n,
+                  hif8_stream_t stream);
+
+/* Zero padding (or cropping) of a row-major matrix: dst[r][c] = src[r][c] for r < src_rows and
+ * c < src_cols, 0 elsewhere in [dst_rows][dst_cols]; elem_bytes 1 (codes), 2 (bf16) or 4.  The
+ * linears whose in_features is not a multiple of 64 or out_features not a multiple of 8 run the
+ * MFMA GEMMs on operands padded with zeros (zero codes decode to 0, so the padding adds nothing)
+ * and crop the output.  Any alignment.  No counterpart in the reference (its vendor GEMM takes
+ * any shape). */
+int hif8_pad_2d(const void *src, int64_t src_rows, int64_t src_cols, void *dst, int64_t dst_rows,
+                int64_t dst_cols, int elem_bytes, hif8_stream_t stream);
 
 /* ---------------------------------------------------------------------------
  * Producer fusion for the modulated LayerNorm in front of the self-attention q/k/v

@@ -110,6 +110,59 @@ def quant_hif8_torch_bf16(x_bits) -> np.ndarray:
     return out
 
 
+def f16_to_f32(bits) -> np.ndarray:
+    """fp16 bit patterns (uint16) -> exact float32 values."""
+    return np.asarray(bits, dtype=np.uint16).view(np.float16).astype(F32)
+
+
+def f32_to_f16(x) -> np.ndarray:
+    """float32 -> fp16 bits, round-to-nearest-even with subnormals, overflow to Inf
+    (c10::Half's conversion; numpy's float32 -> float16 cast is the same IEEE rounding)."""
+    with np.errstate(all="ignore"):
+        return np.ascontiguousarray(np.asarray(x, dtype=F32).astype(np.float16)).view(np.uint16)
+
+
+def quant_hif8_torch_f16(x_bits) -> np.ndarray:
+    """QFuncs/hif8.py:6-23 on an fp16 tensor without ``force_fp32`` (QTensor.py:101-102 not
+    taken): the fp16 branch of :10-11, offset 2^-14, and every op computing in float32 and
+    rounding its result to fp16, as torch's fp16 CPU ops do.  fp16 bits in, fp16 bits out.
+    log2 is evaluated in float64 and rounded straight to fp16 (torch rounds its float32 log2 to
+    fp16; the tests pin that the two agree on every input).  In fp16 the rounded log2 of a value
+    just below a power of two can be that power's exponent, so ``floor`` moves up a binade there
+    (the tests count those inputs); 2^(e - mb) overflows to Inf for e = 16."""
+    x = f16_to_f32(x_bits)
+    rh = lambda v: f16_to_f32(f32_to_f16(v))                            # noqa: E731
+    with np.errstate(all="ignore"):
+        xu = np.abs(x)                                                      # :7
+        sign = (x > 0).astype(F32) - (x < 0).astype(F32)                    # :8
+        t = rh(xu + F32(2.0 ** -14))                                        # :11, the sum in fp16
+        lg = np.log2(t.astype(np.float64)).astype(np.float16).astype(F32)   # log2, one rounding
+        e = np.floor(lg)                                                    # :11
+        abse = np.abs(e)                                                    # :15
+        mant_bits = np.zeros_like(abse)                                     # :16-19
+        mant_bits[abse <= 15] = 1
+        mant_bits[abse <= 7] = 2
+        mant_bits[abse <= 3] = 3
+        p1 = rh(np.power(np.float64(2.0), (-e + mant_bits).astype(np.float64)).astype(F32))  # 2.0**(-e+mb)
+        m = rh(xu * p1)                                                     # :21
+        f = np.floor(rh(m + F32(0.5)))
+        p2 = rh(np.power(np.float64(2.0), (e - mant_bits).astype(np.float64)).astype(F32))   # 2.0**(e-mb)
+        r = rh(f * p2)
+        res = rh(r * sign)
+    return f32_to_f16(res)
+
+
+def quant_dequant_f16(x_bits, semantics: str) -> np.ndarray:
+    """``quant_dequant_float`` on an fp16 tensor (QTensor.py:94-128), fp16 bits in and out:
+    ``"npu"`` -- the NPU table has no fp16 kernel, so the fp32 kernel on x.float() and the result
+    cast back (QTensor.py:66-79, 126-127); ``"torch"`` -- ``force_py=True, force_fp32=True``: the
+    float32 torch function, then the cast back; ``"torch_f16"`` -- ``force_py=True`` alone: the
+    torch function in fp16 arithmetic (``quant_hif8_torch_f16``)."""
+    if semantics == "torch_f16":
+        return quant_hif8_torch_f16(x_bits)
+    return f32_to_f16(quant_hif8(f16_to_f32(x_bits), semantics))
+
+
 def _f64_to_bf16(v) -> np.ndarray:
     """float64 -> bf16 bits, one round-to-nearest-even from the exact value (finite inputs)."""
     v = np.asarray(v, dtype=np.float64)
@@ -384,12 +437,16 @@ def weight_input(seed: int, n: int, k: int, std: float = 0.02):
 
 
 def quant_hif8_torch_cpu(x):
-    """QFuncs/hif8.py:6-23 on a torch CPU float32 tensor (the reference's own op
-    sequence, multi-threaded by torch); pinned to ``quant_hif8_torch`` in the tests."""
+    """QFuncs/hif8.py:6-23 on a torch CPU tensor (the reference's own op sequence, with its
+    fp16 branch, multi-threaded by torch); pinned to ``quant_hif8_torch`` (float32),
+    ``quant_hif8_torch_bf16`` and ``quant_hif8_torch_f16`` in the tests."""
     import torch
     x_unsigned = torch.abs(x)
     sign = torch.sign(x)
-    e = torch.floor(torch.log2(x_unsigned + 2 ** -45))
+    if x.dtype == torch.float16:
+        e = torch.floor(torch.log2(x_unsigned + 2 ** -14))
+    else:
+        e = torch.floor(torch.log2(x_unsigned + 2 ** -45))
     abse = e.abs()
     mant_bits = torch.zeros_like(abse)
     mant_bits[abse <= 15] = 1

@@ -48,6 +48,10 @@ from .hif8_linear import (  # noqa: F401
     linear_fwd_wq_split,
     transpose_bf16,
     wgrad_ok,
+    pad_2d,
+    gemm_f32,
+    dense_linear,
+    dense_mm,
 )
 from .ffn import HIF8FFN  # noqa: F401
 from . import dit  # noqa: F401
@@ -87,4 +91,5 @@ __all__ = [
     "qkv_from_modulated_norm", "modulated_norm_quant_static", "GroupedWeight", "grouped_ok", "linear_fwd_grouped", "grouped_weight",
     "attention_fwd", "attention_fwd_ok", "key_list",
     "dit", "OSPNextAttentionBlock", "OSPNextBlocks", "linear_fwd_wq", "linear_fwd_wq_split", "linear_wgrad", "transpose_bf16", "wgrad_ok",
+    "pad_2d", "gemm_f32", "dense_linear", "dense_mm",
 ]

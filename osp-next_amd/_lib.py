@@ -17,7 +17,7 @@ LIB_PATH = os.path.join(_HERE, "libhif8_mi355x.so")
 HIF8_OK = 0
 ERR_SHAPE = -2    # HIF8_ERR_SHAPE: a shape the entry point does not take
 DTYPE_BF16, DTYPE_F32, DTYPE_BF16_AS_F32 = 0, 1, 2
-SEM_NPU, SEM_TORCH, SEM_TORCH_BF16 = 0, 1, 2
+SEM_NPU, SEM_TORCH, SEM_TORCH_BF16, SEM_TORCH_F16 = 0, 1, 2, 3
 # formats of a quantised activation held by the Python layer: bf16 x_q, or its 8-bit codes
 A_BF16, A_CODES = 0, 1
 
@@ -36,12 +36,15 @@ SIGNATURES = {
     "hif8_decode": (_i, [_p, _i64, _p, _i, _p, _p]),
     "hif8_quant_f32": (_i, [_p, _p, _i64, _i, _p]),
     "hif8_quant_bf16": (_i, [_p, _p, _i64, _i, _p]),
+    "hif8_quant_f16": (_i, [_p, _p, _i64, _i, _p]),
     "hif8_linear_fwd": (_i, [_p, _p, _p, _p, _p, _i64, _i64, _i64, _p]),
     "hif8_transpose_codes": (_i, [_p, _i64, _i64, _p, _p]),
     "hif8_transpose_bf16": (_i, [_p, _i64, _i64, _i64, _p, _p]),
     "hif8_linear_split_workspace_bytes": (_i64, [_i64, _i64, _i64]),
     "hif8_linear_fwd_wq_split": (_i, [_p, _p, _p, _p, _i64, _i64, _i64, _p, _i64, _p]),
     "hif8_linear_wgrad": (_i, [_p, _p, _p, _i64, _i64, _i64, _p, _i64, _p]),
+    "hif8_gemm_f32": (_i, [_p, _i, _p, _i, _p, _i, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p]),
+    "hif8_pad_2d": (_i, [_p, _i64, _i64, _p, _i64, _i64, _i, _p]),
     "hif8_linear_fwd_gelu_stat": (_i, [_p, _p, _p, _p, _p, _i64, _i64, _i64, _f, _p, _p]),
     "hif8_gelu_absmax_scale": (_i, [_p, _i64, _f, _p, _p]),
     "hif8_gelu_fake_quant": (_i, [_p, _i64, _p, _f, _p, _i, _p]),

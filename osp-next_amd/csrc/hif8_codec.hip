@@ -441,6 +441,57 @@ __global__ __launch_bounds__(kTPB) void k_qdq_torch_bf16(const uint16_t *__restr
         y[i] = uint16_t(qdq_torch_bf16(x[i]));
 }
 
+// fp16 <-> fp32: exact widening; narrowing by v_cvt_f16_f32, round-to-nearest-even with fp16
+// subnormals and overflow to Inf (the fp16 denormal mode is on), as c10::Half rounds.
+__device__ __forceinline__ float h2f(uint32_t h) { return float(__builtin_bit_cast(_Float16, uint16_t(h))); }
+__device__ __forceinline__ uint32_t f2h(float f) { return __builtin_bit_cast(uint16_t, _Float16(f)); }
+__device__ __forceinline__ float rh(float f) { return h2f(f2h(f)); }
+
+// QFuncs/hif8.py:6-23 on one fp16 value in fp16 arithmetic (the fp16 branch of :10-11, offset
+// 2^-14): each op computed in fp32 and rounded to fp16, as torch's fp16 ops compute.  The floor
+// of the fp16-rounded log2 is unchanged by a log2 error of 32 float32 ulps on every input, so
+// log2f gives torch's exponent.  2^(e - mb) is Inf for e = 16 (|x| >= 57344 gives Inf).  The
+// final "* sign" sets the sign bit of the non-negative fp16 result r (r * -1 is -r exactly, -0
+// for r = 0): written as a float product narrowed to fp16, it is compiled to an fma_mix with a
+// +0 addend, which turns -0 into +0.
+static __device__ uint32_t qdq_torch_f16(uint32_t xh)
+{
+    const float x = h2f(xh);
+    const float xu = fabsf(x);
+    if (!(xu <= 65504.0f)) return 0x7E00u;                          // NaN, Inf -> NaN
+    const float t = rh(xu + 0x1p-14f);                              // x_unsigned + 2**-14
+    const int e = int(__builtin_floorf(rh(log2f(t))));              // floor(log2(.))
+    const int ae = e < 0 ? -e : e;
+    const int mb = ae <= 3 ? 3 : ae <= 7 ? 2 : ae <= 15 ? 1 : 0;
+    const float m = rh(xu * rh(__builtin_ldexpf(1.0f, mb - e)));     // x_unsigned * 2**(-e + mb)
+    const float f = __builtin_floorf(rh(m + 0.5f));                 // floor(. + 0.5)
+    const uint32_t r = f2h(f * rh(__builtin_ldexpf(1.0f, e - mb))); // * 2**(e - mb), >= 0
+    return x < 0.0f ? (r | 0x8000u) : r;                            // * sign (0 for x = +-0)
+}
+
+// quant_dequant_float of an fp16 tensor (hif8_quant_f16): the fp32 kernels' element routes on
+// x.float() with the result cast back, or the fp16-arithmetic torch route.  Elementwise, off the
+// linear's path.
+__global__ __launch_bounds__(kTPB) void k_qdq_f16(const uint16_t *__restrict__ x, uint16_t *__restrict__ y,
+                                                  int64_t n, int sem)
+{
+    const int64_t stride = int64_t(gridDim.x) * kTPB;
+    for (int64_t i = int64_t(blockIdx.x) * kTPB + threadIdx.x; i < n; i += stride) {
+        const uint32_t h = x[i];
+        uint32_t r;
+        if (sem == HIF8_SEM_TORCH_F16) {
+            r = qdq_torch_f16(h);
+        } else {
+            // the empty asm keeps the fp32 result (and the sign of a zero) apart from the
+            // narrowing, which would otherwise absorb qdq_torch's last product into an fma_mix
+            float q = sem == kSemTorch ? qdq_torch(h2f(h)) : qdq_npu(h2f(h));
+            asm volatile("" : "+v"(q));
+            r = f2h(q);
+        }
+        y[i] = uint16_t(r);
+    }
+}
+
 // Byte-matrix transpose, codes [R][C] -> [C][R]: the packed weight W^T that the fused GEMM
 // reads as its weight operand for dgrad (grad_q @ w_q, hif8_linear.py:97).  64 x 64 tiles
 // through LDS; interior tiles of 16-byte aligned matrices move 16 bytes per lane.
@@ -731,6 +782,16 @@ int hif8_quant_bf16(const uint16_t *x, uint16_t *y, int64_t n, int semantics, hi
         return last_launch();
     }
     return launch_quant(x, HIF8_DTYPE_BF16, n, nullptr, y, 1, semantics, 0, stream);
+}
+
+int hif8_quant_f16(const uint16_t *x, uint16_t *y, int64_t n, int semantics, hif8_stream_t stream)
+{
+    if (!x || !y || n <= 0) return HIF8_ERR_ARG;
+    if (semantics != HIF8_SEM_NPU && semantics != HIF8_SEM_TORCH && semantics != HIF8_SEM_TORCH_F16)
+        return HIF8_ERR_ARG;
+    const int grid = grid_for(n, cu_count() * kQdqWgPerCu);
+    hipLaunchKernelGGL(k_qdq_f16, dim3(grid), dim3(kTPB), 0, (hipStream_t)stream, x, y, n, semantics);
+    return last_launch();
 }
 
 int hif8_gelu_absmax_scale(const uint16_t *y, int64_t n, float scale_max, void *state, hif8_stream_t stream)

@@ -36,6 +36,7 @@ fused route, the kernel reads the list of unmasked key rows).
 from __future__ import annotations
 
 import math
+import weakref
 from typing import List, Optional, Sequence, Tuple
 
 import torch
@@ -464,20 +465,39 @@ def attention_key_masked(q: Tensor, k: Tensor, v: Tensor, key_mask: Optional[Ten
     return torch.cat(outs, 0).to(out_dtype)
 
 
-_KEY_LIST_CACHE: list = [None]   # (mask, its version, (key rows, counts)), replaced as one tuple
+# Key lists of the attention masks, per mask tensor and per version of its contents: mask id ->
+# (weak reference to the mask, {version: (key rows, counts)}).  An entry lives exactly as long as
+# its mask (a finaliser drops it), so a HIP graph that captured an attention over a mask keeps
+# valid key-list memory for as long as the caller keeps that mask, like any other static input of
+# the graph; lists of earlier versions of a mask modified in place stay too.
+_KEY_LISTS: dict = {}
+
+
+def _drop_key_lists(key: int, ref) -> None:
+    ent = _KEY_LISTS.get(key)
+    if ent is not None and ent[0] is ref:
+        del _KEY_LISTS[key]
 
 
 def _cached_key_list(key_mask: Optional[Tensor]) -> Tuple[Optional[Tensor], Optional[Tensor]]:
-    """``key_list(key_mask)``, kept for the last mask seen: every block of a step attends with
-    the same mask tensor.  The entry is one tuple, swapped whole, so concurrent callers never
-    pair one mask with another's list."""
+    """``key_list(key_mask)``, built once per mask tensor (and version): the blocks of a step
+    alternate between a few masks (token and group masks of the Skiparse blocks), and each keeps
+    its own lists."""
     if key_mask is None:
         return None, None
-    hit = _KEY_LIST_CACHE[0]
-    if hit is None or hit[0] is not key_mask or hit[1] != key_mask._version:
-        hit = (key_mask, key_mask._version, key_list(key_mask.bool()))
-        _KEY_LIST_CACHE[0] = hit
-    return hit[2]
+    key = id(key_mask)
+    ent = _KEY_LISTS.get(key)
+    if ent is None or ent[0]() is not key_mask:
+        ref = weakref.ref(key_mask)
+        ent = (ref, {})
+        _KEY_LISTS[key] = ent
+        weakref.finalize(key_mask, _drop_key_lists, key, ref)
+    lists = ent[1]
+    hit = lists.get(key_mask._version)
+    if hit is None:
+        hit = key_list(key_mask.bool())
+        lists[key_mask._version] = hit
+    return hit
 
 
 def _grouped_kv(k: HIF8Linear, v: HIF8Linear, text: Tensor) -> Optional[Tuple[Tensor, Tensor]]:

@@ -144,6 +144,10 @@ def attention_fwd(q: Tensor, k: Tensor, v: Tensor, key_idx: Optional[Tensor] = N
     if key_idx is not None:
         if key_idx.dtype != torch.int32 or key_idx.dim() != 2 or key_idx.shape[0] != B or key_idx.stride(1) != 1:
             raise ValueError("key_idx must be an int32 [batch, keys] tensor with contiguous rows")
+        # the kernel reads key_count[b] entries of row b, clamped only to the row stride: a row
+        # shorter than the keys (a narrow or sliced list) would let a larger count run past it
+        if key_idx.shape[1] != Nkv:
+            raise ValueError(f"key_idx rows must hold one entry per key ({Nkv}), got {key_idx.shape[1]}")
         idx_ptr, idx_bs = key_idx.data_ptr(), key_idx.stride(0)
     scale = 1.0 / math.sqrt(D) if softmax_scale is None else float(softmax_scale)
     st_ptr = o_state.ptr if o_state is not None else 0

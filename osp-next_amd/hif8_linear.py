@@ -14,10 +14,12 @@ bit-identical to the reference's; only the fp32 accumulation order differs.
 Backward (hif8_linear.py:88-111) quantises the incoming gradient with
 ``scale_max_backward`` through the same HIP kernels.  dgrad ``grad_q @ w_q``
 runs on the forward's GEMM against the transposed weight codes, and wgrad
-``grad_q^T @ x_q`` on the decode-free GEMM over the two operands transposed
-(token dimension padded to the k-step), when the operands are bf16 (the
-reference's autocast case); other dtypes use torch matmuls on the same
-dequantised operands.
+``grad_q^T @ x_q`` on the decode-free GEMM reading both operands token-major,
+when the operands are bf16 (the reference's autocast case); an fp32 operand takes
+the library's fp32 GEMM (``hif8_gemm_f32``) on the same dequantised operands.
+Shapes outside the MFMA tiles (in_features % 64, out_features % 8, or the dgrad's
+reduction % 64) run those GEMMs on zero-padded operands (``hif8_pad_2d``).  No
+product runs on a vendor or torch GEMM.
 """
 from __future__ import annotations
 
@@ -66,6 +68,40 @@ class QuantState:
 def _aligned(t: Tensor) -> Tensor:
     """The kernels use 128-bit accesses: realign offset views with one copy."""
     return t if t.data_ptr() % 16 == 0 else t.clone()
+
+
+def _round_up(v: int, m: int) -> int:
+    return (v + m - 1) // m * m
+
+
+def pad_2d(t: Tensor, rows: int, cols: int) -> Tensor:
+    """t [R, C] into a new [rows, cols] tensor with zeros outside t, or cropped where smaller
+    (hif8_pad_2d)."""
+    _lib.require_gpu_tensor(t, "t")
+    if t.dim() != 2:
+        raise ValueError("pad_2d takes a 2-D tensor")
+    R_, C_ = t.shape
+    out = torch.empty((rows, cols), dtype=t.dtype, device=t.device)
+    if R_ == 0 or C_ == 0:
+        return out.zero_()
+    _lib.check(_lib.load().hif8_pad_2d(t.data_ptr(), R_, C_, out.data_ptr(), rows, cols, t.element_size(),
+                                       _lib.stream_ptr(t.device)), "hif8_pad_2d")
+    return out
+
+
+def gemm_f32(a: Tensor, b: Tensor, M: int, N: int, K: int, a_strides, b_strides,
+             out_dtype: torch.dtype = torch.float32) -> Tensor:
+    """c[M, N] = sum_k a[m, k] b[k, n] with fp32 accumulation on bf16 or fp32 operands given by
+    their element strides (m, k) and (k, n) (hif8_gemm_f32): the backward's products of a layer
+    computing in fp32."""
+    if not (a.is_cuda and b.is_cuda):
+        raise ValueError("gemm_f32 takes GPU tensors (the HiF8 path has no CPU route)")
+    c = torch.empty((M, N), dtype=out_dtype, device=a.device)
+    _lib.check(_lib.load().hif8_gemm_f32(a.data_ptr(), _lib.dtype_code(a.dtype), b.data_ptr(),
+                                         _lib.dtype_code(b.dtype), c.data_ptr(), _lib.dtype_code(out_dtype), M, N, K,
+                                         int(a_strides[0]), int(a_strides[1]), int(b_strides[0]), int(b_strides[1]),
+                                         _lib.stream_ptr(a.device)), "hif8_gemm_f32")
+    return c
 
 
 def _dtype_arg(x: Tensor, as_f32: bool) -> int:
@@ -169,6 +205,7 @@ class PackedWeight:
         self.scale_max = float(scale_max)
         self.key = (w.data_ptr(), weight._version, w.device)
         self._codes_t: Optional[Tensor] = None
+        self._padded: dict = {}
 
     def dequantize(self, dtype: Optional[torch.dtype] = None) -> Tensor:
         return decode(self.codes, self.state, dtype or self.src_dtype)
@@ -178,6 +215,27 @@ class PackedWeight:
         if self._codes_t is None:
             self._codes_t = transpose_codes(self.codes)
         return self._codes_t
+
+    def codes_t_padded(self, k_rows: int, n_cols: int) -> Tensor:
+        """The transposed codes zero-padded to [k_rows, n_cols] (built once per shape)."""
+        key = ("t", k_rows, n_cols)
+        if key not in self._padded:
+            self._padded[key] = pad_2d(self.codes_t(), k_rows, n_cols)
+        return self._padded[key]
+
+    def padded(self, n_rows: int, k_cols: int) -> "PackedWeight":
+        """The same weight with its codes zero-padded to [n_rows, k_cols] (zero codes decode to
+        0), sharing the state: the operand of a GEMM over zero-padded shapes (built once)."""
+        key = (n_rows, k_cols)
+        p = self._padded.get(key)
+        if p is None:
+            p = object.__new__(PackedWeight)
+            p.shape = (n_rows, k_cols)
+            p.src_dtype, p.state, p.scale_max, p.key = self.src_dtype, self.state, self.scale_max, self.key
+            p.codes = pad_2d(self.codes, n_rows, k_cols)
+            p._codes_t, p._padded = None, {}
+            self._padded[key] = p
+        return p
 
 
 def transpose_codes(codes: Tensor) -> Tensor:
@@ -191,27 +249,32 @@ def transpose_codes(codes: Tensor) -> Tensor:
 
 
 def dgrad_fused_ok(grad_q: Tensor, w: "PackedWeight") -> bool:
-    """Shapes and dtypes the fused dgrad takes: bf16 gradient and weight, the weight's
-    out dim (the reduction) a multiple of 64 and its in dim a multiple of 8."""
+    """Dtypes the MFMA dgrad takes: bf16 gradient and weight (other shapes than the tiles'
+    are zero-padded by ``linear_dgrad``)."""
     N, K = w.shape
-    return (grad_q.dtype == torch.bfloat16 and w.src_dtype == torch.bfloat16 and N % 64 == 0 and K % 8 == 0
-            and N < (1 << 22))
+    return grad_q.dtype == torch.bfloat16 and w.src_dtype == torch.bfloat16 and _round_up(N, 64) < (1 << 22)
 
 
 def linear_dgrad(grad_q2: Tensor, w: "PackedWeight") -> Tensor:
     """grad_q [M, N] @ w_q [N, K] -> [M, K] bf16 (hif8_linear.py:97): the forward GEMM with the
     transposed weight codes [K, N] as its weight, on the route the forward takes at this M (the
     fused GEMM, or the transposed codes decoded once and the decode-free GEMM with its last
-    partial wave of tiles split over k ranges)."""
+    partial wave of tiles split over k ranges).  The reduction (N) is padded to a multiple of 64
+    and the output features (K) to a multiple of 8 with zeros where they are not."""
     M, N = grad_q2.shape
     K = w.shape[1]
+    Np, Kp = _round_up(N, 64), _round_up(K, 8)
     g = _aligned(grad_q2.contiguous())
+    if Np != N:
+        g = pad_2d(g, M, Np)
+    codes_t = w.codes_t() if (Np, Kp) == (N, K) else w.codes_t_padded(Kp, Np)
     if decode_once(M):
-        return linear_fwd_wq_split(g, decode(w.codes_t(), w.state, torch.bfloat16))
-    y = torch.empty((M, K), dtype=torch.bfloat16, device=g.device)
-    _lib.check(_lib.load().hif8_linear_fwd(g.data_ptr(), w.codes_t().data_ptr(), w.state.ptr, None, y.data_ptr(),
-                                           M, K, N, _lib.stream_ptr(g.device)), "hif8_linear_fwd (dgrad)")
-    return y
+        y = linear_fwd_wq_split(g, decode(codes_t, w.state, torch.bfloat16))
+    else:
+        y = torch.empty((M, Kp), dtype=torch.bfloat16, device=g.device)
+        _lib.check(_lib.load().hif8_linear_fwd(g.data_ptr(), codes_t.data_ptr(), w.state.ptr, None, y.data_ptr(),
+                                               M, Kp, Np, _lib.stream_ptr(g.device)), "hif8_linear_fwd (dgrad)")
+    return y if Kp == K else pad_2d(y, M, K)
 
 
 def transpose_bf16(x2: Tensor, rows_pad: Optional[int] = None) -> Tensor:
@@ -228,8 +291,9 @@ def transpose_bf16(x2: Tensor, rows_pad: Optional[int] = None) -> Tensor:
 
 
 def wgrad_ok(grad_q2: Tensor, x_q2: Tensor) -> bool:
-    """Shapes and dtypes linear_wgrad takes: bf16 operands, in_features a multiple of 8."""
-    return (grad_q2.dtype == torch.bfloat16 and x_q2.dtype == torch.bfloat16 and x_q2.shape[1] % 8 == 0
+    """Operands linear_wgrad takes: bf16, the same tokens (features that are not multiples of 8
+    are zero-padded by linear_wgrad)."""
+    return (grad_q2.dtype == torch.bfloat16 and x_q2.dtype == torch.bfloat16
             and grad_q2.shape[0] == x_q2.shape[0] and grad_q2.shape[0] > 0)
 
 
@@ -242,8 +306,13 @@ def linear_wgrad(grad_q2: Tensor, x_q2: Tensor, split_tail: bool = True, transpo
     row-major GEMM over the padded tokens (the zeros add nothing)."""
     M, N = grad_q2.shape
     K = x_q2.shape[1]
-    g = grad_q2.contiguous()
-    x = x_q2.contiguous()
+    Np, Kp = _round_up(N, 8), _round_up(K, 8)
+    if (Np, Kp) != (N, K):
+        g = pad_2d(grad_q2.contiguous(), M, Np) if Np != N else grad_q2
+        x = pad_2d(x_q2.contiguous(), M, Kp) if Kp != K else x_q2
+        return pad_2d(linear_wgrad(g, x, split_tail, transposed), N, K)
+    g = _aligned(grad_q2.contiguous())
+    x = _aligned(x_q2.contiguous())
     L = _lib.load()
     if not transposed:
         dw = torch.empty((N, K), dtype=torch.bfloat16, device=g.device)
@@ -320,6 +389,49 @@ def linear_fwd_wq(a: Tensor, w_q: Tensor, bias: Optional[Tensor], y_state: Optio
     return y
 
 
+def _autocast_bf16() -> bool:
+    return torch.is_autocast_enabled("cuda") and torch.get_autocast_dtype("cuda") == torch.bfloat16
+
+
+def dense_linear(x2: Tensor, w: Tensor, bias: Optional[Tensor]) -> Tensor:
+    """``F.linear(x2, w, bias)`` for already dequantised operands x2 [M, K], w [N, K] on the
+    library's GEMMs: in bf16 (the autocast case, or bf16 operands) the decode-free MFMA GEMM on
+    zero-padded shapes where needed, output bf16; otherwise the fp32 GEMM in the operands' result
+    dtype."""
+    M, K = x2.shape
+    N = w.shape[0]
+    if _autocast_bf16() or (x2.dtype == torch.bfloat16 and w.dtype == torch.bfloat16):
+        a = _aligned(x2.to(torch.bfloat16).contiguous())
+        wq = _aligned(w.to(torch.bfloat16).contiguous())
+        Np, Kp = _round_up(N, 8), _round_up(K, 64)
+        b = None
+        if bias is not None:
+            b = bias.detach().to(torch.bfloat16).reshape(1, N).contiguous()
+            b = pad_2d(b, 1, Np).view(Np) if Np != N else b.view(N)
+        if Kp != K:
+            a = pad_2d(a, M, Kp)
+        if (Np, Kp) != (N, K):
+            wq = pad_2d(wq, Np, Kp)
+        y = linear_fwd_wq(a, wq, b)
+        return y if Np == N else pad_2d(y, M, N)
+    ct = torch.promote_types(x2.dtype, w.dtype)
+    y = gemm_f32(x2.contiguous(), w.contiguous(), M, N, K, (K, 1), (1, K), out_dtype=ct)
+    return y if bias is None else y + bias.to(ct)
+
+
+def dense_mm(a: Tensor, b: Tensor) -> Tensor:
+    """``a @ b`` for 2-D a [M, R], b [R, N] on the library's GEMMs: in bf16 (autocast or bf16
+    operands) the token-major MFMA GEMM on a^T (one transpose) and b, output bf16; otherwise the
+    fp32 GEMM on the strided operands."""
+    M, R = a.shape
+    N = b.shape[1]
+    if _autocast_bf16() or (a.dtype == torch.bfloat16 and b.dtype == torch.bfloat16):
+        a_t = transpose_bf16(_aligned(a.to(torch.bfloat16).contiguous()))        # [R, M]
+        return linear_wgrad(a_t, _aligned(b.to(torch.bfloat16).contiguous()))   # a_t^T @ b
+    ct = torch.promote_types(a.dtype, b.dtype)
+    return gemm_f32(a, b, M, N, R, (a.stride(0), a.stride(1)), (b.stride(0), b.stride(1)), out_dtype=ct)
+
+
 def fused_shape_ok(N: int, K: int) -> bool:
     """Shapes hif8_linear_fwd takes: in_features K % 64 == 0, out_features N % 8 == 0."""
     return K % 64 == 0 and N % 8 == 0 and K < (1 << 22)
@@ -327,14 +439,24 @@ def fused_shape_ok(N: int, K: int) -> bool:
 
 def linear_any(a: Tensor, a_fmt: int, a_state: Optional[QuantState], w: PackedWeight,
                bias: Optional[Tensor]) -> Tensor:
-    """y = x_q @ w_q^T + bias in bf16 for any shape: the fused GEMM where it applies, else
-    the vendor bf16 GEMM on the same dequantised operands (decoded on the GPU)."""
+    """y = x_q @ w_q^T + bias in bf16 for any shape: the GEMM routes of linear_fwd, on operands
+    zero-padded to in_features % 64 == 0 and out_features % 8 == 0 where the layer's are not (the
+    zeros add nothing to the sums; the output is cropped back)."""
     N, K = w.shape
     if fused_shape_ok(N, K):
         return linear_fwd(a, a_fmt, a_state, w, bias)
+    M = a.shape[0]
+    Np, Kp = _round_up(N, 8), _round_up(K, 64)
+    if not fused_shape_ok(Np, Kp):
+        raise ValueError(f"in_features {K} is beyond the GEMMs' k range")
     xq = a if a_fmt == _lib.A_BF16 else decode(a, a_state, torch.bfloat16)
-    b = bias.detach().to(torch.bfloat16) if bias is not None else None
-    return torch.nn.functional.linear(xq.to(torch.bfloat16), w.dequantize(torch.bfloat16), b)
+    xq = pad_2d(_aligned(xq.contiguous()), M, Kp) if Kp != K else xq
+    bp = None
+    if bias is not None:
+        bp = bias.detach().to(torch.bfloat16).reshape(1, N).contiguous()
+        bp = pad_2d(bp, 1, Np).view(Np) if Np != N else bp.view(N)
+    y = linear_fwd(xq, _lib.A_BF16, None, w.padded(Np, Kp), bp)
+    return y if Np == N else pad_2d(y, M, N)
 
 
 def linear_fwd(a: Tensor, a_fmt: int, a_state: Optional[QuantState], w: PackedWeight,
@@ -542,19 +664,20 @@ class _HIF8LinearFunction(torch.autograd.Function):
         else:
             x_q = ctx.a
         grad_q, _ = _quant(grad_output.contiguous(), ctx.smb)            # :93
-        g_2d = grad_q.reshape(-1, grad_q.shape[-1])
+        g_2d = grad_q.reshape(-1, grad_q.shape[-1]).contiguous()
+        M, N = g_2d.shape
+        K = ctx.packed.shape[1]
         if dgrad_fused_ok(g_2d, ctx.packed):                              # :97, grad_q @ w_q
-            grad_input = linear_dgrad(g_2d, ctx.packed).to(ctx.x_dtype).view(ctx.x_shape)
-        else:
-            w_q = ctx.packed.dequantize(ctx.w_dtype)
-            ct = torch.promote_types(g_2d.dtype, w_q.dtype)
-            grad_input = (g_2d.to(ct) @ w_q.to(ct).contiguous()).to(ctx.x_dtype).view(ctx.x_shape)
-        x_2d = x_q.reshape(-1, x_q.shape[-1])
+            grad_input = linear_dgrad(g_2d, ctx.packed)
+        else:                                                             # fp32: the fp32 GEMM
+            w_q = ctx.packed.dequantize(ctx.w_dtype)                      # [N, K]
+            grad_input = gemm_f32(g_2d, w_q, M, K, N, (N, 1), (K, 1))
+        grad_input = grad_input.to(ctx.x_dtype).view(ctx.x_shape)
+        x_2d = x_q.reshape(-1, x_q.shape[-1]).contiguous()
         if wgrad_ok(g_2d, x_2d):                                            # :104, g^T @ x_q
             grad_weight = linear_wgrad(g_2d, x_2d).to(ctx.w_dtype)
-        else:
-            ctw = torch.promote_types(g_2d.dtype, x_2d.dtype)
-            grad_weight = (g_2d.t().contiguous().to(ctw) @ x_2d.to(ctw)).to(ctx.w_dtype)
+        else:                                                               # g[M, N]^T x[M, K]
+            grad_weight = gemm_f32(g_2d, x_2d, N, K, M, (1, N), (K, 1)).to(ctx.w_dtype)
         grad_bias = g_2d.sum(0).to(ctx.b_dtype) if ctx.has_bias else None                   # :107
         return grad_input, grad_weight, grad_bias, None, None, None, None
 

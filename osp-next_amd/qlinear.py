@@ -23,12 +23,11 @@ from typing import Dict, List, Optional, Union
 
 import torch
 import torch.nn as nn
-import torch.nn.functional as F
 from torch import Tensor
 from torch.autograd import Function
 
 from . import _lib
-from .hif8_linear import HIF8Linear, PackedWeight, QuantState
+from .hif8_linear import HIF8Linear, PackedWeight, QuantState, dense_linear, dense_mm
 from .quant import QType, quant_dequant_float
 
 FORMAT = "hif8-packed-1"
@@ -38,8 +37,21 @@ _DTYPES = {"torch.bfloat16": torch.bfloat16, "torch.float32": torch.float32}
 # ------------------------------------------------------------------ QLinear
 
 
+def _linear(x_q: Tensor, w_q: Tensor, b: Optional[Tensor]) -> Tensor:
+    """F.linear on the library's GEMMs (dense_linear), any leading dims."""
+    y = dense_linear(x_q.reshape(-1, x_q.shape[-1]), w_q, b)
+    return y.view(*x_q.shape[:-1], y.shape[-1])
+
+
+def _mm(a: Tensor, b: Tensor) -> Tensor:
+    """a @ b for a [..., R] (flattened to 2-D) and b [R, N] on the library's GEMMs (dense_mm)."""
+    y = dense_mm(a.reshape(-1, a.shape[-1]), b)
+    return y.view(*a.shape[:-1], y.shape[-1])
+
+
 class LinearForward(Function):
-    """QLinear.py:13-43: saves x and w, re-quantises both in backward."""
+    """QLinear.py:13-43: saves x and w, re-quantises both in backward.  The products run on the
+    library's GEMMs (dense_linear, dense_mm) in the dtype autocast gives them."""
 
     @staticmethod
     @torch.amp.custom_fwd(device_type="cuda")
@@ -49,7 +61,7 @@ class LinearForward(Function):
         ctx.save_for_backward(x, w)
         ctx.qp, ctx.qp_in, ctx.quant_grad = qp, qp_in, quant_grad
         ctx.has_bias = b is not None
-        return F.linear(x_q, w_q, b)
+        return _linear(x_q, w_q, b)
 
     @staticmethod
     @torch.amp.custom_bwd(device_type="cuda")
@@ -62,14 +74,14 @@ class LinearForward(Function):
             g_t = quant_dequant_float(grad_out.flatten(0, -2).transpose(-1, -2).contiguous(), ctx.qp_in, force_fp32=True)
         else:
             g_q, g_t = grad_out, grad_out.flatten(0, -2).transpose(-1, -2)
-        grad_in = g_q @ w_q
-        grad_w = g_t @ x_q.flatten(0, -2)
+        grad_in = _mm(g_q, w_q)
+        grad_w = _mm(g_t, x_q.flatten(0, -2))
         grad_b = grad_out.flatten(0, -2).sum(0) if ctx.has_bias else None
         return grad_in, grad_w, grad_b, None, None, None
 
 
 class LinearForwardFast(Function):
-    """QLinear.py:46-70: saves the quantised x_q and w_q instead."""
+    """QLinear.py:46-70: saves the quantised x_q and w_q instead (products as LinearForward)."""
 
     @staticmethod
     @torch.amp.custom_fwd(device_type="cuda")
@@ -79,15 +91,15 @@ class LinearForwardFast(Function):
         ctx.save_for_backward(x_q, w_q)
         ctx.qp_in, ctx.quant_grad = qp_in, quant_grad
         ctx.has_bias = b is not None
-        return F.linear(x_q, w_q, b)
+        return _linear(x_q, w_q, b)
 
     @staticmethod
     @torch.amp.custom_bwd(device_type="cuda")
     def backward(ctx, grad_out):
         x_q, w_q = ctx.saved_tensors
         g_q = quant_dequant_float(grad_out, ctx.qp_in, force_fp32=True) if ctx.quant_grad else grad_out
-        grad_in = g_q @ w_q
-        grad_w = g_q.flatten(0, -2).transpose(-1, -2) @ x_q.flatten(0, -2)
+        grad_in = _mm(g_q, w_q)
+        grad_w = _mm(g_q.flatten(0, -2).transpose(-1, -2), x_q.flatten(0, -2))
         grad_b = grad_out.flatten(0, -2).sum(0) if ctx.has_bias else None
         return grad_in, grad_w, grad_b, None, None, None
 

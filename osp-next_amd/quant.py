@@ -78,7 +78,13 @@ def _qdq_inplace(x: Tensor, y: Tensor, semantics: int) -> None:
         return
     L = _lib.load()
     s = _lib.stream_ptr(x.device)
-    if x.dtype == torch.bfloat16:
+    if x.dtype == torch.float16:
+        if semantics == _lib.SEM_TORCH_BF16:
+            raise ValueError("the bf16-arithmetic torch route takes a bfloat16 tensor")
+        _lib.check(L.hif8_quant_f16(x.data_ptr(), y.data_ptr(), n, semantics, s), "hif8_quant_f16")
+    elif semantics == _lib.SEM_TORCH_F16:
+        raise ValueError("the fp16-arithmetic torch route takes a float16 tensor")
+    elif x.dtype == torch.bfloat16:
         _lib.check(L.hif8_quant_bf16(x.data_ptr(), y.data_ptr(), n, semantics, s), "hif8_quant_bf16")
     elif semantics == _lib.SEM_TORCH_BF16:
         raise ValueError("the bf16-arithmetic torch route takes a bfloat16 tensor")
@@ -111,10 +117,11 @@ def quant_dequant_float(x: Tensor, Q: QType, force_py: bool = False, force_fp32:
     torch function ``quant_hif8`` (``QFuncs/hif8.py:6-23``).  The output has the
     input's dtype (QTensor.py:126-127).  The torch function runs in the tensor's
     own precision unless ``force_fp32`` (QTensor.py:101-102): on a bf16 tensor every
-    op then rounds to bf16 (HIF8_SEM_TORCH_BF16).  The NPU kernel computes in fp32
-    for bf16 and fp32 alike; fp16 and other dtypes go through fp32 like
-    QTensor.py:72-79.  The fp16-precision torch route (force_py=True on an fp16
-    tensor without force_fp32, with its 2^-14 offset) is not implemented and raises.
+    op then rounds to bf16 (HIF8_SEM_TORCH_BF16), on an fp16 tensor to fp16 with the
+    fp16 offset 2^-14 of QFuncs/hif8.py:10-11 (HIF8_SEM_TORCH_F16).  The NPU kernel
+    computes in fp32 for bf16 and fp32 alike; an fp16 tensor takes the fp32 kernel on
+    its fp32 values and is cast back (QTensor.py:72-79), in one pass of
+    ``hif8_quant_f16``; other dtypes go through fp32.
     """
     if Q.desc in ("fp16", "bf16", "fp32"):
         return x
@@ -125,11 +132,10 @@ def quant_dequant_float(x: Tensor, Q: QType, force_py: bool = False, force_fp32:
         if x.dtype == torch.bfloat16:
             semantics = _lib.SEM_TORCH_BF16
         elif x.dtype == torch.float16:
-            raise NotImplementedError("the fp16-precision torch route (force_py=True, force_fp32=False on an "
-                                      "fp16 tensor) is not implemented; pass force_fp32=True")
+            semantics = _lib.SEM_TORCH_F16
     dtype_ori = x.dtype
     xc = x.contiguous()
-    if xc.dtype not in (torch.bfloat16, torch.float32):
+    if xc.dtype not in (torch.bfloat16, torch.float32, torch.float16):
         xc = xc.to(torch.float32)
     out = torch.empty_like(xc)
     _qdq_inplace(xc, out, semantics)

@@ -274,3 +274,30 @@ def test_block_check_rejects_planted_mistakes(dit, name):
     want = mod.block(sd, x, e, text, grid, kind, f2s, s2f, num_heads=2, linear="exact")
     nw, mx = block_errors(got, want, out_layout(kind, f2s, s2f, x, grid))
     assert not (nw < TOL_EXACT[0] and mx < TOL_EXACT[1]), (name, nw, mx)
+
+
+def test_key_list_cache_is_per_mask(dit):
+    """The attention's key lists are kept per mask tensor and version: masks used in turn (the
+    token and group masks of alternating Skiparse blocks) keep their own lists, the lists of a mask
+    stay while it lives (a captured graph reads their addresses), a mask modified in place gets new
+    lists without dropping the old ones, and a mask's entry goes when the mask does."""
+    import gc
+    a = torch.tensor([[True, False, True, True], [True, True, False, False]])
+    b = torch.tensor([[False, True, True, True], [True, False, True, False]])
+    la = dit._cached_key_list(a)
+    lb = dit._cached_key_list(b)
+    assert dit._cached_key_list(a)[0] is la[0] and dit._cached_key_list(b)[1] is lb[1]
+    assert la[1].tolist() == [3, 2] and la[0][0, :3].tolist() == [0, 2, 3] and la[0][1, :2].tolist() == [0, 1]
+    a_copy = a.clone()
+    assert dit._cached_key_list(a_copy)[0] is not la[0]
+    assert dit._cached_key_list(a)[0] is la[0]                 # the copy did not evict a's lists
+    a[0, 1] = True                                             # in place: a new version
+    la2 = dit._cached_key_list(a)
+    assert la2[0] is not la[0] and la2[1].tolist() == [4, 2]
+    ent = dit._KEY_LISTS[id(a)][1]
+    assert len(ent) == 2 and any(v[0] is la[0] for v in ent.values())
+    n = len(dit._KEY_LISTS)
+    del a, a_copy
+    gc.collect()
+    assert len(dit._KEY_LISTS) == n - 2
+    assert dit._cached_key_list(None) == (None, None)

@@ -85,8 +85,34 @@ def test_torch_bf16_route_every_bf16(pkg, R, golden):
     assert np.array_equal(host_bits(y), got)
     yt = pkg.quant_dequant_float(x, pkg.QType("hif8"), force_py=True, force_fp32=True)
     assert np.array_equal(host_bits(yt), golden["ex"]["torch_qdq"])
-    with pytest.raises(NotImplementedError):
-        pkg.quant_dequant_float(x.half(), pkg.QType("hif8"), force_py=True)
+
+
+def test_f16_routes_every_f16(pkg, R):
+    """quant_dequant_float of an fp16 tensor (hif8_quant_f16), every fp16 input bit for bit against
+    the oracle in its three routes: the NPU kernel on x.float() cast back (force_py=False), the fp32
+    torch function cast back (force_py with force_fp32), and the torch function in fp16 arithmetic
+    with the 2^-14 offset (force_py alone; the oracle's restatement is pinned to torch's fp16 CPU
+    ops).  NaN outputs are compared as NaN."""
+    allh = ALL_BF16
+    x = torch.from_numpy(allh.view(np.int16)).view(torch.float16).to(DEV)
+    Q = pkg.QType("hif8")
+    for kw, sem in (({}, "npu"), ({"force_py": True, "force_fp32": True}, "torch"),
+                    ({"force_py": True}, "torch_f16")):
+        y = pkg.quant_dequant_float(x, Q, **kw)
+        assert y.dtype == torch.float16
+        got = y.view(torch.int16).cpu().numpy().view(np.uint16)
+        want = R.quant_dequant_f16(allh, sem)
+        nan_g, nan_w = (got & 0x7FFF) > 0x7C00, (want & 0x7FFF) > 0x7C00
+        assert np.array_equal(nan_g, nan_w), sem
+        bad = np.nonzero(got[~nan_g] != want[~nan_w])[0]
+        assert bad.size == 0, (sem, [hex(v) for v in allh[~nan_g][bad[:8]]])
+    # odd offsets and lengths take the same elementwise route
+    xs = x[3:3 + 1001]
+    got = pkg.quant_dequant_float(xs, Q, force_py=True).view(torch.int16).cpu().numpy().view(np.uint16)
+    assert np.array_equal(got, R.quant_dequant_f16(allh[3:3 + 1001], "torch_f16"))
+    with pytest.raises(ValueError):
+        y = torch.empty_like(x)
+        pkg.quant._qdq_inplace(x, y, pkg._lib.SEM_TORCH_BF16)
 
 
 def test_codes_every_bf16_unit_scale(pkg, golden):

@@ -125,3 +125,38 @@ def test_dit_block_fused_route_replays(pkg):
         ref = blk(x, tm, tm, e, grid, grid, rope, text, fused=True).clone()
         graph, out = capture(lambda: blk(x, tm, tm, e, grid, grid, rope, text, fused=True))
         replay_and_check(graph, out, ref, lambda: blk(x2, tm, tm, e, grid, grid, rope, text, fused=True))
+
+
+def test_dit_block_replays_with_other_masks_between(pkg):
+    """The block's captured graph holds the device addresses of its mask's key lists.  Eager calls
+    on other mask objects between the replays -- a copy of the mask, and a mask with more padding --
+    must not free or replace those lists: each replay still equals the eager result (the key lists
+    are kept per mask tensor, for as long as the mask lives)."""
+    print("[graph] DiT block, other masks between replays", flush=True)
+    from ospnext_amd import dit as D
+    from test_dit_cpu import block_inputs, make_block
+    blk = make_block(D, "token", True, False, quant="hif8", device=DEV)
+    for m in blk.modules():
+        if isinstance(m, pkg.HIF8Linear):
+            m.prepack()
+    grid = (2, 5, 8)
+    x, e, text = (t.to(DEV) for t in block_inputs(grid))
+    rope = D.SkiparseRopeWrapper(D.rope_freqs(128).to(DEV))
+    tm, _ = D.skiparse_masks(1, grid, 2, DEV)
+    other = tm.clone()
+    other[:, -7:] = False
+    with torch.no_grad():
+        ref = blk(x, tm, tm, e, grid, grid, rope, text, fused=True).clone()
+        ref_other = blk(x, other, other, e, grid, grid, rope, text, fused=True).clone()
+        assert not torch.equal(bits(ref), bits(ref_other))
+        graph, out = capture(lambda: blk(x, tm, tm, e, grid, grid, rope, text, fused=True))
+        for rep in range(3):
+            copy = tm.clone()                      # a new mask object, new lists
+            y1 = blk(x, copy, copy, e, grid, grid, rope, text, fused=True)
+            y2 = blk(x, other, other, e, grid, grid, rope, text, fused=True)
+            del copy
+            torch.cuda.synchronize()
+            assert torch.equal(bits(y1), bits(ref)) and torch.equal(bits(y2), bits(ref_other))
+            graph.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(bits(out), bits(ref)), f"replay {rep}"

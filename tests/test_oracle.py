@@ -228,6 +228,51 @@ def test_torch_bf16_log2_is_far_from_bf16_boundaries(R):
     assert margin.min() >= 10.0, margin.min()
 
 
+def test_torch_f16_route_matches_torch_every_f16(R):
+    """quant_dequant_float(fp16, force_py=True, force_fp32=False) runs QFuncs/hif8.py on the fp16
+    tensor itself, with the fp16 offset 2^-14 (:10-11): the reference's expression on torch's CPU
+    fp16 kernels against the oracle's fp16 restatement, every fp16 input bit for bit (NaN
+    wherever torch gives NaN: the NaN and Inf inputs)."""
+    torch = pytest.importorskip("torch")
+    allh = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    x = torch.from_numpy(allh.view(np.int16)).view(torch.float16)
+    got = R.quant_hif8_torch_cpu(x).view(torch.int16).numpy().view(np.uint16)
+    want = R.quant_hif8_torch_f16(allh)
+    nan_g, nan_w = (got & 0x7FFF) > 0x7C00, (want & 0x7FFF) > 0x7C00
+    assert np.array_equal(nan_g, nan_w) and nan_w.sum() == 2048
+    assert np.array_equal(got[~nan_g], want[~nan_w])
+    xf = R.f16_to_f32(allh)
+    fin = np.isfinite(xf)
+    # against the fp32 route (force_fp32=True, then the cast back): the 2^-14 offset moves the
+    # exponent of every |x| < 2^-11 it changes, 2834 inputs; from 57344 up both give Inf
+    f32 = R.quant_dequant_f16(allh, "torch")
+    d = np.nonzero((want != f32) & fin)[0]
+    assert d.size == 2834 and np.abs(xf[d]).max() < 2.0 ** -11
+    big = fin & (np.abs(xf) >= 57344.0)
+    assert np.all((want[big] & 0x7FFF) == 0x7C00) and np.all((f32[big] & 0x7FFF) == 0x7C00)
+    # known answers of the fp16 grid: ties away from zero, 3/2/1 mantissa bits by |e|
+    def q(v):
+        return float(R.f16_to_f32(R.quant_hif8_torch_f16(R.f32_to_f16(np.array([v], np.float32))))[0])
+    assert q(1.0625) == 1.125 and q(15.75) == 16.0 and q(-0.3) == -0.3125 and q(1000.0) == 1024.0
+    assert q(0.0) == 0.0 and q(2.0 ** -14) == 2.0 ** -14
+
+
+def test_torch_f16_log2_floor_is_stable(R):
+    """The fp16 route floors log2(fp16(|x| + 2^-14)) rounded to fp16.  For every fp16 |x| that
+    floor is unchanged when log2 is off by up to 32 float32 ulps either way, so torch's float32
+    log2 on the CPU and log2f on the GPU give the same exponent.  The rounding to fp16 itself
+    moves the floor up a binade on 89 inputs (values just below a power of two), which the
+    restatement keeps."""
+    xu = R.f16_to_f32(np.arange(0x7C00, dtype=np.uint16))        # every non-negative finite fp16
+    t = R.f16_to_f32(R.f32_to_f16(xu + np.float32(2.0 ** -14))).astype(np.float64)
+    lg = np.log2(t)
+    e0 = np.floor(lg.astype(np.float16).astype(np.float64))
+    for s in (-1.0, 1.0):
+        lp = lg * (1.0 + s * 32 * 2.0 ** -24)
+        assert np.array_equal(np.floor(lp.astype(np.float16).astype(np.float64)), e0)
+    assert int(np.sum(e0 != np.floor(lg))) == 89
+
+
 # ---------------------------------------------------------- invariants
 
 
