@@ -24,6 +24,7 @@
 namespace hif8 {
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 // ---------------------------------------------------------------- kernels
 
@@ -172,13 +173,41 @@ __device__ __forceinline__ void scalar_elem(const void *xv, void *outv, int64_t 
 // DT kBF16F32 loads bf16 and computes as kF32 on the exact fp32 values.  GELU (kBF16, MODE 1):
 // each element is first replaced by its GELU, rounded to bf16 (the FFN's GELU layer, applied in
 // the down-projection's quantisation instead of in a pass of its own).
+// span > 0: workgroup b quantises the span * 256 consecutive 16-element groups from
+// b * span * 256 on (the grid covers the tensor once, in dispatch order, so the groups in flight
+// at any time lie in one moving window of memory); span 0: a grid-stride loop.
 template <int DT, int MODE, bool GELU = false>
 __global__ __launch_bounds__(kTPB) void k_quant(const void *__restrict__ xv, int64_t n,
                                                  const State *__restrict__ st, void *__restrict__ outv,
-                                                 int sem, int use_state)
+                                                 int sem, int use_state, int span)
 {
     __shared__ __attribute__((aligned(16))) uint8_t lds[kLdsBytes];
     const int tid = threadIdx.x;
+    const int64_t ngrp = n >> 4;  // 16 elements per step
+    const int64_t stride = int64_t(gridDim.x) * kTPB;
+    // This workgroup's iterations: base G0 (a multiple of 256 groups) from i0 in steps of istep
+    // while G0 < iend.  In the quantise modes thread tid's input chunk j (16 bytes) of an iteration
+    // is chunk G0 * kVec + j * 256 + tid of the tensor, so every load and store instruction of a
+    // wave covers one contiguous span (the operation is elementwise: which 16 elements a thread
+    // holds does not matter); chunks past the last whole group are masked.  The decode mode keeps
+    // one 16-code group per thread (g = G0 + tid).
+    const int64_t i0 = span ? int64_t(blockIdx.x) * span * kTPB : int64_t(blockIdx.x) * kTPB;
+    const int64_t istep = span ? int64_t(kTPB) : stride;
+    const int64_t iend = span ? (i0 + int64_t(span) * kTPB < ngrp ? i0 + int64_t(span) * kTPB : ngrp) : ngrp;
+    constexpr int kVec = DT == kF32 ? 4 : 2;      // 16-byte input chunks per 16 elements
+    constexpr int kIpc = 16 / kVec;              // elements per input chunk
+    const int64_t nchunk = ngrp * kVec;
+    const u32x4 *xq = (const u32x4 *)xv;
+    // the first iteration's input is requested before the tables are set up, so its latency
+    // overlaps the table loads and the barrier
+    u32x4 pre[4] = {};
+    if (MODE != 2 && i0 < iend) {
+#pragma unroll
+        for (int j = 0; j < kVec; ++j) {
+            const int64_t c = i0 * kVec + j * kTPB + tid;
+            if (c < nchunk) pre[j] = ld_stream(&xq[c]);
+        }
+    }
     float s = use_state ? st->scale : 1.0f;
     bool fast = use_state ? (st->fast != 0) : true;
     // NaN inputs map to the +Inf entry of the table; unless an amax pass proved
@@ -202,14 +231,11 @@ __global__ __launch_bounds__(kTPB) void k_quant(const void *__restrict__ xv, int
     const uint16_t *lut16 = (const uint16_t *)(lds + kLdsLutBf16);
     const float *lut32 = (const float *)(lds + kLdsLutF32);
 
-    const int64_t ngrp = n >> 4;  // 16 elements per step
-    const int64_t stride = int64_t(gridDim.x) * kTPB;
-    int64_t g = int64_t(blockIdx.x) * kTPB + tid;
-
     if (MODE == 2) {
         // decode: 16 codes -> 16 outputs
         const uint4 *cq = (const uint4 *)xv;
-        for (; g < ngrp; g += stride) {
+        for (int64_t g = i0 + tid; g - tid < iend; g += istep) {
+            if (g >= ngrp) break;
             uint4 c = cq[g];
             uint32_t cw[4] = {c.x, c.y, c.z, c.w};
             if (DT == kBF16) {
@@ -220,9 +246,9 @@ __global__ __launch_bounds__(kTPB) void k_quant(const void *__restrict__ xv, int
                     o[2 * j] = uint32_t(lut16[d & 0xFF]) | (uint32_t(lut16[(d >> 8) & 0xFF]) << 16);
                     o[2 * j + 1] = uint32_t(lut16[(d >> 16) & 0xFF]) | (uint32_t(lut16[d >> 24]) << 16);
                 }
-                uint4 *out = (uint4 *)outv;
-                out[2 * g] = make_uint4(o[0], o[1], o[2], o[3]);
-                out[2 * g + 1] = make_uint4(o[4], o[5], o[6], o[7]);
+                u32x4 *out = (u32x4 *)outv;
+                st_stream(&out[2 * g], u32x4{o[0], o[1], o[2], o[3]});
+                st_stream(&out[2 * g + 1], u32x4{o[4], o[5], o[6], o[7]});
             } else {
                 uint4 *out = (uint4 *)outv;
 #pragma unroll
@@ -241,25 +267,20 @@ __global__ __launch_bounds__(kTPB) void k_quant(const void *__restrict__ xv, int
         return;
     }
 
-    constexpr int kVec = DT == kF32 ? 4 : 2;      // 16-byte loads per 16 elements
     const bool out16 = DT == kBF16 || MODE == 3;  // bf16 output (MODE 1/3)
     if (fast) {
-        // the next group's input is loaded one iteration ahead (two groups in flight)
-        u32x4 pre[4] = {};
-        if (g < ngrp) {
-            const u32x4 *xq = (const u32x4 *)xv;
-#pragma unroll
-            for (int j = 0; j < kVec; ++j) pre[j] = ld_stream(&xq[kVec * g + j]);
-        }
-        for (; g < ngrp; g += stride) {
+        // the next iteration's input is loaded one iteration ahead (two in flight)
+        for (int64_t G0 = i0; G0 < iend; G0 += istep) {
             uint32_t codes[4];
             uint32_t wide[16];   // per element: magnitude bits of xs, and the full bits for fp32
             uint32_t xs_full[16];
             u32x4 cur[4] = {pre[0], pre[1], pre[2], pre[3]};
-            if (g + stride < ngrp) {
-                const u32x4 *xq = (const u32x4 *)xv;
+            if (G0 + istep < iend) {
 #pragma unroll
-                for (int j = 0; j < kVec; ++j) pre[j] = ld_stream(&xq[kVec * (g + stride) + j]);
+                for (int j = 0; j < kVec; ++j) {
+                    const int64_t c = (G0 + istep) * kVec + j * kTPB + tid;
+                    pre[j] = c < nchunk ? ld_stream(&xq[c]) : u32x4{0u, 0u, 0u, 0u};
+                }
             }
             if (DT == kBF16F32) {
                 // the 16 bf16 values as the fp32 words x.float() holds
@@ -321,7 +342,14 @@ __global__ __launch_bounds__(kTPB) void k_quant(const void *__restrict__ xv, int
                 }
             }
             if (MODE == 0) {
-                st_stream(&((u32x4 *)outv)[g], u32x4{codes[0], codes[1], codes[2], codes[3]});
+                // chunk j's kIpc codes are bytes j * kIpc .. of codes[]
+#pragma unroll
+                for (int j = 0; j < kVec; ++j) {
+                    const int64_t c = G0 * kVec + j * kTPB + tid;
+                    if (c >= nchunk) continue;
+                    if (kIpc == 8) st_stream(&((u32x2 *)outv)[c], u32x2{codes[2 * j], codes[2 * j + 1]});
+                    else st_stream(&((uint32_t *)outv)[c], codes[j]);
+                }
                 continue;
             }
             // qdq output through the decode table
@@ -350,19 +378,30 @@ __global__ __launch_bounds__(kTPB) void k_quant(const void *__restrict__ xv, int
                     }
                 }
             }
-            if (out16) {
-                u32x4 *out = (u32x4 *)outv;
-                out[2 * g] = u32x4{y[0] | (y[1] << 16), y[2] | (y[3] << 16), y[4] | (y[5] << 16), y[6] | (y[7] << 16)};
-                out[2 * g + 1] = u32x4{y[8] | (y[9] << 16), y[10] | (y[11] << 16), y[12] | (y[13] << 16), y[14] | (y[15] << 16)};
-            } else {
-                u32x4 *out = (u32x4 *)outv;
+            // chunk j's outputs are y[j * kIpc ..], at chunk c of the output's own element size
 #pragma unroll
-                for (int j = 0; j < 4; ++j) out[4 * g + j] = u32x4{y[4 * j], y[4 * j + 1], y[4 * j + 2], y[4 * j + 3]};
+            for (int j = 0; j < kVec; ++j) {
+                const int64_t c = G0 * kVec + j * kTPB + tid;
+                if (c >= nchunk) continue;
+                const uint32_t *yj = y + j * kIpc;
+                if (out16 && kIpc == 8) {
+                    st_stream(&((u32x4 *)outv)[c], u32x4{yj[0] | (yj[1] << 16), yj[2] | (yj[3] << 16),
+                                                         yj[4] | (yj[5] << 16), yj[6] | (yj[7] << 16)});
+                } else if (out16) {
+                    st_stream(&((u32x2 *)outv)[c], u32x2{yj[0] | (yj[1] << 16), yj[2] | (yj[3] << 16)});
+                } else if (kIpc == 4) {
+                    st_stream(&((u32x4 *)outv)[c], u32x4{yj[0], yj[1], yj[2], yj[3]});
+                } else {
+                    st_stream(&((u32x4 *)outv)[2 * c], u32x4{yj[0], yj[1], yj[2], yj[3]});
+                    st_stream(&((u32x4 *)outv)[2 * c + 1], u32x4{yj[4], yj[5], yj[6], yj[7]});
+                }
             }
         }
     } else {
-        // degenerate scale (amax Inf/NaN, scale 0/Inf/NaN): element-wise reference route
-        for (int64_t j = g; j < (ngrp << 4); j += stride) scalar_elem<DT, MODE, GELU>(xv, outv, j, s, sem);
+        // degenerate scale (amax Inf/NaN, scale 0/Inf/NaN): element-wise reference route, a
+        // grid-stride loop over the elements (each visited once whatever the grid)
+        for (int64_t j = int64_t(blockIdx.x) * kTPB + tid; j < (ngrp << 4); j += stride)
+            scalar_elem<DT, MODE, GELU>(xv, outv, j, s, sem);
     }
     // tail (n % 16) through the scalar route
     for (int64_t j = (ngrp << 4) + int64_t(blockIdx.x) * kTPB + tid; j < n; j += stride)
@@ -591,6 +630,14 @@ __global__ __launch_bounds__(kTPB) void k_transpose_bf16(const uint16_t *__restr
 
 // Workgroups per CU (measured on the 14B activation): amax streams best with one
 // (4 waves per CU, 8 x 16 B loads in flight per lane); encode with 4, qdq with 8.
+// k_quant's span (groups of 16 elements per thread, per workgroup): a one-pass grid of spans in
+// dispatch order streams at copy speed, where a grid-stride loop over the whole tensor spreads
+// the workgroups' accesses over it (copy probe, 774 MB in + out: 6.2-6.5 TB/s against 4.4-5.3
+// at 4-8 workgroups per CU).  0 selects the grid-stride loop everywhere.
+#ifndef HIF8_QUANT_SPAN
+#define HIF8_QUANT_SPAN 4
+#endif
+constexpr int kQuantSpan = HIF8_QUANT_SPAN;
 constexpr int kAmaxWgPerCu = 1;
 constexpr int kEncodeWgPerCu = 4;
 constexpr int kQdqWgPerCu = 8;
@@ -649,9 +696,18 @@ template <int DT, int MODE, bool GELU = false>
 static void launch_k_quant(const void *x, int64_t n, const State *st, void *out, int sem, int use_state, int wg_per_cu,
                            hipStream_t s)
 {
-    const int fit = resident_wgs<DT, MODE, GELU>();
-    const int grid = grid_for((n + 15) / 16, cu_count() * (wg_per_cu < fit ? wg_per_cu : fit));
-    hipLaunchKernelGGL((k_quant<DT, MODE, GELU>), dim3(grid), dim3(kTPB), 0, s, x, n, st, out, sem, use_state);
+    const int64_t ngrp = (n + 15) / 16;
+    int grid, span = 0;
+    if (kQuantSpan > 0 && ngrp >= int64_t(kQuantSpan) * kTPB * cu_count()) {
+        // one pass of spans over the tensor (at least a workgroup per CU)
+        const int64_t blocks = (ngrp + int64_t(kQuantSpan) * kTPB - 1) / (int64_t(kQuantSpan) * kTPB);
+        grid = int(blocks);
+        span = kQuantSpan;
+    } else {
+        const int fit = resident_wgs<DT, MODE, GELU>();
+        grid = grid_for(ngrp, cu_count() * (wg_per_cu < fit ? wg_per_cu : fit));
+    }
+    hipLaunchKernelGGL((k_quant<DT, MODE, GELU>), dim3(grid), dim3(kTPB), 0, s, x, n, st, out, sem, use_state, span);
 }
 
 extern "C" {

@@ -29,16 +29,39 @@ __device__ __forceinline__ uint32_t f2bf_pk(float lo, float hi)
     return __builtin_bit_cast(uint32_t, r);
 }
 
-// QFuncs/hif8.py:6-23 on one fp32 value, with the same fp32 operations.
-// floor(log2(v)) of the normal value v = |x| + 2^-45 is taken from its exponent
-// field; torch's log2 agrees with it wherever the result can differ.
+// floor of the float32 log2 of a normal float v, as torch takes it (torch.floor(torch.log2(v))):
+// the exponent field E, except that log2(v) of the last few v below 2^(E+1) rounds up to the
+// integer k = E + 1.  v = 2^k (1 - j 2^-24) has log2 k - delta, delta = -log2(1 - j 2^-24), and
+// rounds to k when delta is below half the float32 spacing there, 2^(b-24) with 2^b the binade of
+// |k - delta|: for j < 2^b ln 2, i.e. j <= c(b) = ceil(2^b ln 2) - 1 = 0, 1, 2, 5, 11, 22, 44, 88
+// for b = 0 .. 7.  (numpy's and torch's float32 log2 round the same way on the 256 floats below
+// every power of two in [2^-50, 2^19].)  It matters when v = |x| + 2^-45 lies a few units below
+// 2^-44 or 2^-43: there x is half of v or less, and the two floors round x differently.
+__device__ __forceinline__ int floor_log2_f32(float v)
+{
+    const uint32_t vb = f2u(v);
+    const int E = int((vb >> 23) & 0xFF) - 127;
+    const int k = E + 1;
+    const uint32_t ak = uint32_t(k < 0 ? -k : k);
+    // b = floor(log2 |k - delta|): for k > 0 that of k - 1 (k - delta lies below k), for k < 0 that
+    // of |k| (|k - delta| lies above |k|); no round-up for |k - delta| < 2 (c = 0)
+    const uint32_t m = k > 0 ? ak - 1u : ak;
+    if (m < 2u) return E;
+    const int b = 31 - __builtin_clz(m);
+    constexpr uint8_t kC[8] = {0, 1, 2, 5, 11, 22, 44, 88};
+    const uint32_t below = 0x7FFFFFu - (vb & 0x7FFFFFu);      // j - 1 for v = 2^k (1 - j 2^-24)
+    return below < kC[b] ? k : E;
+}
+
+// QFuncs/hif8.py:6-23 on one fp32 value, with the same fp32 operations; floor(log2(v)) of the
+// normal value v = |x| + 2^-45 as torch's float32 log2 gives it (floor_log2_f32).
 static __device__ float qdq_torch(float x)
 {
     float xu = fabsf(x);
     float sign = float(x > 0.0f) - float(x < 0.0f);
     if (!(xu <= 3.402823466e38f)) return __builtin_nanf("");   // NaN, Inf -> NaN
     float v = xu + 0x1p-45f;
-    int e = int((f2u(v) >> 23) & 0xFF) - 127;
+    int e = floor_log2_f32(v);
     int ae = e < 0 ? -e : e;
     int mb = ae <= 3 ? 3 : ae <= 7 ? 2 : ae <= 15 ? 1 : 0;
     float t = xu * __builtin_ldexpf(1.0f, mb - e);

@@ -87,6 +87,23 @@ def test_torch_bf16_route_every_bf16(pkg, R, golden):
     assert np.array_equal(host_bits(yt), golden["ex"]["torch_qdq"])
 
 
+def test_fp32_torch_route_log2_bands(pkg, R):
+    """The fp32 torch route (HIF8_SEM_TORCH) on every float32 x whose |x| + 2^-45 lies within 64
+    units below a power of two 2^k (k in [-47, 40]): the device floors log2 the way torch's
+    float32 log2 rounds (up to k for the last few floats below 2^k), bit for bit against the
+    oracle, which tests/test_oracle.py pins to torch's CPU ops on the same values."""
+    from test_oracle import fp32_log2_band_inputs
+    x = fp32_log2_band_inputs()
+    xt = torch.from_numpy(x).to(DEV)
+    y = torch.empty_like(xt)
+    pkg._lib.check(pkg._lib.load().hif8_quant_f32(xt.data_ptr(), y.data_ptr(), xt.numel(), pkg._lib.SEM_TORCH,
+                                                  pkg._lib.stream_ptr(xt.device)), "hif8_quant_f32")
+    want = R.quant_hif8_torch(x)
+    got = host_bits(y)
+    bad = np.nonzero(got != want.view(np.uint32))[0]
+    assert bad.size == 0, [(float(x[i]), float(y[i]), float(want[i])) for i in bad[:6]]
+
+
 def test_f16_routes_every_f16(pkg, R):
     """quant_dequant_float of an fp16 tensor (hif8_quant_f16), every fp16 input bit for bit against
     the oracle in its three routes: the NPU kernel on x.float() cast back (force_py=False), the fp32
@@ -134,7 +151,7 @@ def _wide_bf16(rng, n):
     return t.view(torch.int16).numpy().view(np.uint16)
 
 
-@pytest.mark.parametrize("n", [1, 7, 15, 16, 17, 255, 4097, 65539, 1 << 20])
+@pytest.mark.parametrize("n", [1, 7, 15, 16, 17, 255, 4097, 65539, 1 << 20, (1 << 22) + 4099, 9000011])
 def test_bf16_sizes_and_tails(pkg, R, n):
     rng = np.random.default_rng(n)
     xb = _wide_bf16(rng, n)
@@ -155,7 +172,7 @@ def test_bf16_sizes_and_tails(pkg, R, n):
     assert np.array_equal(host_bits(pkg.decode(c, st)), want_npu)
 
 
-@pytest.mark.parametrize("n", [5, 16, 1000, 65536 + 9])
+@pytest.mark.parametrize("n", [5, 16, 1000, 65536 + 9, (1 << 22) + 771, 6000007])
 def test_fp32_path(pkg, R, n):
     rng = np.random.default_rng(100 + n)
     e = rng.integers(-40, 12, n)

@@ -53,7 +53,11 @@ def floor_log2(q: Fraction) -> int:
 
 
 def torch_exact(xf: float) -> float:
-    """QFuncs/hif8.py:6-23 in exact rationals with every fp32 op rounded explicitly."""
+    """QFuncs/hif8.py:6-23 in exact rationals with every fp32 op rounded explicitly.  Its floor of
+    log2 is exact (bit length); torch's float32 log2 rounds up to k for the last few floats below
+    2^k, which changes the result where |x| + 2^-45 is near 2^-44 or 2^-43: the samples of the
+    tests using this avoid those bands, which test_torch_route_fp32_log2_bands_match_torch pins
+    against torch itself."""
     if math.isnan(xf) or math.isinf(xf):
         return math.nan
     x = Fraction(xf)
@@ -226,6 +230,37 @@ def test_torch_bf16_log2_is_far_from_bf16_boundaries(R):
     dist = half - np.abs(lg - np.ldexp(np.round(m * 256.0), e - 8))
     margin = dist[nz] / np.ldexp(1.0, e[nz] - 24)          # in float32 units of lg
     assert margin.min() >= 10.0, margin.min()
+
+
+def fp32_log2_band_inputs():
+    """float32 x for which v = |x| + 2^-45 lies within 64 units below (or at) a power of two
+    2^k, k in [-47, 40], both signs: where torch's float32 log2 of v rounds up to k."""
+    xs = []
+    for k in range(-47, 41):
+        top = np.float32(2.0 ** k).view(np.uint32)
+        v = (top - np.arange(0, 64, dtype=np.uint32)).view(np.float32)
+        x = (v.astype(np.float64) - 2.0 ** -45).astype(np.float32)
+        x = x[x > 0]
+        nb = np.concatenate([x, np.nextafter(x, np.float32(0)), np.nextafter(x, np.float32(np.inf))])
+        xs.append(nb)
+    x = np.unique(np.concatenate(xs))
+    return np.concatenate([x, -x]).astype(np.float32)
+
+
+def test_torch_route_fp32_log2_bands_match_torch(R):
+    """The fp32 torch route floors torch's float32 log2 of |x| + 2^-45, which rounds up to the next
+    integer for the last few floats below a power of two; where v is near 2^-44 or 2^-43 the
+    result depends on it.  The oracle against torch's CPU ops on every such band value."""
+    torch = pytest.importorskip("torch")
+    x = fp32_log2_band_inputs()
+    got = R.quant_hif8_torch_cpu(torch.from_numpy(x)).numpy()
+    want = R.quant_hif8_torch(x)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    # the band changes results (against the exponent-field floor) near 2^-44 and 2^-43 only
+    v = (np.abs(x) + np.float32(2.0 ** -45)).astype(np.float32)
+    e_field = ((v.view(np.uint32) >> 23) & 0xFF).astype(np.int64) - 127
+    e_torch = np.floor(np.log2(v)).astype(np.int64)
+    assert np.any(e_field != e_torch)
 
 
 def test_torch_f16_route_matches_torch_every_f16(R):
