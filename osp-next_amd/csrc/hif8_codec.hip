@@ -173,27 +173,32 @@ __device__ __forceinline__ void scalar_elem(const void *xv, void *outv, int64_t 
 // DT kBF16F32 loads bf16 and computes as kF32 on the exact fp32 values.  GELU (kBF16, MODE 1):
 // each element is first replaced by its GELU, rounded to bf16 (the FFN's GELU layer, applied in
 // the down-projection's quantisation instead of in a pass of its own).
-// span > 0: workgroup b quantises the span * 256 consecutive 16-element groups from
-// b * span * 256 on (the grid covers the tensor once, in dispatch order, so the groups in flight
+// span > 0: workgroup b quantises the span * TPB consecutive 16-element groups from
+// b * span * TPB on (the grid covers the tensor once, in dispatch order, so the groups in flight
 // at any time lie in one moving window of memory); span 0: a grid-stride loop.
-template <int DT, int MODE, bool GELU = false>
-__global__ __launch_bounds__(kTPB) void k_quant(const void *__restrict__ xv, int64_t n,
+// TPB: threads per workgroup (256; 1024 for the GELU route, which holds the table of
+// GELU(bf16) for all 65536 inputs in LDS -- 128 KB of dynamic LDS, so one workgroup per CU --
+// built by every workgroup with the same gelu_bf16 evaluation the scalar route uses, and then
+// applies GELU with one lookup per element instead of its fp32 evaluation, 13 VALU operations
+// and two transcendentals).
+template <int DT, int MODE, bool GELU = false, int TPB = kTPB>
+__global__ __launch_bounds__(TPB) void k_quant(const void *__restrict__ xv, int64_t n,
                                                  const State *__restrict__ st, void *__restrict__ outv,
                                                  int sem, int use_state, int span)
 {
     __shared__ __attribute__((aligned(16))) uint8_t lds[kLdsBytes];
     const int tid = threadIdx.x;
     const int64_t ngrp = n >> 4;  // 16 elements per step
-    const int64_t stride = int64_t(gridDim.x) * kTPB;
+    const int64_t stride = int64_t(gridDim.x) * TPB;
     // This workgroup's iterations: base G0 (a multiple of 256 groups) from i0 in steps of istep
     // while G0 < iend.  In the quantise modes thread tid's input chunk j (16 bytes) of an iteration
     // is chunk G0 * kVec + j * 256 + tid of the tensor, so every load and store instruction of a
     // wave covers one contiguous span (the operation is elementwise: which 16 elements a thread
     // holds does not matter); chunks past the last whole group are masked.  The decode mode keeps
     // one 16-code group per thread (g = G0 + tid).
-    const int64_t i0 = span ? int64_t(blockIdx.x) * span * kTPB : int64_t(blockIdx.x) * kTPB;
-    const int64_t istep = span ? int64_t(kTPB) : stride;
-    const int64_t iend = span ? (i0 + int64_t(span) * kTPB < ngrp ? i0 + int64_t(span) * kTPB : ngrp) : ngrp;
+    const int64_t i0 = span ? int64_t(blockIdx.x) * span * TPB : int64_t(blockIdx.x) * TPB;
+    const int64_t istep = span ? int64_t(TPB) : stride;
+    const int64_t iend = span ? (i0 + int64_t(span) * TPB < ngrp ? i0 + int64_t(span) * TPB : ngrp) : ngrp;
     constexpr int kVec = DT == kF32 ? 4 : 2;      // 16-byte input chunks per 16 elements
     constexpr int kIpc = 16 / kVec;              // elements per input chunk
     const int64_t nchunk = ngrp * kVec;
@@ -204,7 +209,7 @@ __global__ __launch_bounds__(kTPB) void k_quant(const void *__restrict__ xv, int
     if (MODE != 2 && i0 < iend) {
 #pragma unroll
         for (int j = 0; j < kVec; ++j) {
-            const int64_t c = i0 * kVec + j * kTPB + tid;
+            const int64_t c = i0 * kVec + j * TPB + tid;
             if (c < nchunk) pre[j] = ld_stream(&xq[c]);
         }
     }
@@ -214,7 +219,7 @@ __global__ __launch_bounds__(kTPB) void k_quant(const void *__restrict__ xv, int
     // the tensor finite, each 16-element group is checked and patched to kNanCode.
     const bool nan_guard = use_state ? (st->finite == 0) : true;
     // decode tables for this scale
-    {
+    if (tid < 256) {
         uint32_t c = uint32_t(tid);
         float y;
         if (use_state) y = st->lut_f32[c];
@@ -225,41 +230,45 @@ __global__ __launch_bounds__(kTPB) void k_quant(const void *__restrict__ xv, int
     if (MODE != 2) {
         const uint4 *src = (const uint4 *)&kEncTable;
         uint4 *dst = (uint4 *)(lds + kTabLo);
-        for (uint32_t i = tid; i < sizeof(EncTable) / 16; i += kTPB) dst[i] = src[i];
+        for (uint32_t i = tid; i < sizeof(EncTable) / 16; i += TPB) dst[i] = src[i];
+    }
+    extern __shared__ __attribute__((aligned(16))) uint16_t gelu_tab[];
+    if (GELU) {
+        for (uint32_t i = tid; i < 65536u; i += TPB) gelu_tab[i] = uint16_t(gelu_bf16(i));
     }
     __syncthreads();
     const uint16_t *lut16 = (const uint16_t *)(lds + kLdsLutBf16);
     const float *lut32 = (const float *)(lds + kLdsLutF32);
 
     if (MODE == 2) {
-        // decode: 16 codes -> 16 outputs
-        const uint4 *cq = (const uint4 *)xv;
-        for (int64_t g = i0 + tid; g - tid < iend; g += istep) {
-            if (g >= ngrp) break;
-            uint4 c = cq[g];
-            uint32_t cw[4] = {c.x, c.y, c.z, c.w};
-            if (DT == kBF16) {
-                uint32_t o[8];
+        // decode: 16 codes -> 16 outputs per thread and iteration, in chunks of 8 codes (bf16
+        // out, 16 bytes each) or 4 codes (fp32 out), chunk j at G0 * kOc + j * TPB + tid so that
+        // the loads and stores of a wave are contiguous
+        constexpr int kOc = DT == kBF16 ? 2 : 4;     // output chunks of 16 bytes per 16 codes
+        const int64_t noc = ngrp * kOc;
+        for (int64_t G0 = i0; G0 < iend; G0 += istep) {
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    uint32_t d = cw[j];
-                    o[2 * j] = uint32_t(lut16[d & 0xFF]) | (uint32_t(lut16[(d >> 8) & 0xFF]) << 16);
-                    o[2 * j + 1] = uint32_t(lut16[(d >> 16) & 0xFF]) | (uint32_t(lut16[d >> 24]) << 16);
-                }
-                u32x4 *out = (u32x4 *)outv;
-                st_stream(&out[2 * g], u32x4{o[0], o[1], o[2], o[3]});
-                st_stream(&out[2 * g + 1], u32x4{o[4], o[5], o[6], o[7]});
-            } else {
-                uint4 *out = (uint4 *)outv;
+            for (int j = 0; j < kOc; ++j) {
+                const int64_t c = G0 * kOc + j * TPB + tid;
+                if (c >= noc) continue;
+                if (DT == kBF16) {
+                    const u32x2 cw = ((const u32x2 *)xv)[c];
+                    uint32_t o[4];
 #pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    uint32_t d = cw[j];
-                    out[4 * g + j] = make_uint4(f2u(lut32[d & 0xFF]), f2u(lut32[(d >> 8) & 0xFF]),
-                                                f2u(lut32[(d >> 16) & 0xFF]), f2u(lut32[d >> 24]));
+                    for (int h = 0; h < 2; ++h) {
+                        const uint32_t d = cw[h];
+                        o[2 * h] = uint32_t(lut16[d & 0xFF]) | (uint32_t(lut16[(d >> 8) & 0xFF]) << 16);
+                        o[2 * h + 1] = uint32_t(lut16[(d >> 16) & 0xFF]) | (uint32_t(lut16[d >> 24]) << 16);
+                    }
+                    st_stream(&((u32x4 *)outv)[c], u32x4{o[0], o[1], o[2], o[3]});
+                } else {
+                    const uint32_t d = ((const uint32_t *)xv)[c];
+                    st_stream(&((u32x4 *)outv)[c], u32x4{f2u(lut32[d & 0xFF]), f2u(lut32[(d >> 8) & 0xFF]),
+                                                         f2u(lut32[(d >> 16) & 0xFF]), f2u(lut32[d >> 24])});
                 }
             }
         }
-        for (int64_t j = (ngrp << 4) + int64_t(blockIdx.x) * kTPB + tid; j < n; j += stride) {
+        for (int64_t j = (ngrp << 4) + int64_t(blockIdx.x) * TPB + tid; j < n; j += stride) {
             uint32_t c = ((const uint8_t *)xv)[j];
             if (DT == kBF16) ((uint16_t *)outv)[j] = lut16[c];
             else ((float *)outv)[j] = lut32[c];
@@ -278,7 +287,7 @@ __global__ __launch_bounds__(kTPB) void k_quant(const void *__restrict__ xv, int
             if (G0 + istep < iend) {
 #pragma unroll
                 for (int j = 0; j < kVec; ++j) {
-                    const int64_t c = (G0 + istep) * kVec + j * kTPB + tid;
+                    const int64_t c = (G0 + istep) * kVec + j * TPB + tid;
                     pre[j] = c < nchunk ? ld_stream(&xq[c]) : u32x4{0u, 0u, 0u, 0u};
                 }
             }
@@ -295,7 +304,8 @@ __global__ __launch_bounds__(kTPB) void k_quant(const void *__restrict__ xv, int
                 uint32_t p[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
                 if (GELU) {
 #pragma unroll
-                    for (int k = 0; k < 8; ++k) p[k] = gelu_bf16x2(p[k]);
+                    for (int k = 0; k < 8; ++k)
+                        p[k] = uint32_t(gelu_tab[p[k] & 0xFFFFu]) | (uint32_t(gelu_tab[p[k] >> 16]) << 16);
                 }
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
@@ -345,7 +355,7 @@ __global__ __launch_bounds__(kTPB) void k_quant(const void *__restrict__ xv, int
                 // chunk j's kIpc codes are bytes j * kIpc .. of codes[]
 #pragma unroll
                 for (int j = 0; j < kVec; ++j) {
-                    const int64_t c = G0 * kVec + j * kTPB + tid;
+                    const int64_t c = G0 * kVec + j * TPB + tid;
                     if (c >= nchunk) continue;
                     if (kIpc == 8) st_stream(&((u32x2 *)outv)[c], u32x2{codes[2 * j], codes[2 * j + 1]});
                     else st_stream(&((uint32_t *)outv)[c], codes[j]);
@@ -381,7 +391,7 @@ __global__ __launch_bounds__(kTPB) void k_quant(const void *__restrict__ xv, int
             // chunk j's outputs are y[j * kIpc ..], at chunk c of the output's own element size
 #pragma unroll
             for (int j = 0; j < kVec; ++j) {
-                const int64_t c = G0 * kVec + j * kTPB + tid;
+                const int64_t c = G0 * kVec + j * TPB + tid;
                 if (c >= nchunk) continue;
                 const uint32_t *yj = y + j * kIpc;
                 if (out16 && kIpc == 8) {
@@ -400,11 +410,11 @@ __global__ __launch_bounds__(kTPB) void k_quant(const void *__restrict__ xv, int
     } else {
         // degenerate scale (amax Inf/NaN, scale 0/Inf/NaN): element-wise reference route, a
         // grid-stride loop over the elements (each visited once whatever the grid)
-        for (int64_t j = int64_t(blockIdx.x) * kTPB + tid; j < (ngrp << 4); j += stride)
+        for (int64_t j = int64_t(blockIdx.x) * TPB + tid; j < (ngrp << 4); j += stride)
             scalar_elem<DT, MODE, GELU>(xv, outv, j, s, sem);
     }
     // tail (n % 16) through the scalar route
-    for (int64_t j = (ngrp << 4) + int64_t(blockIdx.x) * kTPB + tid; j < n; j += stride)
+    for (int64_t j = (ngrp << 4) + int64_t(blockIdx.x) * TPB + tid; j < n; j += stride)
         scalar_elem<DT, MODE, GELU>(xv, outv, j, s, sem);
 }
 
@@ -710,6 +720,26 @@ static void launch_k_quant(const void *x, int64_t n, const State *st, void *out,
     hipLaunchKernelGGL((k_quant<DT, MODE, GELU>), dim3(grid), dim3(kTPB), 0, s, x, n, st, out, sem, use_state, span);
 }
 
+// The GELU route with the GELU table in LDS: a persistent grid of one 1024-thread workgroup per
+// CU (the table's 128 KB of LDS), each table built once per workgroup.
+constexpr int kGeluTPB = 1024;
+constexpr size_t kGeluTabBytes = 65536 * 2;
+static void launch_gelu_quant(const void *x, int64_t n, const State *st, void *out, int sem, hipStream_t s)
+{
+    static bool attr_set[64] = {false};
+    int dev = 0;
+    if (hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < 64 && !attr_set[dev]) {
+        (void)hipFuncSetAttribute((const void *)k_quant<kBF16, 1, true, kGeluTPB>,
+                                  hipFuncAttributeMaxDynamicSharedMemorySize, int(kGeluTabBytes));
+        attr_set[dev] = true;
+    }
+    const int64_t ngrp = (n + 15) / 16;
+    const int64_t need = (ngrp + kGeluTPB - 1) / kGeluTPB;
+    const int grid = int(need < cu_count() ? (need > 0 ? need : 1) : cu_count());
+    hipLaunchKernelGGL((k_quant<kBF16, 1, true, kGeluTPB>), dim3(grid), dim3(kGeluTPB), kGeluTabBytes, s, x, n, st,
+                       out, sem, 1, 0);
+}
+
 extern "C" {
 
 const char *hif8_strerror(int status)
@@ -782,8 +812,8 @@ static int launch_quant(const void *x, int dtype, int64_t n, const void *state, 
     const State *st = (const State *)state;
 #define HIF8_LAUNCH(DT, MODE) launch_k_quant<DT, MODE>(x, n, st, out, sem, use_state, wpc, s)
     if (gelu) {
-        if (dtype != HIF8_DTYPE_BF16 || mode != 1) return HIF8_ERR_ARG;
-        launch_k_quant<kBF16, 1, true>(x, n, st, out, sem, use_state, wpc, s);
+        if (dtype != HIF8_DTYPE_BF16 || mode != 1 || !use_state) return HIF8_ERR_ARG;
+        launch_gelu_quant(x, n, st, out, sem, s);
     } else if (dtype == HIF8_DTYPE_BF16) {
         if (mode == 0) HIF8_LAUNCH(kBF16, 0);
         else if (mode == 1 || mode == 3) HIF8_LAUNCH(kBF16, 1);
