@@ -21,9 +21,11 @@ import sys
 # ds_read_b64 of 8 codes per n-tile and lane), looks the 32 codes of each lane up in the
 # per-lane decode table (a v_perm address and a ds_read_u16 each) and packs n-tile 0's
 # looked-up values into its MFMA operand; n-tiles 1..3 are packed in the phase that uses them,
-# before MFMA 16, 32 and 48.  Phase 1 opens with the k-step's barrier and issues 7 of the 12
-# global->LDS loads of the k-step after next; the next phase 0 issues the other 5 and advances
-# the source offsets.
+# before MFMA 16, 32 and 48.  Phase 1 opens with the k-step's barrier and issues the 12
+# global->LDS loads of the k-step after next (into the stage the barrier freed); the next phase 0
+# advances the source offsets.  Issued four gaps apart from gap 1, the last load has the rest of
+# phase 1 and all of phase 0 to land (with 5 of them in phase 0, as before, the kernel ran
+# 1-1.5 % slower).
 #
 # The ops are placed greedily, in the order below, each at the first gap from its pacing
 # position on that has a free slot: fragment reads are never in adjacent gaps and loads sit
@@ -37,7 +39,7 @@ NGAPS = 64
 # three, but lab copies timed with s_memtime ran the loop at 2611 cycles per k-step with three
 # and 2474 with two (MFMAs alone: 2089).
 CAP = 2
-DTL_GAPS = {1: (1, 5, 9, 13, 17, 21, 25), 0: (1, 5, 9, 13, 17)}
+DTL_GAPS = {1: tuple(range(1, 48, 4)), 0: ()}
 # pacing (first gap each op may take): X fragment j at X_START + X_STEP * j; lookup LL at
 # LK_START + LK_NUM * LL // LK_DEN, at least CODE_GAPS after the last code read; the packs of
 # the current set's n-tile i from PK_CUR[i] (two gaps apart), the next set's n-tile 0 from PK_NEXT
@@ -87,10 +89,12 @@ def schedule(phase):
         raise RuntimeError(f"no room for {op.text}")
 
     for n, g in enumerate(DTL_GAPS[phase]):
+        # a load that opens a group of four also writes m0 (two issue slots)
         if phase == 1:
-            put(_Op(f"issue_dtl<S>(c, {n});", "dtl", cost=2), g)
+            put(_Op(f"issue_dtl<S, {n}>(c);", "dtl", cost=2 if n % 4 == 0 else 1), g)
         else:
-            put(_Op(f"issue_dtl<1 - S>(c, {len(DTL_GAPS[1]) + n});", "dtl", cost=2), g)
+            n1 = len(DTL_GAPS[1]) + n
+            put(_Op(f"issue_dtl<1 - S, {n1}>(c);", "dtl", cost=2 if n1 % 4 == 0 else 1), g)
     for i in (1, 2, 3):
         for d in range(4):
             place(_Op(f"pk<{cur}, {i}, {d}>(c);", "valu", earliest=PK_CUR[i] + 2 * d, latest=16 * i - 2))
@@ -113,7 +117,7 @@ def schedule(phase):
                   latest=NGAPS - 3, ties=(f"tie8(c.T[{nxt}][0]);",)))
     if phase == 0:
         for a in range(12):
-            place(_Op(f"adv<{a}>(c);", "valu", earliest=DTL_GAPS[0][-1] + 1 + 2 * a))
+            place(_Op(f"adv<{a}>(c);", "valu", earliest=(DTL_GAPS[0][-1] + 1 if DTL_GAPS[0] else 0) + 2 * a))
 
     ops = {}
     pre = ["wait_lgkm<0>();"] if phase == 0 else ["wait_lgkm<0>();", "wait_vm<0>();", "barrier();"]
@@ -153,6 +157,8 @@ def emit(phase):
 def generate():
     return ("// Generated by gen_gemm_schedule.py -- do not edit.\n"
             "// Main-loop phase bodies of k_linear_dtl (hif8_gemm_dtl.hip).\n\n"
+            "// global->LDS loads of a k-step issued by phase 1 (the following phase 0 issues the rest)\n"
+            f"constexpr int kLoadsPhase1 = {len(DTL_GAPS[1])};\n\n"
             + emit(0) + "\n\n" + emit(1) + "\n")
 
 

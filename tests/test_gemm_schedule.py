@@ -67,6 +67,38 @@ def test_main_loop_hazards(dtl_asm):
         assert not errors, "\n".join(errors[:20])
 
 
+def test_load_groups_share_m0(dtl_asm):
+    """Global->LDS loads go in groups of four behind one m0 write: in each main loop, every
+    `buffer_load_dwordx4 ... lds` without an offset follows an m0 write, the next three carry
+    offsets 0x400, 0x800, 0xc00 in order, and nothing else writes m0 in between."""
+    loops = _dtl_loop_lines(dtl_asm[0])
+    assert len(loops) == 2
+    for lines in loops:
+        expect, m0_set, groups = None, False, 0
+        for ln in lines:
+            op = ln.split()[0] if ln.split() else ""
+            if "m0" in ln and not op.startswith("buffer_load"):
+                assert op == "s_mov_b32" and ln.split()[1].rstrip(",") == "m0", ln
+                assert expect in (None, 0x1000), f"m0 written inside a group: {ln}"
+                m0_set, expect = True, None
+            elif op == "buffer_load_dwordx4" and ln.rstrip().endswith("lds"):
+                m = re.search(r"offset:(0x[0-9a-f]+|\d+)", ln)
+                off = int(m.group(1), 0) if m else 0
+                if off == 0:
+                    assert m0_set, f"group load without its m0 write: {ln}"
+                    m0_set, expect, groups = False, 0x400, groups + 1
+                else:
+                    assert off == expect, f"offset {off:#x} where {expect} was due: {ln}"
+                    expect = off + 0x400
+        assert groups == 6 and expect == 0x1000, (groups, expect)
+
+
+def _dtl_loop_lines(asm):
+    """The instruction lines of each MFMA main loop of the fused kernel's assembly."""
+    import isa_check
+    return [[text for _, _, text in body] for body in isa_check.mfma_loops(asm)]
+
+
 def test_checker_catches_planted_mistakes():
     """The checker must flag a read of an in-flight LDS load and a VALU->MFMA gap of 1."""
     import isa_check
