@@ -195,6 +195,12 @@ def time_ffn(pkg, torch, x, reps):
     out["fused_TFLOPs"] = round(flops / (out["fused_ms"] * 1e-3) / 1e12, 1)
     out["speedup"] = round(out["sequence_ms"] / out["fused_ms"], 4)
     out["up_epilogue_cost"] = round(out["up_gemm_gelu_stat_ms"] / out["up_gemm_plain_ms"] - 1.0, 4)
+    # the GELU quantisation pass reads y and writes x_q: 2 + 2 bytes per element (its one-workgroup
+    # prep kernel, which tables x_q over y for the state, is inside the timed call)
+    qbytes = 4.0 * x.shape[0] * ffn
+    out["gelu_fake_quant_GBps"] = round(qbytes / (out["gelu_fake_quant_ms"] * 1e-3) / 1e9, 1)
+    out["gelu_fake_quant_frac"] = round(out["gelu_fake_quant_GBps"] / 8000.0, 4)
+    out["plain_fake_quant_GBps"] = round(qbytes / (out["plain_fake_quant_ms"] * 1e-3) / 1e9, 1)
     out["what"] = "FFN 5120->13824->5120 on x[75600,5120] bf16, prepacked weights, no autograd"
     del mod
     return out

@@ -124,6 +124,10 @@ int hif8_fake_quant_to_bf16(const void *x, int dtype, int64_t n, const void *sta
  * in every kernel.  y: n bf16, x_q: n bf16, 16-byte aligned.  No counterpart of its own in the
  * reference, which runs GELU, amax and the fake quant as separate tensor ops. */
 int hif8_gelu_absmax_scale(const uint16_t *y, int64_t n, float scale_max, void *state, hif8_stream_t stream);
+/* The GELU those kernels apply, written out: g = GELU(y) for n bf16 values (nn.GELU(approximate=
+ * "tanh") on a bf16 tensor, osp_next.py:875), through the window table the quantisation pass uses
+ * (closed forms outside |y| in [0.0024, 6)).  y and g 16-byte aligned. */
+int hif8_gelu_bf16(const uint16_t *y, uint16_t *g, int64_t n, hif8_stream_t stream);
 int hif8_gelu_fake_quant(const uint16_t *y, int64_t n, void *state, float scale_max, uint16_t *x_q, int semantics,
                          hif8_stream_t stream);
 

@@ -40,6 +40,7 @@ from .hif8_linear import (  # noqa: F401
     linear_fwd_gelu_stat,
     gelu_absmax_scale,
     gelu_fake_quant,
+    gelu_bf16,
     GroupedWeight,
     grouped_ok,
     linear_fwd_grouped,
@@ -87,7 +88,7 @@ __all__ = [
     "_HIF8QKVQuantFunction", "attention_with_mask", "hif8_attention_with_mask",
     "scaled_dot_product_attention_with_mask", "LinearForward", "LinearForwardFast", "QLinear", "replace_linear",
     "save_packed", "load_packed", "pack_state_dict", "packed_from_codes", "fused_shape_ok", "linear_any",
-    "linear_fwd_gelu_stat", "gelu_absmax_scale", "gelu_fake_quant", "HIF8FFN", "WanLayerNorm", "modulate", "modulated_norm_quant", "affine_norm_quant",
+    "linear_fwd_gelu_stat", "gelu_absmax_scale", "gelu_fake_quant", "gelu_bf16", "HIF8FFN", "WanLayerNorm", "modulate", "modulated_norm_quant", "affine_norm_quant",
     "qkv_from_modulated_norm", "modulated_norm_quant_static", "GroupedWeight", "grouped_ok", "linear_fwd_grouped", "grouped_weight",
     "attention_fwd", "attention_fwd_ok", "key_list",
     "dit", "OSPNextAttentionBlock", "OSPNextBlocks", "linear_fwd_wq", "linear_fwd_wq_split", "linear_wgrad", "transpose_bf16", "wgrad_ok",

@@ -48,6 +48,7 @@ SIGNATURES = {
     "hif8_linear_fwd_gelu_stat": (_i, [_p, _p, _p, _p, _p, _i64, _i64, _i64, _f, _p, _p]),
     "hif8_gelu_absmax_scale": (_i, [_p, _i64, _f, _p, _p]),
     "hif8_gelu_fake_quant": (_i, [_p, _i64, _p, _f, _p, _i, _p]),
+    "hif8_gelu_bf16": (_i, [_p, _p, _i64, _p]),
     "hif8_modln_amax": (_i, [_p, _p, _p, _i64, _i64, _i64, _f, _p, _f, _p, _p]),
     "hif8_linear_fwd_grouped": (_i, [_p, _p, ctypes.POINTER(_p), _p, ctypes.POINTER(_p), ctypes.POINTER(_i64), _i,
                                      _i64, _i64, _p]),

@@ -149,14 +149,13 @@ __global__ __launch_bounds__(kTPB) void k_absmax(const void *__restrict__ xv, in
     else fold_amax(st, m, gridDim.x, DT, smax, red + kTPB / 64);
 }
 
-// Element j of k_quant through the scalar reference route (GELU: of the GELU of a bf16 element).
-template <int DT, int MODE, bool GELU = false>
+// Element j of k_quant through the scalar reference route.
+template <int DT, int MODE>
 __device__ __forceinline__ void scalar_elem(const void *xv, void *outv, int64_t j, float s, int sem)
 {
     uint32_t xb, yb, code;
     if (DT == kBF16) {
         xb = ((const uint16_t *)xv)[j];
-        if (GELU) xb = gelu_bf16(xb);
         slow_elem<kBF16>(xb, s, sem, yb, code);
     } else {
         xb = DT == kF32 ? ((const uint32_t *)xv)[j] : uint32_t(((const uint16_t *)xv)[j]) << 16;
@@ -170,18 +169,11 @@ __device__ __forceinline__ void scalar_elem(const void *xv, void *outv, int64_t 
 
 // MODE 0: codes, MODE 1: qdq in the arithmetic dtype (bf16 for kBF16, fp32 otherwise),
 // MODE 2: decode codes -> x_q, MODE 3: qdq rounded to the bf16 GEMM operand.
-// DT kBF16F32 loads bf16 and computes as kF32 on the exact fp32 values.  GELU (kBF16, MODE 1):
-// each element is first replaced by its GELU, rounded to bf16 (the FFN's GELU layer, applied in
-// the down-projection's quantisation instead of in a pass of its own).
+// DT kBF16F32 loads bf16 and computes as kF32 on the exact fp32 values.
 // span > 0: workgroup b quantises the span * TPB consecutive 16-element groups from
 // b * span * TPB on (the grid covers the tensor once, in dispatch order, so the groups in flight
 // at any time lie in one moving window of memory); span 0: a grid-stride loop.
-// TPB: threads per workgroup (256; 1024 for the GELU route, which holds the table of
-// GELU(bf16) for all 65536 inputs in LDS -- 128 KB of dynamic LDS, so one workgroup per CU --
-// built by every workgroup with the same gelu_bf16 evaluation the scalar route uses, and then
-// applies GELU with one lookup per element instead of its fp32 evaluation, 13 VALU operations
-// and two transcendentals).
-template <int DT, int MODE, bool GELU = false, int TPB = kTPB>
+template <int DT, int MODE, int TPB = kTPB>
 __global__ __launch_bounds__(TPB) void k_quant(const void *__restrict__ xv, int64_t n,
                                                  const State *__restrict__ st, void *__restrict__ outv,
                                                  int sem, int use_state, int span)
@@ -231,10 +223,6 @@ __global__ __launch_bounds__(TPB) void k_quant(const void *__restrict__ xv, int6
         const uint4 *src = (const uint4 *)&kEncTable;
         uint4 *dst = (uint4 *)(lds + kTabLo);
         for (uint32_t i = tid; i < sizeof(EncTable) / 16; i += TPB) dst[i] = src[i];
-    }
-    extern __shared__ __attribute__((aligned(16))) uint16_t gelu_tab[];
-    if (GELU) {
-        for (uint32_t i = tid; i < 65536u; i += TPB) gelu_tab[i] = uint16_t(gelu_bf16(i));
     }
     __syncthreads();
     const uint16_t *lut16 = (const uint16_t *)(lds + kLdsLutBf16);
@@ -302,11 +290,6 @@ __global__ __launch_bounds__(TPB) void k_quant(const void *__restrict__ xv, int6
                 u32x4 a = cur[0];
                 u32x4 b = cur[1];
                 uint32_t p[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-                if (GELU) {
-#pragma unroll
-                    for (int k = 0; k < 8; ++k)
-                        p[k] = uint32_t(gelu_tab[p[k] & 0xFFFFu]) | (uint32_t(gelu_tab[p[k] >> 16]) << 16);
-                }
 #pragma unroll
                 for (int j = 0; j < 4; ++j) {
                     uint32_t p0 = p[2 * j], p1 = p[2 * j + 1];
@@ -411,11 +394,11 @@ __global__ __launch_bounds__(TPB) void k_quant(const void *__restrict__ xv, int6
         // degenerate scale (amax Inf/NaN, scale 0/Inf/NaN): element-wise reference route, a
         // grid-stride loop over the elements (each visited once whatever the grid)
         for (int64_t j = int64_t(blockIdx.x) * TPB + tid; j < (ngrp << 4); j += stride)
-            scalar_elem<DT, MODE, GELU>(xv, outv, j, s, sem);
+            scalar_elem<DT, MODE>(xv, outv, j, s, sem);
     }
     // tail (n % 16) through the scalar route
     for (int64_t j = (ngrp << 4) + int64_t(blockIdx.x) * TPB + tid; j < n; j += stride)
-        scalar_elem<DT, MODE, GELU>(xv, outv, j, s, sem);
+        scalar_elem<DT, MODE>(xv, outv, j, s, sem);
 }
 
 // QFuncs/hif8.py:6-23 evaluated on a bf16 tensor without force_fp32 (quant_dequant_float with
@@ -474,6 +457,235 @@ __global__ __launch_bounds__(kTPB) void k_gelu_absmax(const uint16_t *__restrict
 }
 
 // The state after a GELU-statistic GEMM: amax|GELU(y)| from max y, or pending.
+// g = GELU(y) through the window table, 8 values per thread and step.
+__global__ __launch_bounds__(kTPB) void k_gelu_bf16(const uint16_t *__restrict__ y, uint16_t *__restrict__ g, int64_t n)
+{
+    __shared__ __attribute__((aligned(16))) uint16_t win[2 * kGeluWinN];
+    gelu_win_fill(win, threadIdx.x, kTPB);
+    __syncthreads();
+    const int64_t n8 = n >> 3;
+    const int64_t stride = int64_t(gridDim.x) * kTPB;
+    auto gel = [&](uint32_t w) {   // words with an Inf or NaN take the evaluation itself
+        const uint32_t e = ((w & 0x7F807F80u) + 0x00800080u) & 0x80008000u;
+        return e ? gelu_bf16x2(w) : gelu_win_bf16x2(w, win);
+    };
+    for (int64_t i = int64_t(blockIdx.x) * kTPB + threadIdx.x; i < n8; i += stride) {
+        const u32x4 v = ld_stream(&((const u32x4 *)y)[i]);
+        ((u32x4 *)g)[i] = u32x4{gel(v.x), gel(v.y), gel(v.z), gel(v.w)};
+    }
+    for (int64_t j = (n8 << 3) + int64_t(blockIdx.x) * kTPB + threadIdx.x; j < n; j += stride)
+        g[j] = uint16_t(gel(y[j]) & 0xFFFFu);
+}
+
+// ---------------------------------------------------------------------------------------------
+// x_q = qdq(GELU(y) * s) / s of a bf16 y (the down-projection's _quant of the GELU layer's
+// output) through a table of x_q over y.  For a state with a finite scale, proven finite by its
+// amax pass (GELU(y) finite, hence y finite), x_q is a function of y's 16 bits; per sign it is
+// constant below the smallest magnitude whose GELU quantises to a non-zero code and above the
+// magnitude where it saturates (and, for y < 0, from -6 on, where GELU(y) is -0), so over the
+// HiF8 range -- about 39 binades, some 5000 magnitudes -- it is tabled, with one entry for
+// y = +-0 and one for the constant run below.  k_gelu_quant_prep (one workgroup, launched before
+// every pass) finds the bounds -- a parallel search over the binades, then within one: x_q is
+// monotone in |y| there -- and fills the table into the state with the per-element route (GELU
+// through its window table, then the codec's table route: the bits of slow_elem).  k_gelu_quant
+// copies it to LDS and maps 16 inputs per thread and step with a clamp and a lookup each, about
+// 6 VALU operations per element against the 25 of GELU plus the codec.  States without a proven
+// finite input, or a degenerate scale, take the per-element reference route.
+constexpr uint32_t kGqWinOff = 2048;   // gelu_bf16 window table, in the gap of the codec's LDS map
+static_assert(kGqWinOff + 4 * kGeluWinN <= kTabLo, "GELU window table overlaps the encode table");
+// GELU(y) = -0 for y <= -6 (0xC0C0): the window table's edge, checked for every input by a test
+// (torch's CPU evaluation reaches -0 from -5.06, the device's rounding of 1 + tanh(u) later)
+constexpr uint32_t kGeluNegZero = kGeluWinHi;
+constexpr int kGqPrepTPB = 1024;
+
+// x_q(GELU(y)) of one finite bf16 input, through the window table and the codec's table route
+__device__ __forceinline__ uint32_t gq_eval(uint32_t yb, float s, int sem, const uint8_t *lds)
+{
+    const uint32_t g = gelu_win_bf16x2(yb, (const uint16_t *)(lds + kGqWinOff)) & 0xFFFFu;
+    return fast_elem_bf16<kBF16>(bf2f(g), s, sem, lds, false);
+}
+
+// The state's table for its scale and sem (one workgroup of kGqPrepTPB threads).
+__global__ __launch_bounds__(kGqPrepTPB) void k_gelu_quant_prep(State *__restrict__ st, int sem)
+{
+    __shared__ __attribute__((aligned(16))) uint8_t lds[kLdsBytes];
+    __shared__ uint32_t bnd[8];
+    const uint32_t tid = threadIdx.x;
+    const float s = st->scale;
+    if (!(st->fast != 0 && st->finite != 0)) {
+        if (tid == 0) st->gq[0] = 0u;
+        return;
+    }
+    // codec tables (bf16 decode table and encode table) and the GELU window table
+    if (tid < 256) ((uint16_t *)(lds + kLdsLutBf16))[tid] = st->lut_bf16[tid];
+    {
+        const uint4 *src = (const uint4 *)&kEncTable;
+        uint4 *dst = (uint4 *)(lds + kTabLo);
+        for (uint32_t i = tid; i < sizeof(EncTable) / 16; i += kGqPrepTPB) dst[i] = src[i];
+    }
+    gelu_win_fill((uint16_t *)(lds + kGqWinOff), tid, kGqPrepTPB);
+    if (tid == 0) {
+        bnd[0] = 0x7F80u;   // T: first binade start m = 128 t with f+(m) != f+(1)
+        bnd[1] = 0u;        // U: last binade start with f+(m) != f+(0x7F7F)
+        bnd[2] = 0x3B01u;   // V: first binade start up to 0x3B00 with f-(m) != f-(1) (none: 0x3B01)
+    }
+    __syncthreads();
+    // f+(m) = x_q(GELU(m)), f-(m) = x_q(GELU(-m)).  f+ is monotone in m; so is f- below the GELU
+    // window, where GELU(-m) = rnd(-m / 2); f-(m) = x_q(-0) from kGeluNegZero on.
+    const uint32_t f1p = gq_eval(1u, s, sem, lds), ftp = gq_eval(0x7F7Fu, s, sem, lds);
+    const uint32_t f1n = gq_eval(0x8001u, s, sem, lds);
+    if (tid >= 1 && tid < 255) {
+        const uint32_t m = tid << 7;
+        const uint32_t v = gq_eval(m, s, sem, lds);
+        if (v != f1p) atomicMin(&bnd[0], m);
+        if (v != ftp) atomicMax(&bnd[1], m);
+    } else if (tid >= 257 && tid <= 256 + 0x3B00u / 128u) {
+        const uint32_t m = (tid - 256u) << 7;
+        if (gq_eval(0x8000u | m, s, sem, lds) != f1n) atomicMin(&bnd[2], m);
+    }
+    __syncthreads();
+    const uint32_t T = bnd[0], U = bnd[1], V = bnd[2];
+    if (tid == 0) {
+        bnd[4] = T;                                           // lo+ <= T (T differs, or is the top)
+        bnd[5] = U + 128u < 0x7F7Fu ? U + 128u : 0x7F7Fu;     // hi+ <= U + 128 (equal to f+(top))
+        bnd[6] = V;                                           // lo- <= V
+    }
+    __syncthreads();
+    // within one binade: lo+ in (T - 128, T], hi+ in (U, U + 128], lo- in (V - 128, V]
+    if (tid < 128) {
+        const uint32_t m = T - 127u + tid;
+        if (m < T && m <= 0x7F7Fu && gq_eval(m, s, sem, lds) != f1p) atomicMin(&bnd[4], m);
+    } else if (tid < 256) {
+        const uint32_t m = U + 1u + (tid - 128u);
+        if (m < bnd[5] && gq_eval(m, s, sem, lds) == ftp) atomicMin(&bnd[5], m);
+    } else if (tid < 384 && V < 0x3B01u) {
+        const uint32_t m = V - 127u + (tid - 256u);
+        if (m < V && gq_eval(0x8000u | m, s, sem, lds) != f1n) atomicMin(&bnd[6], m);
+    }
+    __syncthreads();
+    // table over [lo, hi]: entry 0 is m = 0, entry 1 every 0 < m < lo, entry 2 + k m = lot + k.
+    // A range past the table's capacity (scales far outside the model's) tables its top part from
+    // lot, and the pass evaluates inputs in [lo, lot) element by element.
+    uint32_t lo = bnd[4] < bnd[6] ? bnd[4] : bnd[6];
+    lo = lo > 2u ? lo : 2u;
+    const uint32_t hi = bnd[5] > kGeluNegZero ? bnd[5] : kGeluNegZero;
+    const uint32_t lot = hi + 3u - lo > kGqCap ? hi + 3u - kGqCap : lo;
+    const uint32_t top = 2u + hi - lot;
+    for (uint32_t e = tid; e <= top; e += kGqPrepTPB) {
+        const uint32_t m = e < 2u ? e : lot + e - 2u;
+        // GELU of +m and -m in one packed evaluation, then the codec on each
+        const uint32_t g2 = gelu_win_bf16x2(m | ((m | 0x8000u) << 16), (const uint16_t *)(lds + kGqWinOff));
+        st->gq_tab[e] = fast_elem_bf16<kBF16>(bf2f(g2 & 0xFFFFu), s, sem, lds, false) |
+                        (fast_elem_bf16<kBF16>(bf2f(g2 >> 16), s, sem, lds, false) << 16);
+    }
+    if (tid == 0) {
+        st->gq[0] = 1u;
+        st->gq[1] = lo;
+        st->gq[2] = lot;
+        st->gq[3] = top;
+    }
+}
+
+// x_q of the two bf16 values of a word through the table: entry max(sat(m - (lot - 2)), min(m, 1))
+// clamped to top, byte 4 * entry + 2 * sign
+__device__ __forceinline__ uint32_t gq_word(uint32_t w, const uint32_t *tab, uint32_t lom2, uint32_t top)
+{
+    typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+    const u16x2 m = __builtin_bit_cast(u16x2, w & 0x7FFF7FFFu);
+    const u16x2 l2 = {uint16_t(lom2), uint16_t(lom2)}, t2 = {uint16_t(top), uint16_t(top)};
+    const u16x2 i = __builtin_elementwise_min(
+        __builtin_elementwise_max(__builtin_elementwise_sub_sat(m, l2), __builtin_elementwise_min(m, u16x2{1, 1})), t2);
+    const uint32_t off = __builtin_bit_cast(uint32_t, i << u16x2{2, 2}) | ((w >> 14) & 0x00020002u);
+    const uint8_t *tb = (const uint8_t *)tab;
+    return uint32_t(*(const uint16_t *)(tb + (off & 0xFFFFu))) | (uint32_t(*(const uint16_t *)(tb + (off >> 16))) << 16);
+}
+
+// x_q of one bf16 input through the reference route (GELU evaluated, then slow_elem)
+__device__ __forceinline__ uint32_t gq_ref(uint32_t yb, float s, int sem)
+{
+    uint32_t o, code;
+    slow_elem<kBF16>(gelu_bf16(yb), s, sem, o, code);
+    return o;
+}
+
+__global__ __launch_bounds__(kTPB) void k_gelu_quant(const uint16_t *__restrict__ y, int64_t n,
+                                                     const State *__restrict__ st, uint16_t *__restrict__ xq, int sem,
+                                                     int span)
+{
+    __shared__ __attribute__((aligned(16))) uint32_t tab[kGqCap];
+    const uint32_t tid = threadIdx.x;
+    const int64_t ngrp = n >> 4;
+    const int64_t stride = int64_t(gridDim.x) * kTPB;
+    const int64_t i0 = span ? int64_t(blockIdx.x) * span * kTPB : int64_t(blockIdx.x) * kTPB;
+    const int64_t istep = span ? int64_t(kTPB) : stride;
+    const int64_t iend = span ? (i0 + int64_t(span) * kTPB < ngrp ? i0 + int64_t(span) * kTPB : ngrp) : ngrp;
+    const int64_t nchunk = ngrp * 2;
+    const u32x4 *yq = (const u32x4 *)y;
+    // chunk j (16 bytes) of an iteration G0 is chunk G0 * 2 + j * 256 + tid: each load and store
+    // instruction of a wave covers one contiguous run.  The first iteration's input is requested
+    // before the table is copied.
+    u32x4 pre[2] = {};
+    if (i0 < iend) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int64_t c = i0 * 2 + j * kTPB + tid;
+            if (c < nchunk) pre[j] = ld_stream(&yq[c]);
+        }
+    }
+    const float s = st->scale;
+    if (st->gq[0] == 0u) {
+        // the per-element reference route (this workgroup's span, or its grid-stride share)
+        const int64_t j0 = span ? i0 * 16 + tid : int64_t(blockIdx.x) * kTPB + tid;
+        for (int64_t j = j0; j < (iend << 4); j += span ? int64_t(kTPB) : stride) xq[j] = uint16_t(gq_ref(y[j], s, sem));
+        for (int64_t j = (ngrp << 4) + int64_t(blockIdx.x) * kTPB + tid; j < n; j += stride)
+            xq[j] = uint16_t(gq_ref(y[j], s, sem));
+        return;
+    }
+    const uint32_t lo = st->gq[1], lot = st->gq[2], top = st->gq[3];
+    {
+        const u32x4 *src = (const u32x4 *)st->gq_tab;
+        for (uint32_t i = tid; i <= top / 4u; i += kTPB) ((u32x4 *)tab)[i] = src[i];
+    }
+    __syncthreads();
+    const uint32_t lom2 = lot - 2u;
+    const bool split = lot > lo;
+    for (int64_t G0 = i0; G0 < iend; G0 += istep) {
+        const u32x4 cur[2] = {pre[0], pre[1]};
+        if (G0 + istep < iend) {
+#pragma unroll
+            for (int j = 0; j < 2; ++j) {
+                const int64_t c = (G0 + istep) * 2 + j * kTPB + tid;
+                pre[j] = c < nchunk ? ld_stream(&yq[c]) : u32x4{0u, 0u, 0u, 0u};
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const int64_t c = G0 * 2 + j * kTPB + tid;
+            const uint32_t w[4] = {cur[j].x, cur[j].y, cur[j].z, cur[j].w};
+            uint32_t o[4];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) o[k] = gq_word(w[k], tab, lom2, top);
+            if (split) {
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+#pragma unroll
+                    for (int h = 0; h < 2; ++h) {
+                        const uint32_t b = (w[k] >> (16 * h)) & 0xFFFFu, m = b & 0x7FFFu;
+                        if (m >= lo && m < lot)
+                            o[k] = (o[k] & (0xFFFF0000u >> (16 * h))) | (gq_ref(b, s, sem) << (16 * h));
+                    }
+                }
+            }
+            if (c < nchunk) st_stream(&((u32x4 *)xq)[c], u32x4{o[0], o[1], o[2], o[3]});
+        }
+    }
+    // tail (n % 16)
+    for (int64_t j = (ngrp << 4) + int64_t(blockIdx.x) * kTPB + tid; j < n; j += stride) {
+        const uint32_t b = y[j], m = b & 0x7FFFu;
+        xq[j] = uint16_t((split && m >= lo && m < lot) ? gq_ref(b, s, sem) : (gq_word(b, tab, lom2, top) & 0xFFFFu));
+    }
+}
+
 __global__ __launch_bounds__(kTPB) void k_gelu_stat_settle(State *__restrict__ st, float smax)
 {
     __shared__ uint32_t lds[2];
@@ -690,19 +902,19 @@ using namespace hif8;
 // Workgroups of one k_quant instantiation that fit on a CU at once (its registers decide: 65 or
 // more VGPRs allow 7 or fewer waves per SIMD), read once from the runtime.  A grid of more
 // workgroups per CU than fit would run the excess as a second, partial wave.
-template <int DT, int MODE, bool GELU> static int resident_wgs()
+template <int DT, int MODE> static int resident_wgs()
 {
     static int wgs = 0;
     if (wgs == 0) {
         int b = 0;
-        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&b, k_quant<DT, MODE, GELU>, kTPB, 0) != hipSuccess || b <= 0)
+        if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&b, k_quant<DT, MODE>, kTPB, 0) != hipSuccess || b <= 0)
             b = 1;
         wgs = b;
     }
     return wgs;
 }
 
-template <int DT, int MODE, bool GELU = false>
+template <int DT, int MODE>
 static void launch_k_quant(const void *x, int64_t n, const State *st, void *out, int sem, int use_state, int wg_per_cu,
                            hipStream_t s)
 {
@@ -714,30 +926,39 @@ static void launch_k_quant(const void *x, int64_t n, const State *st, void *out,
         grid = int(blocks);
         span = kQuantSpan;
     } else {
-        const int fit = resident_wgs<DT, MODE, GELU>();
+        const int fit = resident_wgs<DT, MODE>();
         grid = grid_for(ngrp, cu_count() * (wg_per_cu < fit ? wg_per_cu : fit));
     }
-    hipLaunchKernelGGL((k_quant<DT, MODE, GELU>), dim3(grid), dim3(kTPB), 0, s, x, n, st, out, sem, use_state, span);
+    hipLaunchKernelGGL((k_quant<DT, MODE>), dim3(grid), dim3(kTPB), 0, s, x, n, st, out, sem, use_state, span);
 }
 
-// The GELU route with the GELU table in LDS: a persistent grid of one 1024-thread workgroup per
-// CU (the table's 128 KB of LDS), each table built once per workgroup.
-constexpr int kGeluTPB = 1024;
-constexpr size_t kGeluTabBytes = 65536 * 2;
+// The GELU route: the prep kernel, then spans of HIF8_GELU_SPAN x 256 groups per workgroup
+// (each copies the table from the state first), or a grid-stride loop over a grid of resident
+// workgroups for tensors under one span per CU.  On the 14B FFN-down input a sweep of the span
+// gave 846 / 696 / 718 / 715 / 748 / 795 / 803 / 815 us for 1 / 2 / 3 / 4 / 8 / 16 / 32 / 64.
+#ifndef HIF8_GELU_SPAN
+#define HIF8_GELU_SPAN 2
+#endif
+constexpr int kGeluSpan = HIF8_GELU_SPAN;
 static void launch_gelu_quant(const void *x, int64_t n, const State *st, void *out, int sem, hipStream_t s)
 {
-    static bool attr_set[64] = {false};
-    int dev = 0;
-    if (hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < 64 && !attr_set[dev]) {
-        (void)hipFuncSetAttribute((const void *)k_quant<kBF16, 1, true, kGeluTPB>,
-                                  hipFuncAttributeMaxDynamicSharedMemorySize, int(kGeluTabBytes));
-        attr_set[dev] = true;
-    }
     const int64_t ngrp = (n + 15) / 16;
-    const int64_t need = (ngrp + kGeluTPB - 1) / kGeluTPB;
-    const int grid = int(need < cu_count() ? (need > 0 ? need : 1) : cu_count());
-    hipLaunchKernelGGL((k_quant<kBF16, 1, true, kGeluTPB>), dim3(grid), dim3(kGeluTPB), kGeluTabBytes, s, x, n, st,
-                       out, sem, 1, 0);
+    int grid, span = 0;
+    if (ngrp >= int64_t(kGeluSpan) * kTPB * cu_count()) {
+        grid = int((ngrp + int64_t(kGeluSpan) * kTPB - 1) / (int64_t(kGeluSpan) * kTPB));
+        span = kGeluSpan;
+    } else {
+        static int fit = 0;
+        if (fit == 0) {
+            int b = 0;
+            if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&b, k_gelu_quant, kTPB, 0) != hipSuccess || b <= 0) b = 1;
+            fit = b;
+        }
+        grid = grid_for(ngrp, cu_count() * fit);
+    }
+    hipLaunchKernelGGL(k_gelu_quant_prep, dim3(1), dim3(kGqPrepTPB), 0, s, (State *)st, sem);
+    hipLaunchKernelGGL(k_gelu_quant, dim3(grid), dim3(kTPB), 0, s, (const uint16_t *)x, n, st, (uint16_t *)out, sem,
+                       span);
 }
 
 extern "C" {
@@ -887,6 +1108,15 @@ int hif8_gelu_absmax_scale(const uint16_t *y, int64_t n, float scale_max, void *
     const int grid = grid_for((n + 7) / 8, cu_count() * kGeluAmaxWgPerCu);
     hipLaunchKernelGGL(k_gelu_absmax, dim3(grid), dim3(kTPB), 0, (hipStream_t)stream, y, n, (State *)state,
                        scale_max, 0);
+    return last_launch();
+}
+
+int hif8_gelu_bf16(const uint16_t *y, uint16_t *g, int64_t n, hif8_stream_t stream)
+{
+    if (!y || !g || n <= 0) return HIF8_ERR_ARG;
+    if (!aligned16(y) || !aligned16(g)) return HIF8_ERR_ALIGN;
+    const int grid = grid_for((n + 7) / 8, cu_count() * kQdqWgPerCu);
+    hipLaunchKernelGGL(k_gelu_bf16, dim3(grid), dim3(kTPB), 0, (hipStream_t)stream, y, g, n);
     return last_launch();
 }
 

@@ -46,6 +46,59 @@ __device__ __forceinline__ uint32_t gelu_bf16x2(uint32_t w)
 }
 __device__ __forceinline__ uint32_t gelu_bf16(uint32_t b) { return gelu_bf16x2(b & 0xFFFFu) & 0xFFFFu; }
 
+// gelu_bf16 over all finite inputs from a window table of 2 x 1440 values.  Outside the window
+// of magnitudes [kGeluWinLo, kGeluWinHi) the rounded GELU has a closed form:
+//   |x| < kGeluWinLo (0.0024):  GELU(x) = rnd(x * 0.5) -- 0.5 x (1 + tanh(u)) = 0.5 x + 0.399 x^2
+//                               + ..., whose x^2 term is below half a bf16 unit of 0.5 x there;
+//   x >= kGeluWinHi (6.0):      GELU(x) = x -- 1 - tanh(u) < 2^-34 rounds to 1 in fp32;
+//   x <= -kGeluWinHi:           GELU(x) = -0 -- likewise tanh(u) = -1 and 1 + tanh(u) = 0
+// (torch's tanh GELU of a bf16 tensor meets them from 0x3B4B, 2.75 and -5.06 on; the window is
+// wider, and a test compares the window route with torch's GELU for every bf16 input).  Inside
+// the window, entry 2 * (|x| bits - kGeluWinLo) + sign is gelu_bf16 of that input, so the
+// magnitude -kGeluWinHi + 1 unit (entry 2 * (kGeluWinN - 1) + 1) holds the -0 that every larger
+// negative magnitude takes.
+constexpr uint32_t kGeluWinLo = 0x3B20u, kGeluWinHi = 0x40C0u;
+constexpr uint32_t kGeluWinN = kGeluWinHi - kGeluWinLo;   // 1440 magnitudes per sign
+
+// The window table (2 * kGeluWinN values, interleaved by sign) from gelu_bf16; threads tid of
+// nthreads share the work.
+__device__ __forceinline__ void gelu_win_fill(uint16_t *tab, uint32_t tid, uint32_t nthreads)
+{
+    for (uint32_t i = tid; i < kGeluWinN; i += nthreads) {
+        const uint32_t b = kGeluWinLo + i;
+        *(uint32_t *)(tab + 2 * i) = gelu_bf16x2(b | ((b | 0x8000u) << 16));   // (+x, -x) in one word
+    }
+}
+
+// gelu_bf16x2(w) for a word of two FINITE bf16 values through the window table at LDS byte
+// address tab, with packed 16-bit arithmetic and no branches: ~20 VALU operations and two
+// lookups per word, against the evaluation's 26 and four transcendentals.
+__device__ __forceinline__ uint32_t gelu_win_bf16x2(uint32_t w, const uint16_t *tab)
+{
+    typedef unsigned short u16x2 __attribute__((ext_vector_type(2)));
+    typedef short i16x2 __attribute__((ext_vector_type(2)));
+    const u16x2 lo2 = {uint16_t(kGeluWinLo), uint16_t(kGeluWinLo)};
+    const u16x2 m = __builtin_bit_cast(u16x2, w & 0x7FFF7FFFu);
+    // index i = min(max(m - lo, 0), N - 1), byte offset 4 i + 2 sign
+    const u16x2 i0 = __builtin_elementwise_sub_sat(m, lo2);
+    const u16x2 i1 = __builtin_elementwise_min(i0, u16x2{uint16_t(kGeluWinN - 1), uint16_t(kGeluWinN - 1)});
+    const uint32_t off = (__builtin_bit_cast(uint32_t, i1 << u16x2{2, 2})) | ((w >> 14) & 0x00020002u);
+    const uint8_t *tb = (const uint8_t *)tab;
+    const uint32_t t0 = *(const uint16_t *)(tb + (off & 0xFFFFu));
+    const uint32_t t1 = *(const uint16_t *)(tb + (off >> 16));
+    const uint32_t t = t0 | (t1 << 16);
+    // masks per half (all ones where true): below the window (m < lo); and the table, not the
+    // positive tail (m < hi, or negative).  m - lo and m - hi fit in int16.
+    const i16x2 ms = __builtin_bit_cast(i16x2, m);
+    const uint32_t tiny = __builtin_bit_cast(uint32_t, (ms - i16x2{short(kGeluWinLo), short(kGeluWinLo)}) >> i16x2{15, 15});
+    const uint32_t neg = __builtin_bit_cast(uint32_t, __builtin_bit_cast(i16x2, w) >> i16x2{15, 15});
+    const uint32_t below_hi = __builtin_bit_cast(uint32_t, (ms - i16x2{short(kGeluWinHi), short(kGeluWinHi)}) >> i16x2{15, 15}) | neg;
+    const uint32_t halves = gelu_pk_cvt(__builtin_bit_cast(float, w << 16) * 0.5f,
+                                        __builtin_bit_cast(float, w & 0xFFFF0000u) * 0.5f);
+    const uint32_t r = (below_hi & t) | (~below_hi & w);      // the table, or the positive tail x
+    return (tiny & halves) | (~tiny & r);
+}
+
 // The GELU statistic of a set of bf16 outputs: the largest non-negative value (bf16 bits, 0 when
 // there is none) or kGeluNonFinite when any output is Inf or NaN (GELU(-Inf) and GELU(NaN) are
 // NaN: the amax then needs the full pass).  Accumulated two outputs per 32-bit word, one packed

@@ -13,6 +13,9 @@ constexpr int kBF16F32 = HIF8_DTYPE_BF16_AS_F32;   // bf16 storage, fp32 arithme
 constexpr int kSemNpu = HIF8_SEM_NPU;
 constexpr int kSemTorch = HIF8_SEM_TORCH;
 
+// Entries of the GELU quantisation pass's table of x_q over y (hif8_codec.hip, k_gelu_quant).
+constexpr uint32_t kGqCap = 5248;
+
 // Per-tensor quantisation state (device memory, hif8_state_size() bytes).
 struct alignas(256) State {
     uint32_t counter;      // workgroups finished in the running amax pass (reset by the last)
@@ -25,6 +28,12 @@ struct alignas(256) State {
     uint32_t pending;      // 1 when a GEMM's GELU statistic left amax|GELU(y)| to an amax pass
     uint16_t lut_bf16[256];  // bf16 bits of x_q(code) = rnd(decode(code) / scale)
     float lut_f32[256];      // fp32 decode(code) / scale
+    // For the GELU quantisation pass of the tensor this state scales (written by its prep kernel
+    // before every pass): x_q over y for y = +-0, the run 0 < |y| < lo, and |y| = lot .. hi
+    // (entry e: x_q of +|y| in the low half, of -|y| in the high half); gq[0..3] = valid, lo, lot,
+    // top (the last entry).
+    uint32_t gq[4];
+    uint32_t gq_tab[kGqCap];
 };
 
 static_assert(sizeof(State) % 256 == 0, "state size");

@@ -587,6 +587,20 @@ def gelu_absmax_scale(y: Tensor, scale_max: float, state: QuantState) -> QuantSt
     return state
 
 
+def gelu_bf16(y: Tensor) -> Tensor:
+    """GELU(y) of a bf16 tensor as the library's GELU quantisation applies it (hif8_gelu_bf16):
+    nn.GELU(approximate="tanh") on bf16, ``osp_next.py:875``."""
+    _lib.require_gpu_tensor(y, "y")
+    if y.dtype != torch.bfloat16:
+        raise TypeError("gelu_bf16 takes a bfloat16 tensor")
+    y = _aligned(y)
+    out = torch.empty_like(y)
+    if y.numel():
+        _lib.check(_lib.load().hif8_gelu_bf16(y.data_ptr(), out.data_ptr(), y.numel(), _lib.stream_ptr(y.device)),
+                   "hif8_gelu_bf16")
+    return out
+
+
 def gelu_fake_quant(y: Tensor, state: QuantState, scale_max: float = 15.0, semantics: int = _lib.SEM_NPU) -> Tensor:
     """``_quant(GELU(y))[0]`` in bf16 without writing GELU(y) (hif8_gelu_fake_quant), with the state
     from ``linear_fwd_gelu_stat`` or ``gelu_absmax_scale`` (a pending state is completed first)."""

@@ -137,3 +137,98 @@ def test_hif8ffn_fused_forward(pkg, dim, ffn, M):
     assert not mod.fused_ok(x)
     mod(x).float().sum().backward()
     assert x.grad is not None and torch.isfinite(x.grad.float()).all()
+
+
+def _all_bf16():
+    return torch.arange(65536, dtype=torch.int32).to(torch.int16).view(torch.bfloat16).to(DEV)
+
+
+# Finite bf16 inputs whose library GELU may differ from torch's on the GPU by one bf16 unit (the
+# device's tanh is 1 - 2 / (1 + e^(2|u|)) from the hardware exp2 and reciprocal, not torch's
+# tanhf): none, measured over all 65280 finite inputs.
+GELU_TORCH_DIFF_MAX = 0
+
+
+def test_gelu_bf16_every_input(pkg):
+    """GELU of every bf16 value through the window route (the one the quantisation pass applies)
+    against torch's tanh GELU on the GPU: the closed forms outside the window hold exactly,
+    inside it at most GELU_TORCH_DIFF_MAX of the 65280 finite inputs round one unit apart, and the
+    non-finite inputs give GELU(+Inf) = +Inf and NaN for -Inf and NaN."""
+    print("[gelu] gelu_bf16 over every bf16 input", flush=True)
+    y = _all_bf16()
+    g = pkg.gelu_bf16(y)
+    ref = torch.nn.functional.gelu(y, approximate="tanh")
+    yb = y.view(torch.int16).to(torch.int32) & 0xFFFF
+    gb = g.view(torch.int16).to(torch.int32) & 0xFFFF
+    rb = ref.view(torch.int16).to(torch.int32) & 0xFFFF
+    mag, neg = yb & 0x7FFF, yb >= 0x8000
+    finite = mag < 0x7F80
+    # closed forms
+    tiny = finite & (mag < 0x3B20)
+    half = (y.float() * 0.5).to(torch.bfloat16).view(torch.int16).to(torch.int32) & 0xFFFF
+    assert torch.equal(gb[tiny], half[tiny])
+    assert torch.equal(gb[finite & ~neg & (mag >= 0x40C0)], yb[finite & ~neg & (mag >= 0x40C0)])
+    assert bool((gb[finite & neg & (mag >= 0x40C0)] == 0x8000).all())
+    # torch meets the same closed forms there
+    outside = finite & ((mag < 0x3B20) | (mag >= 0x40C0))
+    assert torch.equal(gb[outside], rb[outside])
+    # inside: equal but for a few one-unit roundings
+    diff = finite & (gb != rb)
+    n = int(diff.sum())
+    print(f"[gelu] {n} finite inputs round one unit apart from torch", flush=True)
+    assert n <= GELU_TORCH_DIFF_MAX
+    if n:
+        assert bool(((gb[diff] - rb[diff]).abs() == 1).all())
+    # non-finite
+    assert int(gb[yb == 0x7F80]) == 0x7F80
+    nan_in = ~finite & ~(yb == 0x7F80)
+    assert bool(torch.isnan(g[nan_in].float()).all())
+
+
+@pytest.mark.parametrize("sem", [0, 1])
+def test_gelu_quant_table_route_equals_scalar_route(pkg, sem):
+    """The GELU quantisation pass through its table of x_q over y (the route of a state that proved
+    its input finite) gives the x_q of the per-element route (GELU evaluated for each element, then
+    the reference qdq) for every finite bf16 input, at scales that move the tabled range of |y| over
+    the whole bf16 range -- the extreme ones (2^-30, 2^30) need more entries than the table holds,
+    so part of the range is evaluated element by element.  The input is long enough for the pass's
+    span grid.  A state not proven finite takes the per-element route, with the same x_q."""
+    print(f"[gelu] table route vs scalar route, semantics {sem}", flush=True)
+    y = _all_bf16()
+    y = y[(y.view(torch.int16).to(torch.int32) & 0x7F80) != 0x7F80]
+    reps = (256 * 16 * 64 * 300) // y.numel() + 1
+    y = y[torch.randperm(y.numel(), generator=torch.Generator().manual_seed(sem)).to(DEV)].repeat(reps).contiguous()
+    L = pkg._lib.load()
+    s = pkg._lib.stream_ptr(y.device)
+    for scale in (2.0 ** -30, 2.0 ** -12, 1.0 / 3.0, 1.0, 7.5, 2.0 ** 6, 1000.0, 2.0 ** 18, 2.0 ** 30):
+        st = pkg.QuantState(DEV)
+        pkg._lib.check(L.hif8_set_scale(st.ptr, 0, float(scale), s), "hif8_set_scale")
+        st.buf[24:28].view(torch.int32).fill_(1)   # State.finite = 1 (true of y): the table route
+        fast = pkg.gelu_fake_quant(y, st, 15.0, sem)
+        slow_st = pkg.QuantState(DEV)
+        slow_st.buf.copy_(st.buf)
+        slow_st.buf[16:20].zero_()                 # State.fast = 0: the per-element route
+        slow = pkg.gelu_fake_quant(y, slow_st, 15.0, sem)
+        bad = (fast.view(torch.int16) != slow.view(torch.int16)).nonzero().flatten()
+        if bad.numel():
+            i = bad[:12].cpu()
+            yb = [hex(int(v) & 0xFFFF) for v in y.view(torch.int16)[bad[:12]].cpu()]
+            fb = [hex(int(v) & 0xFFFF) for v in fast.view(torch.int16)[bad[:12]].cpu()]
+            sb = [hex(int(v) & 0xFFFF) for v in slow.view(torch.int16)[bad[:12]].cpu()]
+            print(f"[gelu] scale {scale}: {bad.numel()} differ; y {yb} table {fb} reference {sb}", flush=True)
+        assert torch.equal(fast.view(torch.int16), slow.view(torch.int16)), scale
+        guard_st = pkg.QuantState(DEV)
+        guard_st.buf.copy_(st.buf)
+        guard_st.buf[24:28].zero_()                # State.finite = 0: per element too
+        guarded = pkg.gelu_fake_quant(y, guard_st, 15.0, sem)
+        assert torch.equal(guarded.view(torch.int16), slow.view(torch.int16)), scale
+    # a short tensor (the grid-stride route) with a tail
+    yt = y[: 5 * 4096 + 7].contiguous()
+    st = pkg.QuantState(DEV)
+    pkg._lib.check(L.hif8_set_scale(st.ptr, 0, 2.5, s), "hif8_set_scale")
+    st.buf[24:28].view(torch.int32).fill_(1)
+    slow_st = pkg.QuantState(DEV)
+    slow_st.buf.copy_(st.buf)
+    slow_st.buf[16:20].zero_()
+    assert torch.equal(pkg.gelu_fake_quant(yt, st, 15.0, sem).view(torch.int16),
+                       pkg.gelu_fake_quant(yt, slow_st, 15.0, sem).view(torch.int16))
