@@ -119,7 +119,9 @@ int hif8_fake_quant_to_bf16(const void *x, int dtype, int64_t n, const void *sta
  *     hif8_absmax_scale of GELU(y) would (one read of y);
  *   hif8_gelu_fake_quant: x_q = qdq(GELU(y) * s) / s in bf16 with state's scale -- first running
  *     the amax of GELU(y) when state is pending (hif8_linear_fwd[_wq]_gelu_stat could not settle
- *     it), otherwise reading y once.
+ *     it), otherwise reading y once.  A one-workgroup kernel first tables x_q over y's 16 bits
+ *     into state (for a state whose amax pass proved the input finite), and the pass maps y
+ *     through that table; other states take the per-element evaluation.
  * GELU(y) = bf16(0.5 y (1 + tanh(sqrt(2/pi) (y + 0.044715 y^3)))) in fp32, the same evaluation
  * in every kernel.  y: n bf16, x_q: n bf16, 16-byte aligned.  No counterpart of its own in the
  * reference, which runs GELU, amax and the fake quant as separate tensor ops. */

@@ -27,7 +27,7 @@ OFF_AMAX, OFF_SCALE, OFF_FAST, OFF_LUT16, OFF_LUT32 = 8, 12, 16, 32, 544
 
 def _run_states(pkg, x_rows: torch.Tensor, dtype_code: int, smaxes):
     """hif8_absmax_scale of row i of x_rows (its first element; n = 1) into state (i, j) for each
-    scale_max j; returns the states as a host array [rows, len(smaxes), state_size]."""
+    scale_max j; returns the states' leading fields as a host array [rows, len(smaxes), 1568]."""
     L = pkg._lib.load()
     S = pkg._lib.state_size()
     rows = x_rows.shape[0]
@@ -43,7 +43,8 @@ def _run_states(pkg, x_rows: torch.Tensor, dtype_code: int, smaxes):
             if rc != 0:
                 raise AssertionError(f"hif8_absmax_scale rc {rc} at row {i}")
     torch.cuda.synchronize()
-    return st.cpu().numpy().reshape(rows, len(smaxes), S)
+    # the fields compared below end with lut_f32 (byte 1568); the rest of a state is not copied
+    return st.view(rows, len(smaxes), S)[:, :, :OFF_LUT32 + 1024].cpu().numpy()
 
 
 def _fields(h):
