@@ -465,8 +465,9 @@ __device__ __forceinline__ void qdq_rows(const uint16_t *x, const uint16_t *shif
                 else modln8(xv[j], -mean, rstd, tw, sh, one_lo, one_hi, y);
                 if (MODE == 0) qdq8_ytab(y, ylo, yhi, ytab, o);
                 else qdq8_codec<MODE == 1>(y, s, sem, enc, lut16, o);
-                xo[c] = u32x4{o[0], o[1], o[2], o[3]};
-                if (yo) yo[c] = u32x4{y[0], y[1], y[2], y[3]};
+                // non-temporal: x_q is not read again here (8 % on the 14B producer's pass 2)
+                __builtin_nontemporal_store(u32x4{o[0], o[1], o[2], o[3]}, &xo[c]);
+                if (yo) __builtin_nontemporal_store(u32x4{y[0], y[1], y[2], y[3]}, &yo[c]);
             }
         }
     };
