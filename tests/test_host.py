@@ -138,6 +138,26 @@ def test_status_codes_without_gpu(pkg):
     assert L.hif8_modln_fake_quant(fake, None, None, 4, 5120, 4, fake, fake, 9, fake, None, None) == -1
     assert L.hif8_modln_fake_quant(fake, None, None, 4, 5120, 4, fake, fake, 0, odd, None, None) == -3
     assert L.hif8_modln_fake_quant(fake, None, None, 4, 5120, 4, fake, fake, 0, fake, odd, None) == -3
+    # GELU: the library's GELU and the GELU quantisation pass (pointers, sizes, semantics, alignment)
+    assert L.hif8_gelu_bf16(None, fake, 16, None) == -1
+    assert L.hif8_gelu_bf16(fake, fake, 0, None) == -1
+    assert L.hif8_gelu_bf16(odd, fake, 16, None) == -3
+    assert L.hif8_gelu_fake_quant(fake, 16, None, 15.0, fake, 0, None) == -1
+    assert L.hif8_gelu_fake_quant(fake, 16, fake, 15.0, fake, 2, None) == -1      # NPU or torch only
+    assert L.hif8_gelu_fake_quant(fake, 16, fake, 15.0, odd, 0, None) == -3
+    # fp16 qdq: semantics 0, 1 and 3 (the fp16 torch route); any alignment
+    assert L.hif8_quant_f16(None, fake, 16, 0, None) == -1
+    assert L.hif8_quant_f16(fake, fake, 0, 3, None) == -1
+    assert L.hif8_quant_f16(fake, fake, 16, 2, None) == -1
+    # the fp32 GEMM and the zero padding: pointers, sizes, dtypes, strides, element size
+    assert L.hif8_gemm_f32(None, 0, fake, 0, fake, 1, 4, 4, 4, 4, 1, 4, 1, None) == -1
+    assert L.hif8_gemm_f32(fake, 0, fake, 0, fake, 1, 0, 4, 4, 4, 1, 4, 1, None) == -1
+    assert L.hif8_gemm_f32(fake, 2, fake, 0, fake, 1, 4, 4, 4, 4, 1, 4, 1, None) == -1
+    assert L.hif8_gemm_f32(fake, 0, fake, 0, fake, 1, 4, 4, 4, -4, 1, 4, 1, None) == -1
+    assert L.hif8_gemm_f32(fake, 0, fake, 0, fake, 1, 64 * 65536, 4, 4, 4, 1, 4, 1, None) == -2
+    assert L.hif8_pad_2d(None, 4, 4, fake, 8, 8, 2, None) == -1
+    assert L.hif8_pad_2d(fake, 4, 4, fake, 0, 8, 2, None) == -1
+    assert L.hif8_pad_2d(fake, 4, 4, fake, 8, 8, 3, None) == -1
 
 
 def test_python_layer_refuses_cpu_tensors(pkg):
