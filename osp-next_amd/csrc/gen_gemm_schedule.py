@@ -19,9 +19,10 @@ import sys
 # MFMA m of a phase is n-tile i = m / 16 (16 features) times m-tile j = m % 16 (16 rows).  For
 # the next phase a phase reads its 16 X fragments (ds_read_b128) and the wave's W codes (one
 # ds_read_b64 of 8 codes per n-tile and lane), looks the 32 codes of each lane up in the
-# per-lane decode table (a v_perm address and a ds_read_u16 each) and packs n-tile 0's
-# looked-up values into its MFMA operand; n-tiles 1..3 are packed in the phase that uses them,
-# before MFMA 16, 32 and 48.  Phase 1 opens with the k-step's barrier and issues the 12
+# per-lane decode table (a v_perm address and a ds_read_u16 each) and packs n-tiles 0 and 1's
+# looked-up values into their MFMA operands; n-tiles 2 and 3 are packed in the phase that uses
+# them, before MFMA 32.  (The MFMAs go in 2 x 2 blocks of n-tiles x m-tiles, n-tiles 0 and 1 in
+# the first half of the phase, 2 and 3 in the second: see mm in hif8_gemm_dtl.hip.)  Phase 1 opens with the k-step's barrier and issues the 12
 # global->LDS loads of the k-step after next (into the stage the barrier freed); the next phase 0
 # advances the source offsets.  Issued four gaps apart from gap 1, the last load has the rest of
 # phase 1 and all of phase 0 to land (with 5 of them in phase 0, as before, the kernel ran
@@ -42,12 +43,13 @@ CAP = 2
 DTL_GAPS = {1: tuple(range(1, 48, 4)), 0: ()}
 # pacing (first gap each op may take): X fragment j at X_START + X_STEP * j; lookup LL at
 # LK_START + LK_NUM * LL // LK_DEN, at least CODE_GAPS after the last code read; the packs of
-# the current set's n-tile i from PK_CUR[i] (two gaps apart), the next set's n-tile 0 from PK_NEXT
+# the current set's n-tile i (2, 3) from PK_CUR[i] (two gaps apart), the next set's n-tile t (0, 1)
+# from PK_NEXT[t]
 X_START, X_STEP = 2, 3
 LK_START, LK_NUM, LK_DEN = 10, 5, 4
 CODE_GAPS = 6
-PK_CUR = (0, 0, 8, 24)
-PK_NEXT = 52
+PK_CUR = (0, 0, 0, 8)
+PK_NEXT = (52, 44)
 
 
 class _Op:
@@ -95,9 +97,9 @@ def schedule(phase):
         else:
             n1 = len(DTL_GAPS[1]) + n
             put(_Op(f"issue_dtl<1 - S, {n1}>(c);", "dtl", cost=2 if n1 % 4 == 0 else 1), g)
-    for i in (1, 2, 3):
+    for i in (2, 3):
         for d in range(4):
-            place(_Op(f"pk<{cur}, {i}, {d}>(c);", "valu", earliest=PK_CUR[i] + 2 * d, latest=16 * i - 2))
+            place(_Op(f"pk<{cur}, {i}, {d}>(c);", "valu", earliest=PK_CUR[i] + 2 * d, latest=30))
     codes = [f"rd_code<{ns}, {npar}, {i}>(c);" for i in range(4)]
     for t in codes:
         place(_Op(t, "b64", lds=True))
@@ -111,10 +113,11 @@ def schedule(phase):
         place(_Op(f"lka<{r}, {ll}>(c);", "valu", deps=codes, after=after, earliest=LK_START + (LK_NUM * ll) // LK_DEN,
                   ties=("tie_cd(c);",)))
         place(_Op(f"lkr<{nxt}, {r}, {ll}>(c);", "u16", lds=True, after=[(f"lka<{r}, {ll}>(c);", 1)]))
-    tile0 = [f"lkr<{nxt}, {ll % 4}, {ll}>(c);" for ll in range(8)]
-    for d in range(4):
-        place(_Op(f"pk<{nxt}, 0, {d}>(c);", "valu", deps=tile0, after=[(t, 4) for t in tile0], earliest=PK_NEXT + d,
-                  latest=NGAPS - 3, ties=(f"tie8(c.T[{nxt}][0]);",)))
+    for tt in (1, 0):
+        tl = [f"lkr<{nxt}, {ll % 4}, {ll}>(c);" for ll in range(8 * tt, 8 * tt + 8)]
+        for d in range(4):
+            place(_Op(f"pk<{nxt}, {tt}, {d}>(c);", "valu", deps=tl, after=[(t, 4) for t in tl], earliest=PK_NEXT[tt] + d,
+                      latest=NGAPS - 3, ties=(f"tie8(c.T[{nxt}][{tt}]);",)))
     if phase == 0:
         for a in range(12):
             place(_Op(f"adv<{a}>(c);", "valu", earliest=(DTL_GAPS[0][-1] + 1 if DTL_GAPS[0] else 0) + 2 * a))
