@@ -12,13 +12,15 @@
 // Two passes over x, 6 bytes per element in total:
 //   hif8_modln_amax         reads x, writes each row's (mean, rstd) and folds amax|y| into the
 //                           state (its last workgroup computes the scale and decode tables);
+//                           with one modulation row, amax|y| comes from per-column extremes of
+//                           n (k_modln_amax_ext below), without y per element;
 //   hif8_modln_fake_quant   reads x again, recomputes y from the stored statistics (the same
 //                           instructions, so the same bits) and writes x_q (and y if asked).
 //
 // One wavefront per row: lane l holds the 16-byte chunks l, l + 64, ... of the row in
 // registers, so mean and variance are two-pass sums over registers (no re-read), reduced
 // across the wavefront, and the loads of the wavefront's next row are in flight meanwhile.
-// Rows are strided over a grid of 2 workgroups x 4 wavefronts per CU.  With one modulation
+// Rows are strided over a grid of 2-3 workgroups x 4 wavefronts per CU.  With one modulation
 // row, rnd(1 + scale) and shift are computed once per workgroup into LDS as fp32.
 //
 // The same two passes serve the affine LayerNorm in front of the cross-attention's q projection
@@ -45,6 +47,7 @@ constexpr int kTPB = 256;
 constexpr int kWaves = kTPB / 64;
 constexpr int kMaxChunks = 16;   // 16-B chunks per lane: dim <= 16 * 64 * 8 = 8192
 constexpr int kWgPerCu = 3;     // pass 1 (157 VGPRs at dim 5120: 3 wavefronts per SIMD)
+constexpr int kExtWgPerCu = 2;  // pass 1 from per-column extremes (k_modln_amax_ext)
 constexpr int kQdqWgPerCu = 3;  // pass 2
 
 // Sum over the wavefront, returned to every lane: DPP steps within each row of 16 lanes
@@ -140,6 +143,52 @@ __device__ __forceinline__ bf16x2 as_bf2(uint32_t u) { return __builtin_bit_cast
               [c1] CC(C1), [c2] CC(C2), [c3] CC(C3), [c4] CC(C4), [c5] CC(C5), [c6] CC(C6), [c7] CC(C7));      \
     } while (0)
 
+// HIF8_DOT_SUB_MUL folded into running per-column extremes: n = rnd((x - mean) * rstd) of 4 words
+// (8 columns), then mx = max(mx, n) and mn = min(mn, n) per 16-bit half with v_pk_max_f16 /
+// v_pk_min_f16 on the bf16 bit patterns.  Read as fp16, bf16 bit patterns keep their order
+// (both are sign-magnitude with the magnitude monotone in the low 15 bits) wherever neither
+// is an fp16 NaN, i.e. for |n| < 2^121; the caller only folds rows whose n are all finite
+// and far below that.  One asm block, so the n temporaries end inside it.
+#define HIF8_DOT_SUB_MUL_EXT(w, one_lo, one_hi, nmean, rstd, mx, mn)                                           \
+    do {                                                                                                       \
+        float d0_, d1_, d2_, d3_, d4_, d5_, d6_, d7_;                                                          \
+        uint32_t n0_, n1_, n2_, n3_;                                                                           \
+        asm("v_dot2_f32_bf16 %[d0], %[w0], %[lo], %[nm]\n\t"                                                   \
+            "v_dot2_f32_bf16 %[d1], %[w0], %[hi], %[nm]\n\t"                                                   \
+            "v_dot2_f32_bf16 %[d2], %[w1], %[lo], %[nm]\n\t"                                                   \
+            "v_dot2_f32_bf16 %[d3], %[w1], %[hi], %[nm]\n\t"                                                   \
+            "v_dot2_f32_bf16 %[d4], %[w2], %[lo], %[nm]\n\t"                                                   \
+            "v_dot2_f32_bf16 %[d5], %[w2], %[hi], %[nm]\n\t"                                                   \
+            "v_dot2_f32_bf16 %[d6], %[w3], %[lo], %[nm]\n\t"                                                   \
+            "v_dot2_f32_bf16 %[d7], %[w3], %[hi], %[nm]\n\t"                                                   \
+            "v_mul_f32 %[d0], %[d0], %[rs]\n\t"                                                                \
+            "v_mul_f32 %[d1], %[d1], %[rs]\n\t"                                                                \
+            "v_mul_f32 %[d2], %[d2], %[rs]\n\t"                                                                \
+            "v_mul_f32 %[d3], %[d3], %[rs]\n\t"                                                                \
+            "v_mul_f32 %[d4], %[d4], %[rs]\n\t"                                                                \
+            "v_mul_f32 %[d5], %[d5], %[rs]\n\t"                                                                \
+            "v_mul_f32 %[d6], %[d6], %[rs]\n\t"                                                                \
+            "v_mul_f32 %[d7], %[d7], %[rs]\n\t"                                                                \
+            "v_cvt_pk_bf16_f32 %[n0], %[d0], %[d1]\n\t"                                                        \
+            "v_cvt_pk_bf16_f32 %[n1], %[d2], %[d3]\n\t"                                                        \
+            "v_cvt_pk_bf16_f32 %[n2], %[d4], %[d5]\n\t"                                                        \
+            "v_cvt_pk_bf16_f32 %[n3], %[d6], %[d7]\n\t"                                                        \
+            "v_pk_max_f16 %[x0], %[x0], %[n0]\n\t"                                                             \
+            "v_pk_min_f16 %[m0], %[m0], %[n0]\n\t"                                                             \
+            "v_pk_max_f16 %[x1], %[x1], %[n1]\n\t"                                                             \
+            "v_pk_min_f16 %[m1], %[m1], %[n1]\n\t"                                                             \
+            "v_pk_max_f16 %[x2], %[x2], %[n2]\n\t"                                                             \
+            "v_pk_min_f16 %[m2], %[m2], %[n2]\n\t"                                                             \
+            "v_pk_max_f16 %[x3], %[x3], %[n3]\n\t"                                                             \
+            "v_pk_min_f16 %[m3], %[m3], %[n3]"                                                                 \
+            : [n0] "=&v"(n0_), [n1] "=&v"(n1_), [n2] "=&v"(n2_), [n3] "=&v"(n3_), [d0] "=&v"(d0_),             \
+              [d1] "=&v"(d1_), [d2] "=&v"(d2_), [d3] "=&v"(d3_), [d4] "=&v"(d4_), [d5] "=&v"(d5_),             \
+              [d6] "=&v"(d6_), [d7] "=&v"(d7_), [x0] "+v"(mx[0]), [x1] "+v"(mx[1]), [x2] "+v"(mx[2]),          \
+              [x3] "+v"(mx[3]), [m0] "+v"(mn[0]), [m1] "+v"(mn[1]), [m2] "+v"(mn[2]), [m3] "+v"(mn[3])         \
+            : [w0] "v"(w[0]), [w1] "v"(w[1]), [w2] "v"(w[2]), [w3] "v"(w[3]), [lo] "s"(one_lo),                \
+              [hi] "s"(one_hi), [nm] "v"(nmean), [rs] "v"(rstd));                                              \
+    } while (0)
+
 // The bf16 pairs (1, 0) and (0, 1).  They are passed in SGPRs set up by sgpr_word: as an
 // immediate, 0x3F800000 is the bit pattern of fp32 1.0 and gets encoded as the inline
 // constant 1.0, which a packed-bf16 operand does not read as (0, 1).
@@ -214,17 +263,25 @@ __device__ __forceinline__ void fill_mod(uint32_t *lmod, const uint16_t *shift, 
 // pollutes its neighbour only where the row statistics are NaN (x) or where the modulation
 // itself overflows or is NaN (u); both make amax|y| non-finite, so x_q is all NaN there as in
 // the reference, and only the diagnostic y differs.
-__device__ __forceinline__ void modln8(const u32x4 &xv, float nmean, float rstd, const uint32_t (&tw)[8],
-                                       const float (&sh)[8], uint32_t one_lo, uint32_t one_hi, uint32_t (&y)[4])
+// u = rnd(n * t) and y = rnd(u + shift) of 4 words of n: the modulation half of the chain.
+__device__ __forceinline__ void uy8(const uint32_t (&n)[4], const uint32_t (&tw)[8], const float (&sh)[8],
+                                    uint32_t one_lo, uint32_t one_hi, uint32_t (&y)[4])
 {
-    const uint32_t w[4] = {xv.x, xv.y, xv.z, xv.w};
-    uint32_t n[4], u[4];
-    HIF8_DOT_SUB_MUL(n, w, one_lo, one_hi, nmean, rstd);
+    uint32_t u[4];
 #define HIF8_Z(v) "i"(0)
     HIF8_DOT_PAIR8(u, n, tw[0], tw[1], tw[2], tw[3], tw[4], tw[5], tw[6], tw[7], 0, 0, 0, 0, 0, 0, 0, 0, "v", HIF8_Z);
 #undef HIF8_Z
     HIF8_DOT_PAIR8(y, u, one_lo, one_hi, one_lo, one_hi, one_lo, one_hi, one_lo, one_hi, sh[0], sh[1], sh[2], sh[3],
                    sh[4], sh[5], sh[6], sh[7], "s", "v");
+}
+
+__device__ __forceinline__ void modln8(const u32x4 &xv, float nmean, float rstd, const uint32_t (&tw)[8],
+                                       const float (&sh)[8], uint32_t one_lo, uint32_t one_hi, uint32_t (&y)[4])
+{
+    const uint32_t w[4] = {xv.x, xv.y, xv.z, xv.w};
+    uint32_t n[4];
+    HIF8_DOT_SUB_MUL(n, w, one_lo, one_hi, nmean, rstd);
+    uy8(n, tw, sh, one_lo, one_hi, y);
 }
 
 // Affine LayerNorm of the 8 elements of one chunk: y = rnd(fma(w, (x - mean) * rstd, b)).
@@ -364,6 +421,117 @@ __global__ __launch_bounds__(kTPB) void k_modln_amax(const uint16_t *__restrict_
         if (row + step < rows) load_row<NCH, FULL>(x, row + step, dim, lane, nch_row, xa);
         body(xb, row);
         row += step;
+    }
+    uint32_t m = m2.x > m2.y ? m2.x : m2.y;
+    for (int o = 32; o > 0; o >>= 1) m = max(m, (uint32_t)__shfl_xor((int)m, o, 64));
+    if (lane == 0) red[wave] = m;
+    __syncthreads();
+    m = max(max(red[0], red[1]), max(red[2], red[3]));
+    fold_amax(st, m, gridDim.x, kBF16, smax, red + kWaves);
+}
+
+// Pass 1 with one modulation row (MODL) and at most 10 chunks per lane (dim <= 5120).
+// y = rnd(rnd(n * t) + shift) is, for each column, a monotone function of n (non-decreasing
+// for t >= 0, non-increasing for t < 0: every step is a monotone fp32 operation followed by a
+// monotone rounding), so over all rows max|y| of a column is |y| at the column's largest or
+// smallest n.  The row loop computes n and folds it into the lane's per-column max and min
+// (two packed ops per word instead of the modulation, the magnitude and the max); after the
+// loop y is evaluated at the 2 x 8 extremes per chunk with the instructions pass 2 uses, so
+// the amax is the same bits as the max over pass 2's y.
+// Rows whose n could be non-finite (mean or rstd non-finite, or rstd = 0 from an overflowed
+// variance, where (x - mean) * 0 can be NaN) are not folded: a wavefront that meets one
+// re-reads all its rows after the loop and takes every y through the full chain, as the
+// per-element pass does, so NaN rows give the same NaN bits.  One row in registers at a time:
+// 151 VGPRs, 3 wavefronts per SIMD; 2 workgroups per CU stream x faster than 3 here.
+template <int NCH>
+__global__ __launch_bounds__(kTPB) __attribute__((amdgpu_waves_per_eu(3))) void k_modln_amax_ext(
+    const uint16_t *__restrict__ x, const uint16_t *__restrict__ shift, const uint16_t *__restrict__ scale,
+    int64_t rows, int dim, float eps, float *__restrict__ stats, State *__restrict__ st, float smax)
+{
+    extern __shared__ __attribute__((aligned(16))) uint32_t lmod[];
+    __shared__ uint32_t red[kWaves + 2];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int nch_row = dim >> 3;
+    fill_mod<true>(lmod, shift, scale, dim);
+    __syncthreads();
+    typedef uint16_t u16x2 __attribute__((ext_vector_type(2)));
+    u16x2 m2 = {0, 0};
+    const int64_t step = int64_t(gridDim.x) * kWaves;
+    const int64_t row0 = int64_t(blockIdx.x) * kWaves + wave;
+    const uint32_t one_lo = sgpr_word(kOneLo), one_hi = sgpr_word(kOneHi);
+    uint32_t mx[NCH][4], mn[NCH][4];           // fp16 -Inf / +Inf patterns: replaced by the first row
+#pragma unroll
+    for (int j = 0; j < NCH; ++j)
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            mx[j][k] = 0xFC00FC00u;
+            mn[j][k] = 0x7C007C00u;
+        }
+    bool folded = false, redo = false;         // wavefront-uniform
+    for (int64_t row = row0; row < rows; row += step) {
+        u32x4 xv[NCH];
+        load_row<NCH, false>(x, row, dim, lane, nch_row, xv);
+        float mean, rstd;
+        row_stats<NCH, false>(xv, lane, nch_row, dim, eps, mean, rstd);
+        if (lane == 0) {
+            stats[2 * row] = mean;
+            stats[2 * row + 1] = rstd;
+        }
+        if (__builtin_isfinite(mean) && __builtin_isfinite(rstd) && rstd > 0.0f) {
+            folded = true;
+            const float nmean = -mean;
+#pragma unroll
+            for (int j = 0; j < NCH; ++j) {
+                if (lane + 64 * j < nch_row) {
+                    const uint32_t w[4] = {xv[j].x, xv[j].y, xv[j].z, xv[j].w};
+                    HIF8_DOT_SUB_MUL_EXT(w, one_lo, one_hi, nmean, rstd, mx[j], mn[j]);
+                }
+            }
+        } else {
+            redo = true;
+        }
+    }
+    if (folded) {
+        const uint32_t *lm = lmod + opaque_zero();
+#pragma unroll
+        for (int j = 0; j < NCH; ++j) {
+            if (lane + 64 * j < nch_row) {
+                uint32_t tw[8];
+                float sh[8];
+                load_mod<true>(lm, shift, scale, 0, lane + 64 * j, dim, tw, sh);
+                uint32_t y[4], z[4];
+                uy8(mx[j], tw, sh, one_lo, one_hi, y);
+                uy8(mn[j], tw, sh, one_lo, one_hi, z);
+#pragma unroll
+                for (int k = 0; k < 4; ++k) {
+                    m2 = __builtin_elementwise_max(m2, __builtin_bit_cast(u16x2, y[k] & 0x7FFF7FFFu));
+                    m2 = __builtin_elementwise_max(m2, __builtin_bit_cast(u16x2, z[k] & 0x7FFF7FFFu));
+                }
+            }
+            __builtin_amdgcn_sched_barrier(0);   // one chunk's modulation in registers at a time
+        }
+    }
+    if (redo) {
+        for (int64_t row = row0; row < rows; row += step) {
+            u32x4 xv[NCH];
+            load_row<NCH, false>(x, row, dim, lane, nch_row, xv);
+            float mean, rstd;
+            row_stats<NCH, false>(xv, lane, nch_row, dim, eps, mean, rstd);
+            const uint32_t *lm = lmod + opaque_zero();
+#pragma unroll
+            for (int j = 0; j < NCH; ++j) {
+                if (lane + 64 * j < nch_row) {
+                    uint32_t tw[8];
+                    float sh[8];
+                    load_mod<true>(lm, shift, scale, 0, lane + 64 * j, dim, tw, sh);
+                    uint32_t y[4];
+                    modln8(xv[j], -mean, rstd, tw, sh, one_lo, one_hi, y);
+#pragma unroll
+                    for (int k = 0; k < 4; ++k)
+                        m2 = __builtin_elementwise_max(m2, __builtin_bit_cast(u16x2, y[k] & 0x7FFF7FFFu));
+                }
+            }
+        }
     }
     uint32_t m = m2.x > m2.y ? m2.x : m2.y;
     for (int o = 32; o > 0; o >>= 1) m = max(m, (uint32_t)__shfl_xor((int)m, o, 64));
@@ -590,7 +758,14 @@ static void launch_amax(bool modl, int grid, hipStream_t s, const uint16_t *x, c
                         const uint16_t *scale, int64_t rows, int dim, int64_t rpb, float eps, float *stats,
                         State *st, float smax)
 {
-    if constexpr (NCH * 512 <= 6144) {
+    if constexpr (NCH <= 10) {
+        if (modl) {
+            const int g = grid_for_rows(rows, kExtWgPerCu);
+            hipLaunchKernelGGL((k_modln_amax_ext<NCH>), dim3(g), dim3(kTPB), size_t(8 * dim), s, x, shift, scale,
+                               rows, dim, eps, stats, st, smax);
+            return;
+        }
+    } else if constexpr (NCH * 512 <= 6144) {
         if (modl) {
             hipLaunchKernelGGL((k_modln_amax<NCH, true, FULL, false>), dim3(grid), dim3(kTPB), size_t(8 * dim), s, x,
                                shift, scale, nullptr, nullptr, rows, dim, rpb, eps, stats, st, smax);

@@ -135,6 +135,50 @@ def test_modln_non_finite_rows(pkg, R, bad):
     assert np.array_equal(bits(xq).reshape(-1, 256), want)
 
 
+@pytest.mark.parametrize("D", [5120, 1536, 264])
+@pytest.mark.parametrize("case", ["mixed", "nan_row", "few_rows", "overflow"])
+def test_modln_amax_from_column_extremes(pkg, R, D, case):
+    """With one modulation row, pass 1 takes amax|y| from each column's largest and smallest n
+    (y is monotone in n per column).  The cases: columns with 1 + scale < 0 (y decreasing in
+    n), constant rows (n = 0), a row of huge finite values whose variance overflows (rstd = 0:
+    the row goes through the full chain after the loop), a NaN row among finite ones, fewer
+    rows than wavefronts, and a modulation whose product overflows to Inf.  The state's amax
+    must be the max of |y| over the kernel's own y, bit for bit, and x_q the codec's quant of y."""
+    g = torch.Generator().manual_seed(D + len(case))
+    N = 3 if case == "few_rows" else 301
+    x = torch.randn(1, N, D, generator=g) * 2 + 0.25
+    x[:, :, :3] *= 25
+    e = (torch.randn(1, 6, D, generator=g) * 0.5).chunk(6, dim=1)
+    shift, scale = e[0].clone(), e[1].clone()
+    scale[..., 5:9] = -3.0                                   # t = -2: y decreasing in n
+    if case in ("mixed", "nan_row"):
+        x[0, 7] = 1.5                                        # constant rows
+        x[0, 100] = -0.75
+        x[0, 200] = torch.randn(D, generator=g) * 1e25       # sum of squares overflows fp32
+    if case == "nan_row":
+        x[0, 150, D // 3] = float("nan")
+    if case == "overflow":
+        scale[..., 11] = 1e38                                # n * t overflows for |n| > 3.4
+        x[0, 50, 11] = 40.0                                  # n about 17 there
+    x, shift, scale = (t.to(torch.bfloat16).to(DEV) for t in (x, shift, scale))
+    with torch.no_grad():
+        xq, st, y = pkg.modulated_norm_quant(x, shift, scale, return_y=True)
+    yb = bits(y).reshape(-1, D)
+    amax_bits, _ = st.read()
+    assert amax_bits == R.absmax_bf16(yb)
+    if case == "nan_row":
+        assert (amax_bits & 0x7FFF) > 0x7F80
+    if case == "overflow":
+        # Inf in column 11; the word-neighbour's y is Inf * 0 + shift = NaN in the dot2 form
+        # (only the diagnostic y differs: x_q is NaN everywhere either way, as amax = Inf
+        # gives the reference scale 0 and x_q = 0 / 0)
+        assert (amax_bits & 0x7FFF) >= 0x7F80
+    if case == "mixed":
+        assert np.array_equal(yb[7], bits(shift).reshape(D)) and np.array_equal(yb[100], bits(shift).reshape(D))
+    want, _ = R.quant_bf16(yb, 15.0, "npu")
+    assert np.array_equal(bits(xq).reshape(-1, D), want)
+
+
 def test_qkv_from_modulated_norm_equals_three_forwards(pkg):
     D = 1536
     x, shift, scale = make(21, 1, 257, D)
