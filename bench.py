@@ -50,7 +50,7 @@ def time_linear(pkg, torch, x, packed, b, steps, warmup, route="fused"):
 
     route "fused": the fused dequant-GEMM hif8_linear_fwd on the packed weight codes;
     "decode_once": the GEMM phase is hif8_decode of the weight codes into a bf16 buffer, then the
-    decode-free GEMM hif8_linear_fwd_wq (the HIF8Linear route from DECODE_ONCE_MIN_ROWS rows up);
+    decode-free GEMM hif8_linear_fwd_wq (the HIF8Linear route where hif8_linear.decode_once(M, K));
     its two parts are timed separately as well."""
     st = pkg.QuantState(x.device)
     L = pkg._lib.load()
@@ -892,7 +892,7 @@ def main():
     torch.cuda.synchronize()
     route = args.route
     if route == "auto":   # HIF8Linear's own choice for bf16 activations (hif8_linear.decode_once)
-        route = "decode_once" if M >= pkg.hif8_linear.DECODE_ONCE_MIN_ROWS else "fused"
+        route = "decode_once" if pkg.hif8_linear.decode_once(M, K) else "fused"
     log(f"[bench] timing FFN-up step ({route})")
     r = time_linear(pkg, torch, x, packed, b, args.steps, args.warmup, route)
     step_ms = [a + q + d + g for a, q, d, g in zip(r["amax"], r["quant"], r["wdecode"], r["gemm"])]
@@ -1017,7 +1017,7 @@ def main():
     def linear_line(m_, n_, k_, seed, outliers):
         xs, ws, bs = make_inputs(torch, m_, k_, n_, seed=seed, outlier_channels=outliers)
         ps = pkg.PackedWeight(ws, 15.0)
-        r_ = route if args.route != "auto" else ("decode_once" if pkg.hif8_linear.decode_once(m_) else "fused")
+        r_ = route if args.route != "auto" else ("decode_once" if pkg.hif8_linear.decode_once(m_, k_) else "fused")
         rr = time_linear(pkg, torch, xs, ps, bs, max(3, args.steps // 2), 2, r_)
         gm = sum(rr["gemm"]) / len(rr["gemm"])
         st_ms = rr["wall_ms"] / max(3, args.steps // 2)

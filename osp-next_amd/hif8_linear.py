@@ -268,7 +268,7 @@ def linear_dgrad(grad_q2: Tensor, w: "PackedWeight") -> Tensor:
     if Np != N:
         g = pad_2d(g, M, Np)
     codes_t = w.codes_t() if (Np, Kp) == (N, K) else w.codes_t_padded(Kp, Np)
-    if decode_once(M):
+    if decode_once(M, Np):
         y = linear_fwd_wq_split(g, decode(codes_t, w.state, torch.bfloat16))
     else:
         y = torch.empty((M, Kp), dtype=torch.bfloat16, device=g.device)
@@ -354,15 +354,24 @@ def linear_fwd_wq_split(a: Tensor, w_q: Tensor, bias: Optional[Tensor] = None, s
 # GEMM route for bf16 activations: "fused" decodes the packed weight inside the GEMM (each
 # element once per 256-row tile of x), "decode_once" decodes it into a bf16 buffer per call and
 # runs the decode-free twin (hif8_linear_fwd_wq), "auto" takes decode_once from
-# DECODE_ONCE_MIN_ROWS rows up.  Both issue the same MFMA products in the same order: the same bits.
+# DECODE_ONCE_MIN_ROWS rows up, or from DECODE_ONCE_MIN_ROWS_SHORT_K rows up when the reduction
+# depth K is at most SHORT_K.  Both issue the same MFMA products in the same order: the same bits.
+# Measured fused / decode-once times (decode included) on one box: K = 1536 (the 1.3B q/k/v/o
+# and FFN-up) 0.89-0.98 at 4096-8192 rows and 0.98-1.01 at 16384; K = 5120 or more 1.00-1.04 at
+# 4096-8192 rows; every shape 1.00-1.08 from 32760 rows up.
 GEMM_ROUTE = "auto"
-DECODE_ONCE_MIN_ROWS = 8192   # measured: the routes tie near 8192 rows (14B FFN-up), decode_once wins above
+DECODE_ONCE_MIN_ROWS = 8192
+DECODE_ONCE_MIN_ROWS_SHORT_K = 16384
+SHORT_K = 2048
 
 
-def decode_once(M: int) -> bool:
+def decode_once(M: int, K: int) -> bool:
+    """Whether a GEMM of M rows and reduction depth K takes the decode-once route."""
     if GEMM_ROUTE not in ("auto", "fused", "decode_once"):
         raise ValueError(f"GEMM_ROUTE must be auto, fused or decode_once, not {GEMM_ROUTE!r}")
-    return GEMM_ROUTE == "decode_once" or (GEMM_ROUTE == "auto" and M >= DECODE_ONCE_MIN_ROWS)
+    if GEMM_ROUTE != "auto":
+        return GEMM_ROUTE == "decode_once"
+    return M >= (DECODE_ONCE_MIN_ROWS_SHORT_K if K <= SHORT_K else DECODE_ONCE_MIN_ROWS)
 
 
 def linear_fwd_wq(a: Tensor, w_q: Tensor, bias: Optional[Tensor], y_state: Optional[QuantState] = None,
@@ -462,7 +471,7 @@ def linear_any(a: Tensor, a_fmt: int, a_state: Optional[QuantState], w: PackedWe
 def linear_fwd(a: Tensor, a_fmt: int, a_state: Optional[QuantState], w: PackedWeight,
                bias: Optional[Tensor]) -> Tensor:
     """y[M,N] = x_q[M,K] @ w_q[N,K]^T + bias, bf16 out: hif8_linear_fwd (the fused dequant-GEMM),
-    or from DECODE_ONCE_MIN_ROWS rows up the weight decoded once and hif8_linear_fwd_wq.  An
+    or where decode_once(M, K) the weight decoded once and hif8_linear_fwd_wq.  An
     activation given as codes (``a_fmt`` A_CODES, with its ``a_state``) is decoded to its bf16
     x_q first (bit-exact: decode(encode(x)) is the fake quant of x)."""
     M, K = a.shape
@@ -475,7 +484,7 @@ def linear_fwd(a: Tensor, a_fmt: int, a_state: Optional[QuantState], w: PackedWe
         a = decode(a, a_state, torch.bfloat16)
     elif a_fmt != _lib.A_BF16:
         raise ValueError(f"unknown activation format {a_fmt}")
-    if decode_once(M):
+    if decode_once(M, K):
         return linear_fwd_wq(a, w.dequantize(torch.bfloat16), bias)
     y = torch.empty((M, N), dtype=torch.bfloat16, device=a.device)
     b_ptr = None
@@ -536,7 +545,7 @@ def linear_fwd_grouped(a: Tensor, gw: GroupedWeight) -> "List[Tensor]":
     outs = (ctypes.c_void_p * g)(*[y.data_ptr() for y in ys])
     ns = (ctypes.c_int64 * g)(*gw.ns)
     b_ptr = gw.bias.data_ptr() if gw.bias is not None else None
-    if decode_once(M):
+    if decode_once(M, K):
         w_q = torch.empty((sum(gw.ns), K), dtype=torch.bfloat16, device=a.device)
         row = 0
         for p, n in zip(gw.packs, gw.ns):
@@ -563,7 +572,7 @@ def linear_fwd_gelu_stat(a: Tensor, w: PackedWeight, bias: Optional[Tensor], y_s
         raise ValueError(f"in_features mismatch: x has {K}, weight has {w.shape[1]}")
     if a.dtype != torch.bfloat16:
         raise TypeError("the GELU-statistic epilogue takes bf16 activations")
-    if decode_once(M):
+    if decode_once(M, K):
         return linear_fwd_wq(a, w.dequantize(torch.bfloat16), bias, y_state, scale_max)
     y = torch.empty((M, N), dtype=torch.bfloat16, device=a.device)
     b_ptr = None

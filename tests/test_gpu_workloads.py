@@ -64,7 +64,7 @@ def test_config3_full_size_both_routes(pkg, R, name, N, K):
     x, w, b = _config3_operands(M, K, N, seed=31 + N + K)
     packed = pkg.PackedWeight(w, 15.0)
     a, fmt, st = pkg.quantize_activation(x, 15.0, "bf16")
-    assert pkg.hif8_linear.decode_once(M)          # the default route at this M
+    assert pkg.hif8_linear.decode_once(M, K)       # the default route at this M
     y_auto = pkg.linear_fwd(a, fmt, st, packed, b)
     with _route(pkg, "fused"):
         y_fused = pkg.linear_fwd(a, fmt, st, packed, b)

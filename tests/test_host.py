@@ -160,6 +160,28 @@ def test_status_codes_without_gpu(pkg):
     assert L.hif8_pad_2d(fake, 4, 4, fake, 8, 8, 3, None) == -1
 
 
+def test_gemm_route_rule(pkg):
+    """HIF8Linear's route for bf16 activations: decode-once from 8192 rows, or from 16384 rows
+    when the reduction depth is at most 2048; GEMM_ROUTE forces either route."""
+    hl = pkg.hif8_linear
+    assert hl.GEMM_ROUTE == "auto"
+    assert not hl.decode_once(8191, 5120) and hl.decode_once(8192, 5120)
+    assert not hl.decode_once(16383, 1536) and hl.decode_once(16384, 1536)
+    assert not hl.decode_once(8192, 2048) and hl.decode_once(8192, 2049)
+    assert hl.decode_once(32760, 1536) and hl.decode_once(75600, 13824)
+    old = hl.GEMM_ROUTE
+    try:
+        hl.GEMM_ROUTE = "fused"
+        assert not hl.decode_once(75600, 5120)
+        hl.GEMM_ROUTE = "decode_once"
+        assert hl.decode_once(16, 64)
+        hl.GEMM_ROUTE = "other"
+        with pytest.raises(ValueError):
+            hl.decode_once(16, 64)
+    finally:
+        hl.GEMM_ROUTE = old
+
+
 def test_python_layer_refuses_cpu_tensors(pkg):
     torch = pytest.importorskip("torch")
     x = torch.zeros(16, dtype=torch.bfloat16)
