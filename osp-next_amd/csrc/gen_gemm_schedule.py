@@ -179,8 +179,8 @@ def generate():
 # of k-step j + 2.  Between 16-cycle MFMAs a fragment read right after another delays the MFMA
 # stream by about 12 cycles and two loads two gaps apart by about 30 (lab copies timed with
 # s_memtime: reads in gaps 0..15 and loads every 2-4 gaps, 2606 cycles per k-step; reads every
-# other gap and loads every fourth, 2238): reads go in even gaps 2..32, loads in gaps 1, 5, .. 29.  Every phase first waits for all of its fragments (lgkmcnt(0):
-# they were read at least 31 MFMAs earlier).  At the barrier every wave's reads of k-step j are
+# other gap and loads every fourth, 2238): reads go in even gaps 4..34, loads in gaps 1, 5, .. 29.  Every phase first waits for all of its fragments (lgkmcnt(0):
+# they were read at least 29 MFMAs earlier).  At the barrier every wave's reads of k-step j are
 # complete and so are its loads of k-step j + 1 (vmcnt(8): only the X loads of the even phase
 # before may still be in flight); X and W of k-step j + 2 then go into the stages of X of k-step
 # j and W of k-step j - 1, with three and two phases to land.  The source offsets of an operand
@@ -188,7 +188,7 @@ def generate():
 
 W16_MFMAS = 64
 W16_READ_ORDER = [("w", 0)] + [("x", j) for j in range(8)] + [("w", i) for i in range(1, 8)]
-W16_READ_GAPS = tuple(range(2, 34, 2))   # from gap 2 (was 0), with the 2 x 2 MFMA order: 0.2-0.8 % faster, wgrad 1.6 %
+W16_READ_GAPS = tuple(range(4, 36, 2))   # from gap 4 (was 0), with the 2 x 2 MFMA order: 0.4-1.3 % faster, wgrad 2.5 %
 W16_DTL_GAPS = {0: tuple(range(1, 32, 4)), 1: tuple(range(1, 32, 4))}
 W16_ADV_GAPS = tuple(range(40, 48))
 
