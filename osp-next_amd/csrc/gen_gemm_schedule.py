@@ -46,13 +46,14 @@ DTL_GAPS = {1: tuple(range(1, 48, 4)), 0: ()}
 # the current set's n-tile i (2, 3) from PK_CUR[i] (two gaps apart), the next set's n-tile t (0, 1)
 # from PK_NEXT[t].  With the 2 x 2 MFMA order, X reads from gap 4 (was 2) and lookups 1.5 gaps
 # apart (was 1.25) ran 1.2-1.9 % faster on the 14B shapes, and n-tile 3's packs from gap 0 (was
-# 8) another 2-2.9 % (from gap 4 0.5-1.0 %, then from 0 1.5-1.9 %), and lookups at least 8 gaps
-# after the code reads (was 6) 0.5-0.9 % (A/B of builds on one box, each step twice).
+# 8) another 2-2.9 % (from gap 4 0.5-1.0 %, then from 0 1.5-1.9 %), lookups at least 8 gaps
+# after the code reads (was 6) 0.5-0.9 %, and the next set's packs from gaps 48 and 40 (was 52 and
+# 44) 0.2-0.9 % (A/B of builds on one box, each step at least twice).
 X_START, X_STEP = 4, 3
 LK_START, LK_NUM, LK_DEN = 10, 3, 2
 CODE_GAPS = 8
 PK_CUR = (0, 0, 0, 0)
-PK_NEXT = (52, 44)
+PK_NEXT = (48, 40)
 
 
 class _Op:
