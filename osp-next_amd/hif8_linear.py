@@ -356,12 +356,12 @@ def linear_fwd_wq_split(a: Tensor, w_q: Tensor, bias: Optional[Tensor] = None, s
 # runs the decode-free twin (hif8_linear_fwd_wq), "auto" takes decode_once from
 # DECODE_ONCE_MIN_ROWS rows up, or from DECODE_ONCE_MIN_ROWS_SHORT_K rows up when the reduction
 # depth K is at most SHORT_K.  Both issue the same MFMA products in the same order: the same bits.
-# Measured fused / decode-once times (decode included) on one box: K = 1536 (the 1.3B q/k/v/o
-# and FFN-up) 0.89-0.98 at 4096-8192 rows and 0.98-1.01 at 16384; K = 5120 or more 1.00-1.04 at
-# 4096-8192 rows; every shape 1.00-1.08 from 32760 rows up.
+# Measured fused / decode-once times (decode included; alternating A/B on one box): K = 1536 (the
+# 1.3B q/k/v/o and FFN-up) 0.82-0.98 at 4096-16384 rows, 0.99-1.01 at 32760 (config 2), 1.02-1.03
+# from 49152; K = 5120 or more 0.96-1.01 at 4096-8192 rows, 1.01-1.05 from 16384.
 GEMM_ROUTE = "auto"
 DECODE_ONCE_MIN_ROWS = 8192
-DECODE_ONCE_MIN_ROWS_SHORT_K = 16384
+DECODE_ONCE_MIN_ROWS_SHORT_K = 24576
 SHORT_K = 2048
 
 

@@ -161,12 +161,12 @@ def test_status_codes_without_gpu(pkg):
 
 
 def test_gemm_route_rule(pkg):
-    """HIF8Linear's route for bf16 activations: decode-once from 8192 rows, or from 16384 rows
+    """HIF8Linear's route for bf16 activations: decode-once from 8192 rows, or from 24576 rows
     when the reduction depth is at most 2048; GEMM_ROUTE forces either route."""
     hl = pkg.hif8_linear
     assert hl.GEMM_ROUTE == "auto"
     assert not hl.decode_once(8191, 5120) and hl.decode_once(8192, 5120)
-    assert not hl.decode_once(16383, 1536) and hl.decode_once(16384, 1536)
+    assert not hl.decode_once(24575, 1536) and hl.decode_once(24576, 1536)
     assert not hl.decode_once(8192, 2048) and hl.decode_once(8192, 2049)
     assert hl.decode_once(32760, 1536) and hl.decode_once(75600, 13824)
     old = hl.GEMM_ROUTE
